@@ -1,0 +1,199 @@
+#!/usr/bin/env python3
+"""Headline benchmark of the MI355X butterfly path (one GPU).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--operators]
+
+A step is one call of the hot path over one batch of the named BASELINE
+configuration, with inputs already resident in HBM. W untimed steps, then K
+timed steps bracketed by torch.cuda.synchronize(); the timed calls rotate over
+enough input/output buffer sets (> 256 MiB in total) that the 256 MB Infinity
+Cache cannot serve them. Rank 0 prints ONE JSON line with the driver's fields
+plus `roofline` (algorithmic bytes per call / measured call time vs 8 TB/s HBM)
+and `cpu_baseline` (the CPU oracle -- a restatement of the reference CPU path --
+timed on this host over a bounded sample of the same workload).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "transforms/s + achieved HBM GB/s (% of peak) per operator, 1x MI355X"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def _np_to_torch(torch, a):
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    elif a.dtype == np.uint64:
+        a = a.view(np.int64)
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+class Workload:
+    """One BASELINE configuration: plans, resident buffers, a call, its bytes."""
+
+    name = ""
+    dtype = ""
+    description = ""
+    transforms_per_call = 0
+    bytes_per_call = 0  # algorithmic: compulsory input read + output write
+
+    def setup(self, torch, lib, stream):
+        raise NotImplementedError
+
+    def call(self, index):
+        raise NotImplementedError
+
+    def cpu_sample(self, threads):
+        """Returns (seconds, transforms, description) for a bounded CPU run."""
+        raise NotImplementedError
+
+    def config(self):
+        return {"workload": self.description}
+
+    def kernel_name(self):
+        return self.plans[0].algorithm_name()
+
+    def _rotation(self, torch, bytes_per_set):
+        return max(3, -(-2 * MALL_BYTES // max(1, bytes_per_set)))
+
+
+class FwhtFp32(Workload):
+    name = "c1"
+    dtype = "f32"
+    description = "FWHT fp32 unnormalized forward, batch 4096 x n=4096, integer inputs in [-8,8]"
+
+    def __init__(self, log_n=12, batch=4096):
+        self.log_n, self.batch = log_n, batch
+        self.transforms_per_call = batch
+        self.bytes_per_call = 2 * batch * (4 << log_n)
+
+    def setup(self, torch, lib, stream):
+        import cubutterfly_amd as cb
+        from cubutterfly_amd import workloads
+        t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
+                         extents=[1 << self.log_n], batch=self.batch)
+        self.plans = [cb.Plan(lib, t, stream=stream)]
+        host = workloads.fwht_integer_input(self.log_n, self.batch, seed=1)
+        self.host = host
+        sets = self._rotation(torch, self.bytes_per_call)
+        src = _np_to_torch(torch, host).to("cuda")
+        self.inputs = [src.clone() for _ in range(sets)]
+        self.outputs = [torch.empty_like(src) for _ in range(sets)]
+
+    def call(self, index):
+        k = index % len(self.inputs)
+        self.plans[0].execute(self.inputs[k], self.outputs[k])
+
+    def verify(self, torch):
+        import oracle
+        got = self.outputs[0].cpu().numpy()
+        return bool(np.array_equal(got, oracle.fwht_f32(self.host, threads=oracle.default_threads())))
+
+    def cpu_sample(self, threads):
+        import oracle
+        reps, elapsed = 0, 0.0
+        while elapsed < 10.0:
+            t0 = time.perf_counter()
+            oracle.fwht_f32(self.host, threads=threads)
+            elapsed += time.perf_counter() - t0
+            reps += 1
+        return elapsed, reps * self.batch, f"{reps} full C1 batches (4096 x 4096) through reference_fwht"
+
+
+WORKLOADS = {"c1": FwhtFp32}
+DEFAULT_WORKLOAD = "c1"
+
+
+def time_calls(torch, workload, steps, warmup):
+    for i in range(warmup):
+        workload.call(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        workload.call(warmup + i)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per call
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--verify", action="store_true", help="check one output against the oracle")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the butterfly path is single-GPU (every configuration "
+              "shards by rows/limbs with no communication); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import cubutterfly_amd as cb
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    lib = cb.Library()
+    stream = torch.cuda.current_stream().cuda_stream
+    workload = WORKLOADS[args.workload]()
+    workload.setup(torch, lib, stream)
+    torch.cuda.synchronize()
+
+    ms = time_calls(torch, workload, args.steps, args.warmup)
+    transforms_per_s = workload.transforms_per_call / (ms * 1e-3)
+    achieved = workload.bytes_per_call / (ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": transforms_per_s,
+        "unit": "transforms/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": workload.dtype,
+        "data": "synthetic (seeded splitmix64 / mt19937_64 generators)",
+        "config": workload.config(),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": workload.kernel_name(),
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_call": workload.bytes_per_call,
+        },
+    }
+    if args.verify:
+        result["verified"] = workload.verify(torch)
+    if not args.no_cpu:
+        import oracle
+        threads = oracle.default_threads()
+        seconds, transforms, sample = workload.cpu_sample(threads)
+        result["cpu_baseline"] = {
+            "value": transforms / seconds,
+            "unit": "transforms/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": sample + f"; {seconds:.1f} s on {threads} host threads",
+        }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,276 @@
+// FWHT kernels for gfx950: FP32 storage, and FP16 storage with FP32 compute
+// and one final RNE narrowing (the reference's final-storage contract,
+// src/butterfly.cu:1452-1470, 1882-1897).
+//
+// Bit exactness. Each output is a fixed binary tree of fp32 additions, and the
+// tree depends on the ORDER in which index bits are butterflied. The reference
+// CPU oracle and its stage-ordered GPU kernels process bits 0, 1, ..., log n - 1
+// (src/butterfly_reference.cpp:349-369, src/stage_pipeline.cuh:573-680), so
+// these kernels do the same: phase p butterflies bits [4p, 4p+4) entirely in
+// registers, and between phases the block regroups its data through LDS so the
+// next four bits become register bits. Same butterflies, same order, same
+// roundings -- independent of how bits are mapped to lanes and waves.
+//
+// Layout in one workgroup: the block owns 2^LB consecutive elements (whole
+// rows; 2^(LB - log n) rows when n is small). In phase p, thread t register r
+// holds element  lo(t) | r << 4p | hi(t) << (4p + 4), lo/hi being t's bits
+// below/above 4p. Phase 0 is "16 consecutive elements per thread", so loads
+// (and the FP16 stores) are 16-byte vector accesses. The LDS image is padded
+// with one word per 16 (addr = i + i/16), which makes the phase-0 row writes
+// and the strided phase-1 reads conflict-free across a wave's 64 lanes.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "json.hpp"
+#include "planner.hpp"
+
+#include <utility>
+
+namespace cbw {
+namespace {
+
+constexpr int kLE = 4;  // log2 registers per thread per phase (radix-16 phases)
+constexpr int kE = 1 << kLE;
+
+// Phase P's register window starts at bit 4P, clamped so it ends inside the
+// block (when LB is not a multiple of 4 the last window overlaps the previous
+// one; only its new bits are butterflied).
+template <int P, int LB>
+constexpr int window_start() {
+    return P * kLE < LB - kLE ? P * kLE : LB - kLE;
+}
+
+template <int P, int LB>
+__device__ __forceinline__ unsigned phase_index(unsigned t, unsigned r) {
+    constexpr unsigned lo_bits = window_start<P, LB>();
+    const unsigned lo = t & ((1u << lo_bits) - 1u);
+    const unsigned hi = t >> lo_bits;
+    return lo | (r << lo_bits) | (hi << (lo_bits + kLE));
+}
+
+__device__ __forceinline__ unsigned lds_addr(unsigned i) { return i + (i >> kLE); }
+
+template <int P, int LOG_N, int LB>
+__device__ __forceinline__ void register_stages(float (&v)[kE]) {
+    constexpr int s = window_start<P, LB>();
+#pragma unroll
+    for (int j = 0; j < kLE; ++j) {
+        if (s + j >= P * kLE && s + j < LOG_N) {
+            const int d = 1 << j;
+#pragma unroll
+            for (int r = 0; r < kE; ++r) {
+                if ((r & d) == 0) {
+                    const float a = v[r];
+                    const float b = v[r + d];
+                    v[r] = a + b;
+                    v[r + d] = a - b;
+                }
+            }
+        }
+    }
+}
+
+template <int FROM, int TO, int LB>
+__device__ __forceinline__ void exchange(float (&v)[kE], float* lds, unsigned t) {
+    if (FROM > 0) __syncthreads();  // earlier readers of the LDS image are done
+#pragma unroll
+    for (int r = 0; r < kE; ++r) lds[lds_addr(phase_index<FROM, LB>(t, r))] = v[r];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kE; ++r) v[r] = lds[lds_addr(phase_index<TO, LB>(t, r))];
+}
+
+// ---- storage adapters ----------------------------------------------------
+
+struct F32Io {
+    using T = float;
+    // Full path: 16 consecutive floats = four 16-byte loads.
+    static __device__ __forceinline__ void load16(const float* p, float (&v)[kE]) {
+        const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 x = q[k];
+            v[4 * k + 0] = x.x;
+            v[4 * k + 1] = x.y;
+            v[4 * k + 2] = x.z;
+            v[4 * k + 3] = x.w;
+        }
+    }
+    static __device__ __forceinline__ void store16(float* p, const float (&v)[kE]) {
+        float4* q = reinterpret_cast<float4*>(p);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+    }
+    static __device__ __forceinline__ float load1(const float* p) { return *p; }
+    static __device__ __forceinline__ void store1(float* p, float x) { *p = x; }
+};
+
+struct F16Io {
+    using T = __half;
+    static __device__ __forceinline__ void load16(const __half* p, float (&v)[kE]) {
+        const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint4 x = q[k];
+            const unsigned w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[8 * k + 2 * j + 0] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[j] & 0xffffu)));
+                v[8 * k + 2 * j + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[j] >> 16)));
+            }
+        }
+    }
+    static __device__ __forceinline__ void store16(__half* p, const float (&v)[kE]) {
+        uint4* q = reinterpret_cast<uint4*>(p);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            unsigned w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const unsigned lo = __half_as_ushort(__float2half_rn(v[8 * k + 2 * j + 0]));
+                const unsigned hi = __half_as_ushort(__float2half_rn(v[8 * k + 2 * j + 1]));
+                w[j] = lo | (hi << 16);
+            }
+            q[k] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+    static __device__ __forceinline__ float load1(const __half* p) { return __half2float(*p); }
+    static __device__ __forceinline__ void store1(__half* p, float x) { *p = __float2half_rn(x); }
+};
+
+// One workgroup transforms 2^LB consecutive elements (2^(LB-LOG_N) rows).
+// `norm` is 1 or 1/n (normalised inverse), `scale` the FP16 output scale; the
+// two products are applied in this order, as the reference's finalize and
+// narrowing kernel do. Multiplying by 1.0f is exact, so unused factors are 1.
+template <int LOG_N, int LB, class Io>
+__global__ __launch_bounds__(1 << (LB - kLE)) void fwht_resident_kernel(const typename Io::T* __restrict__ input,
+                                                                        typename Io::T* output,
+                                                                        std::uint64_t total, float norm,
+                                                                        float scale) {
+    constexpr int kPhases = (LOG_N + kLE - 1) / kLE;
+    constexpr unsigned kBlock = 1u << LB;
+    __shared__ float lds[kBlock + (kBlock >> kLE)];
+    const unsigned t = threadIdx.x;
+    const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kBlock;
+    const bool full = base + kBlock <= total;
+
+    float v[kE];
+    if (full) {
+        Io::load16(input + base + t * kE, v);
+    } else {
+#pragma unroll
+        for (int r = 0; r < kE; ++r) {
+            const std::uint64_t i = base + t * kE + r;
+            v[r] = i < total ? Io::load1(input + i) : 0.0f;
+        }
+    }
+    register_stages<0, LOG_N, LB>(v);
+    if constexpr (kPhases > 1) {
+        exchange<0, 1, LB>(v, lds, t);
+        register_stages<1, LOG_N, LB>(v);
+    }
+    if constexpr (kPhases > 2) {
+        exchange<1, 2, LB>(v, lds, t);
+        register_stages<2, LOG_N, LB>(v);
+    }
+    if constexpr (kPhases > 3) {
+        exchange<2, 3, LB>(v, lds, t);
+        register_stages<3, LOG_N, LB>(v);
+    }
+#pragma unroll
+    for (int r = 0; r < kE; ++r) v[r] = (v[r] * norm) * scale;
+    // Regroup to "16 consecutive per thread" for 16-byte stores.
+    if constexpr (kPhases > 1) exchange<kPhases - 1, 0, LB>(v, lds, t);
+    if (full) {
+        Io::store16(output + base + t * kE, v);
+    } else {
+#pragma unroll
+        for (int r = 0; r < kE; ++r) {
+            const std::uint64_t i = base + t * kE + r;
+            if (i < total) Io::store1(output + i, v[r]);
+        }
+    }
+}
+
+using Launch = void (*)(const void*, void*, std::uint64_t, float, float, hipStream_t);
+
+template <int LOG_N, class Io>
+constexpr int block_log() {
+    return LOG_N <= 12 ? 12 : LOG_N;
+}
+
+template <int LOG_N, class Io>
+void launch_resident(const void* in, void* out, std::uint64_t total, float norm, float scale, hipStream_t stream) {
+    constexpr int LB = block_log<LOG_N, Io>();
+    const std::uint64_t blocks = (total + (1ull << LB) - 1) >> LB;
+    hipLaunchKernelGGL((fwht_resident_kernel<LOG_N, LB, Io>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(1u << (LB - kLE)), 0, stream, static_cast<const typename Io::T*>(in),
+                       static_cast<typename Io::T*>(out), total, norm, scale);
+}
+
+template <class Io, int... L>
+Launch resident_table_entry(int log_n, std::integer_sequence<int, L...>) {
+    Launch table[] = {nullptr, launch_resident<L + 1, Io>...};
+    return table[log_n];
+}
+
+constexpr int kMaxResidentLog = 13;
+
+template <class Io>
+Launch resident_launcher(int log_n) {
+    if (log_n < 1 || log_n > kMaxResidentLog) return nullptr;
+    return resident_table_entry<Io>(log_n, std::make_integer_sequence<int, kMaxResidentLog>{});
+}
+
+class FwhtExecutor final : public Executor {
+  public:
+    FwhtExecutor(const Request& r, Launch launch) : r_(r), launch_(launch) {
+        norm_ = r.normalize ? 1.0f / static_cast<float>(r.n) : 1.0f;
+        scale_ = r.fp16_final ? r.output_scale : 1.0f;
+        const int lb = r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
+        const std::uint64_t total = r.n * r.batch;
+        blocks_ = (total + (1ull << lb) - 1) >> lb;
+        require(blocks_ <= 0x7fffffffull, "FWHT batch exceeds the launch grid");
+        algorithm = r.fp16_final ? "fwht-fp16-fp32-resident-r16" : "fwht-fp32-resident-r16";
+        reason = "whole rows resident in one workgroup (" + std::to_string(1u << (lb - kLE)) +
+                 " threads x 16 registers, padded LDS exchange); stage order bits 0..log n-1";
+        json::Writer w;
+        w.begin_object()
+            .field("schema_version", 1u)
+            .field("operator", "fwht")
+            .field("algorithm", algorithm)
+            .field("log_n", r.log_n)
+            .field("batch", r.batch)
+            .field("block_elements", std::uint64_t{1} << lb)
+            .field("threads_per_block", 1u << (lb - kLE))
+            .field("registers_per_thread", unsigned(kE))
+            .field("phases", unsigned((r.log_n + kLE - 1) / kLE))
+            .field("grid", blocks_)
+            .field("lds_bytes", std::uint64_t(((1u << lb) + ((1u << lb) >> kLE)) * 4))
+            .end_object();
+        mapping_json = w.str();
+    }
+    void execute(const void* in, void* out, void*, hipStream_t stream) override {
+        launch_(in, out, r_.n * r_.batch, norm_, scale_, stream);
+        hip_check(hipGetLastError(), "FWHT launch");
+    }
+
+  private:
+    Request r_;
+    Launch launch_;
+    float norm_ = 1.0f, scale_ = 1.0f;
+    std::uint64_t blocks_ = 0;
+};
+
+}  // namespace
+
+std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
+    supported(r.log_n <= kMaxResidentLog,
+              "FWHT lengths above 2^" + std::to_string(kMaxResidentLog) + " are not yet lowered for gfx950");
+    supported(!r.allow_mma || r.fp16_final, "MFMA Hadamard blocks require FP16 storage");
+    const Launch launch = r.fp16_final ? resident_launcher<F16Io>(r.log_n) : resident_launcher<F32Io>(r.log_n);
+    require(launch != nullptr, "FWHT length has no launcher");
+    return std::make_unique<FwhtExecutor>(r, launch);
+}
+
+}  // namespace cbw

@@ -1,0 +1,25 @@
+// gfx950 planner: lowers a validated rank-1 request to one executor.
+// Each kernel family exposes a factory; the factory chooses the radix, the
+// stage split between passes and the register/LDS residency for CDNA4
+// (64-wide wavefronts, 160 KB LDS per CU, 256 CUs in 8 XCDs).
+#pragma once
+
+#include "common.hpp"
+#include "descriptor.hpp"
+
+namespace cbw {
+
+std::unique_ptr<Executor> make_fwht_executor(const Request& r);
+std::unique_ptr<Executor> make_fft_executor(const Request& r);
+std::unique_ptr<Executor> make_ntt_executor(const Request& r);
+
+inline std::unique_ptr<Executor> plan_executor(const Request& r) {
+    switch (r.op) {
+        case Op::Fwht: return make_fwht_executor(r);
+        case Op::Fft: return make_fft_executor(r);
+        case Op::Ntt: return make_ntt_executor(r);
+    }
+    throw NotSupported("operator has no MI355X lowering");
+}
+
+}  // namespace cbw
