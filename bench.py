@@ -108,22 +108,111 @@ class FwhtFp32(Workload):
         return elapsed, reps * self.batch, f"{reps} full C1 batches (4096 x 4096) through reference_fwht"
 
 
-WORKLOADS = {"c1": FwhtFp32}
-DEFAULT_WORKLOAD = "c1"
+class NttNegacyclic(Workload):
+    """C2: forward then inverse negacyclic NTT, u32, q = 1073479681, n = 2^16, batch 64."""
+    name = "c2"
+    dtype = "u32"
+    description = ("single-prime negacyclic NTT u32, n=2^16, batch 64, q=1073479681 (30-bit, q = 1 mod 2n); "
+                   "one step = forward then inverse of the batch")
+
+    def __init__(self, log_n=16, batch=64):
+        from cubutterfly_amd import workloads
+        self.log_n, self.batch, self.q = log_n, batch, workloads.C2_MODULUS
+        self.transforms_per_call = 2 * batch  # forward + inverse transforms
+        self.bytes_per_call = 2 * 2 * batch * (4 << log_n)
+
+    def setup(self, torch, lib, stream):
+        import cubutterfly_amd as cb
+        from cubutterfly_amd import workloads
+
+        def plan(inverse):
+            t = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
+                             extents=[1 << self.log_n], batch=self.batch, modulus=self.q, word_bits=32,
+                             inverse=inverse, ring=cb.NttRing.NEGACYCLIC)
+            return cb.Plan(lib, t, stream=stream)
+
+        self.plans = [plan(False), plan(True)]
+        ws_bytes = max(p.workspace_size() for p in self.plans)
+        self.workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
+        for p in self.plans:
+            if p.workspace_size():
+                p.set_workspace(self.workspace, ws_bytes)
+        self.host = workloads.ntt_input(self.log_n, self.batch, self.q, seed=1).astype(np.uint32)
+        src = _np_to_torch(torch, self.host).to("cuda")
+        sets = self._rotation(torch, 3 * src.numel() * 4)
+        self.inputs = [src.clone() for _ in range(sets)]
+        self.spectra = [torch.empty_like(src) for _ in range(sets)]
+        self.outputs = [torch.empty_like(src) for _ in range(sets)]
+
+    def call(self, index):
+        k = index % len(self.inputs)
+        self.plans[0].execute(self.inputs[k], self.spectra[k])
+        self.plans[1].execute(self.spectra[k], self.outputs[k])
+
+    def verify(self, torch):
+        import oracle
+        spectrum = self.spectra[0].cpu().numpy().view(np.uint32).astype(np.uint64)
+        back = self.outputs[0].cpu().numpy().view(np.uint32)
+        expected = oracle.ntt_negacyclic(self.host.astype(np.uint64), self.q, threads=oracle.default_threads())
+        return bool(np.array_equal(spectrum, expected) and np.array_equal(back, self.host))
+
+    def kernel_name(self):
+        return self.plans[0].algorithm_name() + " (forward) + inverse"
+
+    def cpu_sample(self, threads):
+        import oracle
+        x = self.host.astype(np.uint64)
+        reps, elapsed = 0, 0.0
+        while elapsed < 10.0:
+            t0 = time.perf_counter()
+            y = oracle.ntt_negacyclic(x, self.q, threads=threads)
+            oracle.ntt_negacyclic(y, self.q, inverse=True, threads=threads)
+            elapsed += time.perf_counter() - t0
+            reps += 1
+        return elapsed, reps * 2 * self.batch, (f"{reps} full C2 steps (64 x 2^16 forward + inverse) through the "
+                                                "crypto-benchmark composition: psi twist + reference_ntt DIT")
 
 
-def time_calls(torch, workload, steps, warmup):
-    for i in range(warmup):
-        workload.call(i)
+WORKLOADS = {"c1": FwhtFp32, "c2": NttNegacyclic}
+DEFAULT_WORKLOAD = "c2"
+
+
+CALLS_PER_GRAPH = 20
+
+
+def time_calls(torch, workload, stream, steps, warmup, use_graph=True):
+    """Milliseconds per call. W eager warmup calls; then, as the reference
+    times it (a graph of 20 calls replayed, docs/fwht_native_repair_20261107.md:20),
+    the K timed calls run as replays of a captured HIP graph of 20 calls so
+    host submission is not measured. Events are recorded on the plans' stream."""
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            workload.call(i)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        workload.call(warmup + i)
-    stop.record()
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(CALLS_PER_GRAPH):
+                workload.call(i)
+        torch.cuda.synchronize()
+        replays = max(1, -(-steps // CALLS_PER_GRAPH))
+        graph.replay()  # first replay uploads the graph
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / (replays * CALLS_PER_GRAPH), replays * CALLS_PER_GRAPH
+    start.record(stream)
+    with torch.cuda.stream(stream):
+        for i in range(steps):
+            workload.call(warmup + i)
+    stop.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps  # ms per call
+    return start.elapsed_time(stop) / steps, steps
 
 
 def main():
@@ -134,6 +223,7 @@ def main():
     parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--verify", action="store_true", help="check one output against the oracle")
+    parser.add_argument("--eager", action="store_true", help="time eager submissions instead of graph replays")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the butterfly path is single-GPU (every configuration "
@@ -146,12 +236,12 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
     lib = cb.Library()
-    stream = torch.cuda.current_stream().cuda_stream
+    stream = torch.cuda.Stream()  # default priority; plans launch on it
     workload = WORKLOADS[args.workload]()
-    workload.setup(torch, lib, stream)
+    workload.setup(torch, lib, stream.cuda_stream)
     torch.cuda.synchronize()
 
-    ms = time_calls(torch, workload, args.steps, args.warmup)
+    ms, timed = time_calls(torch, workload, stream, args.steps, args.warmup, use_graph=not args.eager)
     transforms_per_s = workload.transforms_per_call / (ms * 1e-3)
     achieved = workload.bytes_per_call / (ms * 1e-3) / 1e9
     result = {
@@ -159,7 +249,7 @@ def main():
         "value": transforms_per_s,
         "unit": "transforms/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": timed,
         "warmup": args.warmup,
         "ms_per_step": ms,
         "higher_is_better": True,
@@ -178,6 +268,7 @@ def main():
             "traffic": None,
             "algorithmic_bytes_per_call": workload.bytes_per_call,
         },
+        "timing": "hip graph of %d calls, replayed" % CALLS_PER_GRAPH if not args.eager else "eager calls",
     }
     if args.verify:
         result["verified"] = workload.verify(torch)

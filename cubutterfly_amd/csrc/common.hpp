@@ -95,6 +95,10 @@ class Executor {
     std::string mapping_json;  // full execution mapping
 };
 
+// Compute units of the current device (256 on MI355X); falls back to 256 when
+// no device is visible so plans can still be described on a CPU-only host.
+int device_cu_count();
+
 // ---- plan-time modular arithmetic (host only) ----------------------------
 using u128 = unsigned __int128;
 inline std::uint64_t mulmod(std::uint64_t a, std::uint64_t b, std::uint64_t q) {

@@ -24,6 +24,7 @@
 #include "json.hpp"
 #include "planner.hpp"
 
+#include <algorithm>
 #include <utility>
 
 namespace cbw {
@@ -70,12 +71,17 @@ __device__ __forceinline__ void register_stages(float (&v)[kE]) {
     }
 }
 
+// Workgroup barrier for LDS traffic only: each wave drains its own LDS
+// operations, then meets the others. Unlike __syncthreads() it does not wait
+// for outstanding global loads, so the next tile's prefetch stays in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int FROM, int TO, int LB>
 __device__ __forceinline__ void exchange(float (&v)[kE], float* lds, unsigned t) {
-    if (FROM > 0) __syncthreads();  // earlier readers of the LDS image are done
+    lds_barrier();  // earlier readers of the LDS image (this or the previous tile) are done
 #pragma unroll
     for (int r = 0; r < kE; ++r) lds[lds_addr(phase_index<FROM, LB>(t, r))] = v[r];
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int r = 0; r < kE; ++r) v[r] = lds[lds_addr(phase_index<TO, LB>(t, r))];
 }
@@ -138,24 +144,17 @@ struct F16Io {
     static __device__ __forceinline__ void store1(__half* p, float x) { *p = __float2half_rn(x); }
 };
 
-// One workgroup transforms 2^LB consecutive elements (2^(LB-LOG_N) rows).
+// A workgroup owns tiles of 2^LB consecutive elements (2^(LB-LOG_N) whole
+// rows) and walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...; the next
+// tile's global loads are issued before the current tile is processed, so
+// HBM reads overlap the register/LDS phases.
 // `norm` is 1 or 1/n (normalised inverse), `scale` the FP16 output scale; the
 // two products are applied in this order, as the reference's finalize and
 // narrowing kernel do. Multiplying by 1.0f is exact, so unused factors are 1.
-template <int LOG_N, int LB, class Io>
-__global__ __launch_bounds__(1 << (LB - kLE)) void fwht_resident_kernel(const typename Io::T* __restrict__ input,
-                                                                        typename Io::T* output,
-                                                                        std::uint64_t total, float norm,
-                                                                        float scale) {
-    constexpr int kPhases = (LOG_N + kLE - 1) / kLE;
-    constexpr unsigned kBlock = 1u << LB;
-    __shared__ float lds[kBlock + (kBlock >> kLE)];
-    const unsigned t = threadIdx.x;
-    const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kBlock;
-    const bool full = base + kBlock <= total;
-
-    float v[kE];
-    if (full) {
+template <int LB, class Io>
+__device__ __forceinline__ void load_tile(const typename Io::T* __restrict__ input, std::uint64_t base,
+                                          std::uint64_t total, unsigned t, float (&v)[kE]) {
+    if (base + (1ull << LB) <= total) {
         Io::load16(input + base + t * kE, v);
     } else {
 #pragma unroll
@@ -164,35 +163,74 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_resident_kernel(const ty
             v[r] = i < total ? Io::load1(input + i) : 0.0f;
         }
     }
-    register_stages<0, LOG_N, LB>(v);
-    if constexpr (kPhases > 1) {
-        exchange<0, 1, LB>(v, lds, t);
-        register_stages<1, LOG_N, LB>(v);
-    }
-    if constexpr (kPhases > 2) {
-        exchange<1, 2, LB>(v, lds, t);
-        register_stages<2, LOG_N, LB>(v);
-    }
-    if constexpr (kPhases > 3) {
-        exchange<2, 3, LB>(v, lds, t);
-        register_stages<3, LOG_N, LB>(v);
-    }
-#pragma unroll
-    for (int r = 0; r < kE; ++r) v[r] = (v[r] * norm) * scale;
-    // Regroup to "16 consecutive per thread" for 16-byte stores.
-    if constexpr (kPhases > 1) exchange<kPhases - 1, 0, LB>(v, lds, t);
-    if (full) {
-        Io::store16(output + base + t * kE, v);
-    } else {
-#pragma unroll
-        for (int r = 0; r < kE; ++r) {
-            const std::uint64_t i = base + t * kE + r;
-            if (i < total) Io::store1(output + i, v[r]);
+}
+
+template <int LOG_N, int LB, class Io>
+__global__ __launch_bounds__(1 << (LB - kLE)) void fwht_resident_kernel(const typename Io::T* __restrict__ input,
+                                                                        typename Io::T* output,
+                                                                        std::uint64_t total, float norm,
+                                                                        float scale, unsigned tiles) {
+    constexpr int kPhases = (LOG_N + kLE - 1) / kLE;
+    constexpr int kLast = kPhases - 1;
+    // Store straight from the last phase when its lanes cover >= 64
+    // consecutive elements; otherwise regroup to 16-per-thread vectors.
+    constexpr bool kDirectStore = kPhases > 1 && window_start<kLast, LB>() >= 6;
+    constexpr unsigned kBlock = 1u << LB;
+    __shared__ float lds[kBlock + (kBlock >> kLE)];
+    const unsigned t = threadIdx.x;
+    unsigned tile = blockIdx.x;
+    if (tile >= tiles) return;
+
+    float v[kE], next[kE];
+    load_tile<LB, Io>(input, std::uint64_t(tile) * kBlock, total, t, v);
+    for (;;) {
+        const std::uint64_t base = std::uint64_t(tile) * kBlock;
+        const unsigned following = tile + gridDim.x;
+        const bool more = following < tiles;
+        if (more) load_tile<LB, Io>(input, std::uint64_t(following) * kBlock, total, t, next);
+
+        register_stages<0, LOG_N, LB>(v);
+        if constexpr (kPhases > 1) {
+            exchange<0, 1, LB>(v, lds, t);
+            register_stages<1, LOG_N, LB>(v);
         }
+        if constexpr (kPhases > 2) {
+            exchange<1, 2, LB>(v, lds, t);
+            register_stages<2, LOG_N, LB>(v);
+        }
+        if constexpr (kPhases > 3) {
+            exchange<2, 3, LB>(v, lds, t);
+            register_stages<3, LOG_N, LB>(v);
+        }
+#pragma unroll
+        for (int r = 0; r < kE; ++r) v[r] = (v[r] * norm) * scale;
+        const bool full = base + kBlock <= total;
+        if constexpr (kDirectStore) {
+#pragma unroll
+            for (int r = 0; r < kE; ++r) {
+                const std::uint64_t i = base + phase_index<kLast, LB>(t, r);
+                if (full || i < total) Io::store1(output + i, v[r]);
+            }
+        } else {
+            if constexpr (kPhases > 1) exchange<kLast, 0, LB>(v, lds, t);
+            if (full) {
+                Io::store16(output + base + t * kE, v);
+            } else {
+#pragma unroll
+                for (int r = 0; r < kE; ++r) {
+                    const std::uint64_t i = base + t * kE + r;
+                    if (i < total) Io::store1(output + i, v[r]);
+                }
+            }
+        }
+        if (!more) break;
+        tile = following;
+#pragma unroll
+        for (int r = 0; r < kE; ++r) v[r] = next[r];
     }
 }
 
-using Launch = void (*)(const void*, void*, std::uint64_t, float, float, hipStream_t);
+using Launch = void (*)(const void*, void*, std::uint64_t, float, float, unsigned, hipStream_t);
 
 template <int LOG_N, class Io>
 constexpr int block_log() {
@@ -200,12 +238,13 @@ constexpr int block_log() {
 }
 
 template <int LOG_N, class Io>
-void launch_resident(const void* in, void* out, std::uint64_t total, float norm, float scale, hipStream_t stream) {
+void launch_resident(const void* in, void* out, std::uint64_t total, float norm, float scale, unsigned grid,
+                     hipStream_t stream) {
     constexpr int LB = block_log<LOG_N, Io>();
-    const std::uint64_t blocks = (total + (1ull << LB) - 1) >> LB;
-    hipLaunchKernelGGL((fwht_resident_kernel<LOG_N, LB, Io>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(1u << (LB - kLE)), 0, stream, static_cast<const typename Io::T*>(in),
-                       static_cast<typename Io::T*>(out), total, norm, scale);
+    const std::uint64_t tiles = (total + (1ull << LB) - 1) >> LB;
+    hipLaunchKernelGGL((fwht_resident_kernel<LOG_N, LB, Io>), dim3(grid), dim3(1u << (LB - kLE)), 0, stream,
+                       static_cast<const typename Io::T*>(in), static_cast<typename Io::T*>(out), total, norm,
+                       scale, static_cast<unsigned>(tiles));
 }
 
 template <class Io, int... L>
@@ -229,11 +268,20 @@ class FwhtExecutor final : public Executor {
         scale_ = r.fp16_final ? r.output_scale : 1.0f;
         const int lb = r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
         const std::uint64_t total = r.n * r.batch;
-        blocks_ = (total + (1ull << lb) - 1) >> lb;
-        require(blocks_ <= 0x7fffffffull, "FWHT batch exceeds the launch grid");
+        const std::uint64_t tiles = (total + (1ull << lb) - 1) >> lb;
+        require(tiles <= 0xffffffffull, "FWHT batch exceeds the tile index range");
+        // Persistent grid: as many resident workgroups as LDS and the 32-wave
+        // CU limit allow, never more than there are tiles.
+        const unsigned threads = 1u << (lb - kLE);
+        const std::uint64_t lds = ((1u << lb) + ((1u << lb) >> kLE)) * 4ull;
+        const unsigned by_waves = 32u / (threads / 64u);
+        const unsigned by_lds = static_cast<unsigned>((160ull * 1024) / lds);
+        const std::uint64_t resident = std::uint64_t(device_cu_count()) * std::min(by_waves, by_lds);
+        grid_ = static_cast<unsigned>(std::min<std::uint64_t>(tiles, resident));
         algorithm = r.fp16_final ? "fwht-fp16-fp32-resident-r16" : "fwht-fp32-resident-r16";
-        reason = "whole rows resident in one workgroup (" + std::to_string(1u << (lb - kLE)) +
-                 " threads x 16 registers, padded LDS exchange); stage order bits 0..log n-1";
+        reason = "whole rows resident in one workgroup (" + std::to_string(threads) +
+                 " threads x 16 registers, padded LDS exchange), persistent grid with next-tile prefetch; "
+                 "stage order bits 0..log n-1";
         json::Writer w;
         w.begin_object()
             .field("schema_version", 1u)
@@ -241,17 +289,18 @@ class FwhtExecutor final : public Executor {
             .field("algorithm", algorithm)
             .field("log_n", r.log_n)
             .field("batch", r.batch)
-            .field("block_elements", std::uint64_t{1} << lb)
-            .field("threads_per_block", 1u << (lb - kLE))
+            .field("tile_elements", std::uint64_t{1} << lb)
+            .field("tiles", tiles)
+            .field("grid", grid_)
+            .field("threads_per_block", threads)
             .field("registers_per_thread", unsigned(kE))
             .field("phases", unsigned((r.log_n + kLE - 1) / kLE))
-            .field("grid", blocks_)
-            .field("lds_bytes", std::uint64_t(((1u << lb) + ((1u << lb) >> kLE)) * 4))
+            .field("lds_bytes", lds)
             .end_object();
         mapping_json = w.str();
     }
     void execute(const void* in, void* out, void*, hipStream_t stream) override {
-        launch_(in, out, r_.n * r_.batch, norm_, scale_, stream);
+        launch_(in, out, r_.n * r_.batch, norm_, scale_, grid_, stream);
         hip_check(hipGetLastError(), "FWHT launch");
     }
 
@@ -259,7 +308,7 @@ class FwhtExecutor final : public Executor {
     Request r_;
     Launch launch_;
     float norm_ = 1.0f, scale_ = 1.0f;
-    std::uint64_t blocks_ = 0;
+    unsigned grid_ = 1;
 };
 
 }  // namespace

@@ -4,6 +4,16 @@
 
 namespace cbw {
 
+int device_cu_count() {
+    int device = 0, count = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    return count;
+}
+
 std::uint64_t powmod(std::uint64_t base, std::uint64_t exponent, std::uint64_t q) {
     std::uint64_t acc = 1 % q;
     base %= q;

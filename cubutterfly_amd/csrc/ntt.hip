@@ -1,10 +1,360 @@
-// NTT kernels for gfx950 (lowering added in a later milestone).
+// NTT kernels for gfx950 and the NttEngine that plans and launches them.
+//
+// One templated pass kernel covers every case: a workgroup owns a tile of
+// 2^LB words = 2^LT transform points x 2^LI independent lines, held as 16
+// words per thread. "ROW" tiles hold 2^LI contiguous rows (transform index in
+// the low tile bits); "COL" tiles hold 2^LI adjacent columns of stride 2^l2
+// (transform index in the high tile bits). The LT transform bits are
+// butterflied four at a time in registers (radix-16 windows, high->low for the
+// Cooley-Tukey forward, low->high for the Gentleman-Sande inverse) with LDS
+// exchanges between windows. Twiddles come from one table per domain indexed by
+// (n + j) >> (b + 1); see ntt_engine.hpp for the formulation.
+//
+// Arithmetic: Shoup multiplication a*w - hi(a*w')*q with w' = floor(w 2^k / q)
+// (V. Shoup; D. Harvey, "Faster arithmetic for number-theoretic transforms",
+// J. Symb. Comp. 2014): result in [0, 2q) for any word a. With 4q below the
+// word size ("lazy"), forward values live in [0, 4q) and inverse values in
+// [0, 2q); otherwise every butterfly keeps [0, 2q). Outputs are canonical.
 #include <hip/hip_runtime.h>
 
+#include "json.hpp"
+#include "ntt_kernels.hpp"
 #include "planner.hpp"
 
+#include <algorithm>
+
 namespace cbw {
-std::unique_ptr<Executor> make_ntt_executor(const Request&) {
-    throw NotSupported("NTT is not yet lowered for gfx950");
+namespace ntt_detail {
+
+template <>
+std::map<PassKey, PassLaunch<std::uint32_t>>& registry<std::uint32_t>() {
+    static std::map<PassKey, PassLaunch<std::uint32_t>> table;
+    return table;
 }
+template <>
+std::map<PassKey, PassLaunch<std::uint64_t>>& registry<std::uint64_t>() {
+    static std::map<PassKey, PassLaunch<std::uint64_t>> table;
+    return table;
+}
+
+}  // namespace ntt_detail
+
+namespace {
+using namespace ntt_detail;
+
+template <class W>
+PassLaunch<W> find_pass(const PassKey& key) {
+    static const bool once = [] {
+        register_u32_lazy();
+        register_u32_strict();
+        register_u64_lazy();
+        register_u64_strict();
+        return true;
+    }();
+    (void)once;
+    auto it = registry<W>().find(key);
+    if (it == registry<W>().end()) throw NotSupported("NTT pass shape has no gfx950 kernel");
+    return it->second;
+}
+
+// ---- host tables ------------------------------------------------------------
+
+template <class W>
+W shoup_factor(std::uint64_t w, std::uint64_t q) {
+    const unsigned bits = sizeof(W) * 8;
+    return static_cast<W>((static_cast<u128>(w) << bits) / q);
+}
+
+// Forward table T[k] (k = m + i, m = 2^s): negacyclic psi^bitrev_logn(k);
+// cyclic w^(bitrev_s(i) n / 2m). The inverse table uses the inverse root.
+template <class W>
+std::vector<TwPair<W>> make_table(std::uint32_t log_n, std::uint64_t q, std::uint64_t root, bool negacyclic) {
+    const std::uint64_t n = std::uint64_t{1} << log_n;
+    std::vector<TwPair<W>> table(n);
+    table[0] = {W(1), shoup_factor<W>(1, q)};
+    if (negacyclic) {
+        // powers[e] = root^e for e < n, then scatter by bit reversal.
+        std::uint64_t p = 1;
+        for (std::uint64_t e = 0; e < n; ++e) {
+            const std::uint64_t k = bit_reverse(e, log_n);
+            if (k) table[k] = {W(p), shoup_factor<W>(p, q)};
+            p = mulmod(p, root, q);
+        }
+    } else {
+        std::vector<std::uint64_t> pw(n / 2);
+        std::uint64_t p = 1;
+        for (std::uint64_t e = 0; e < n / 2; ++e, p = mulmod(p, root, q)) pw[e] = p;
+        for (std::uint32_t s = 0; s < log_n; ++s) {
+            const std::uint64_t m = std::uint64_t{1} << s;
+            for (std::uint64_t i = 0; i < m; ++i) {
+                const std::uint64_t e = bit_reverse(i, s) * (n / (2 * m));
+                table[m + i] = {W(pw[e]), shoup_factor<W>(pw[e], q)};
+            }
+        }
+    }
+    return table;
+}
+
+template <class W>
+struct EngineImplT {
+    NttEngineConfig cfg;
+    bool lazy = false;
+    std::uint32_t l1 = 0, l2 = 0;
+    std::vector<DeviceBuffer> tables;
+    DeviceBuffer domains, poly_domain, in_off, out_off;
+    struct Launch {
+        PassLaunch<W> fn;
+        unsigned grid;
+        PassArgs<W> args;
+        bool reads_workspace, writes_workspace;
+    };
+    std::vector<Launch> launches;
+    std::string json_shape;
+
+    explicit EngineImplT(const NttEngineConfig& c) : cfg(c) {
+        const std::uint32_t log_n = c.log_n;
+        const std::uint64_t n = std::uint64_t{1} << log_n;
+        const unsigned bits = sizeof(W) * 8;
+        std::uint64_t max_q = 0;
+        for (const auto& d : c.domains) max_q = std::max(max_q, d.modulus);
+        lazy = max_q < (std::uint64_t{1} << (bits - 2));
+        // Device domain records and their tables.
+        std::vector<DeviceDomain<W>> host_domains;
+        for (const auto& d : c.domains) {
+            const std::uint64_t q = d.modulus;
+            const std::uint64_t root = c.inverse ? invmod(d.root, q) : d.root;
+            auto table = make_table<W>(log_n, q, root, c.negacyclic);
+            DeviceBuffer buffer;
+            buffer.upload(table);
+            DeviceDomain<W> dd{};
+            dd.q = W(q);
+            dd.q2 = W(2 * q);
+            dd.rwp = shoup_factor<W>(1, q);
+            const std::uint64_t ninv = invmod(n % q, q);
+            dd.ninv = {W(ninv), shoup_factor<W>(ninv, q)};
+            const std::uint64_t last = mulmod(table[1].w, ninv, q);
+            dd.last = {W(last), shoup_factor<W>(last, q)};
+            dd.tw = buffer.as<TwPair<W>>();
+            host_domains.push_back(dd);
+            tables.push_back(std::move(buffer));
+        }
+        domains.upload(host_domains);
+        const std::uint64_t polys = c.polynomials.empty() ? c.batch : c.polynomials.size();
+        require(polys >= 1 && polys <= 0xffffffffull, "NTT batch must be in [1, 2^32)");
+        if (!c.polynomials.empty()) {
+            std::vector<std::uint32_t> pd;
+            std::vector<std::uint64_t> io, oo;
+            for (const auto& p : c.polynomials) {
+                pd.push_back(p.domain);
+                io.push_back(p.input_offset);
+                oo.push_back(p.output_offset);
+            }
+            poly_domain.upload(pd);
+            in_off.upload(io);
+            out_off.upload(oo);
+        }
+        const bool mixed = c.domains.size() > 1;
+        PassArgs<W> base{};
+        base.domains = domains.as<DeviceDomain<W>>();
+        base.poly_domain = poly_domain.as<std::uint32_t>();
+        base.polys = static_cast<std::uint32_t>(polys);
+        constexpr int LB = 12;
+        const bool ct = !c.inverse;
+        // Which physical boundaries differ from the algorithm's native order
+        // (forward: natural in / bit-reversed out; inverse: the opposite).
+        const bool perm_in = ct ? c.input_bit_reversed : !c.input_bit_reversed;
+        const bool perm_out = ct ? !c.output_bit_reversed : c.output_bit_reversed;
+        if (log_n <= 12) {
+            // One pass: whole polynomials per workgroup (one per tile if domains mix).
+            const int li = LB - int(log_n);
+            supported(!mixed || li == 0, "mixed-domain batches need log n >= 12");
+            l1 = 0;
+            l2 = log_n;
+            const std::uint64_t per_tile = std::uint64_t{1} << li;
+            const std::uint64_t tiles = (polys + per_tile - 1) / per_tile;
+            Launch L{};
+            L.fn = find_pass<W>(PassKey{lazy, int(log_n), li, false, ct, perm_in, perm_out, true});
+            L.grid = unsigned(tiles);
+            L.args = base;
+            L.args.l1 = 0;
+            L.args.l2 = log_n;
+            L.args.tiles = unsigned(tiles);
+            L.args.in_off = in_off.as<std::uint64_t>();
+            L.args.out_off = out_off.as<std::uint64_t>();
+            L.args.reduce_input = c.reduce_input;
+            launches.push_back(L);
+            json_shape = "{\"passes\":1,\"tile_log\":" + std::to_string(LB) + "}";
+        } else {
+            supported(log_n <= 20, "NTT lengths above 2^20 are not yet lowered for gfx950");
+            l1 = std::min<std::uint32_t>(8, log_n / 2);
+            l2 = log_n - l1;
+            const int col_li = 4;
+            const int rli = std::min<int>(int(l1), LB - int(l2));
+            const std::uint64_t col_tiles = polys << (l2 - col_li);
+            const std::uint64_t row_tiles = polys << (l1 - rli);
+            require(col_tiles <= 0xffffffffull && row_tiles <= 0xffffffffull, "NTT batch exceeds the grid");
+            Launch A{}, B{};
+            // Pass A: high bits (columns); pass B: low bits (rows).
+            A.args = base;
+            A.args.l1 = l1;
+            A.args.l2 = l2;
+            A.args.tiles = unsigned(col_tiles);
+            A.grid = unsigned(col_tiles);
+            B.args = A.args;
+            B.args.tiles = unsigned(row_tiles);
+            B.grid = unsigned(row_tiles);
+            A.fn = find_pass<W>(PassKey{lazy, int(l1), col_li, true, ct, ct && perm_in, !ct && perm_out, false});
+            B.fn = find_pass<W>(PassKey{lazy, int(l2), rli, false, ct, !ct && perm_in, ct && perm_out, false});
+            if (ct) {  // forward: A reads the input, B writes the output
+                A.args.in_off = in_off.as<std::uint64_t>();
+                A.args.reduce_input = c.reduce_input;
+                A.writes_workspace = true;
+                B.reads_workspace = true;
+                B.args.out_off = out_off.as<std::uint64_t>();
+                launches = {A, B};
+            } else {  // inverse: B reads the input, A writes the output
+                B.args.in_off = in_off.as<std::uint64_t>();
+                B.args.reduce_input = c.reduce_input;
+                B.writes_workspace = true;
+                A.reads_workspace = true;
+                A.args.out_off = out_off.as<std::uint64_t>();
+                launches = {B, A};
+            }
+            json_shape = "{\"passes\":2,\"high_bits\":" + std::to_string(l1) + ",\"low_bits\":" +
+                         std::to_string(l2) + ",\"column_tile_lines\":" + std::to_string(1 << col_li) +
+                         ",\"row_tile_lines\":" + std::to_string(1 << rli) + "}";
+        }
+    }
+
+    std::size_t workspace_bytes() const {
+        if (launches.size() < 2) return 0;
+        const std::uint64_t polys = cfg.polynomials.empty() ? cfg.batch : cfg.polynomials.size();
+        return static_cast<std::size_t>((polys << cfg.log_n) * sizeof(W));
+    }
+
+    void execute(const void* in, void* out, void* ws, hipStream_t stream) const {
+        require(launches.size() < 2 || ws != nullptr, "two-pass NTT needs a workspace");
+        for (const auto& L : launches) {
+            PassArgs<W> a = L.args;
+            a.in = static_cast<const W*>(L.reads_workspace ? ws : in);
+            a.out = static_cast<W*>(L.writes_workspace ? ws : out);
+            L.fn(a, L.grid, stream);
+            hip_check(hipGetLastError(), "NTT pass launch");
+        }
+    }
+};
+
+}  // namespace
+
+struct NttEngine::Impl {
+    std::unique_ptr<EngineImplT<std::uint32_t>> u32;
+    std::unique_ptr<EngineImplT<std::uint64_t>> u64;
+};
+
+NttEngine::NttEngine(const NttEngineConfig& c) : impl_(new Impl) {
+    require(c.word_bits == 32 || c.word_bits == 64, "NTT word bits must be 32 or 64");
+    require(c.log_n >= 1 && c.log_n <= 30, "NTT log n must be in [1, 30]");
+    require(!c.domains.empty(), "NTT needs at least one domain");
+    for (const auto& d : c.domains) {
+        require(d.modulus >= 3 && (c.word_bits == 64 ? d.modulus < (1ull << 63) : d.modulus < (1ull << 31)),
+                "NTT modulus out of range for the word size");
+        require(d.root != 0 && d.root < d.modulus, "NTT root must be in [1, q)");
+    }
+    for (const auto& p : c.polynomials) require(p.domain < c.domains.size(), "polynomial domain out of range");
+    if (c.word_bits == 32)
+        impl_->u32 = std::make_unique<EngineImplT<std::uint32_t>>(c);
+    else
+        impl_->u64 = std::make_unique<EngineImplT<std::uint64_t>>(c);
+    const bool two = passes() == 2;
+    algorithm_ = std::string("ntt-u") + std::to_string(c.word_bits) + (c.negacyclic ? "-negacyclic" : "-cyclic") +
+                 (two ? "-two-pass-r16" : "-resident-r16");
+    json::Writer w;
+    w.begin_object()
+        .field("schema_version", 1u)
+        .field("operator", "ntt")
+        .field("algorithm", algorithm_)
+        .field("word_bits", c.word_bits)
+        .field("log_n", c.log_n)
+        .field("ring", c.negacyclic ? "negacyclic" : "cyclic")
+        .field("direction", c.inverse ? "inverse" : "forward")
+        .field("input_order", c.input_bit_reversed ? "bit_reversed" : "natural")
+        .field("output_order", c.output_bit_reversed ? "bit_reversed" : "natural")
+        .field("arithmetic", "shoup")
+        .field("lazy_reduction", impl_->u32 ? impl_->u32->lazy : impl_->u64->lazy)
+        .key("shape")
+        .value_raw(impl_->u32 ? impl_->u32->json_shape : impl_->u64->json_shape)
+        .field("workspace_bytes", std::uint64_t(workspace_bytes()))
+        .end_object();
+    mapping_json_ = w.str();
+}
+
+NttEngine::~NttEngine() = default;
+
+std::size_t NttEngine::workspace_bytes() const {
+    return impl_->u32 ? impl_->u32->workspace_bytes() : impl_->u64->workspace_bytes();
+}
+
+std::uint32_t NttEngine::passes() const {
+    return std::uint32_t(impl_->u32 ? impl_->u32->launches.size() : impl_->u64->launches.size());
+}
+
+void NttEngine::execute(const void* in, void* out, void* ws, hipStream_t stream) const {
+    if (impl_->u32)
+        impl_->u32->execute(in, out, ws, stream);
+    else
+        impl_->u64->execute(in, out, ws, stream);
+}
+
+// ---- cubutterfly.h NTT plans -------------------------------------------------
+
+namespace {
+
+class NttExecutor final : public Executor {
+  public:
+    explicit NttExecutor(const Request& r) {
+        NttEngineConfig c;
+        c.word_bits = r.word_bits;
+        c.log_n = r.log_n;
+        c.negacyclic = r.negacyclic;
+        c.inverse = r.inverse;
+        c.input_bit_reversed = r.input_bit_reversed;
+        c.output_bit_reversed = r.output_bit_reversed;
+        c.reduce_input = true;  // reference_ntt reduces inputs mod q (src/reference.cpp:601-603)
+        c.batch = r.batch;
+        // Root conventions of the reference (src/reference.cpp:564-582;
+        // crypto_ntt_bench.cu:273-323).
+        const std::uint64_t w = primitive_root_pow2(r.log_n, r.modulus);
+        std::uint64_t root = w;
+        if (r.negacyclic) {
+            if (r.psi) {
+                const std::uint64_t order = std::uint64_t{2} << r.log_n;
+                require(r.psi < r.modulus && powmod(r.psi, order >> 1, r.modulus) == r.modulus - 1,
+                        "psi must be a primitive 2n-th root of unity");
+                root = r.psi;
+            } else {
+                root = psi_for_root(r.log_n, r.modulus, w);
+            }
+        }
+        c.domains.push_back({r.modulus, root});
+        engine_ = std::make_unique<NttEngine>(c);
+        algorithm = engine_->algorithm();
+        mapping_json = engine_->mapping_json();
+        reason = engine_->passes() == 1
+                     ? "whole polynomials resident in one workgroup (radix-16 register windows, LDS exchange)"
+                     : "two passes over high/low index bits (coalesced column and row tiles), merged-twist "
+                       "Cooley-Tukey / Gentleman-Sande with Shoup arithmetic";
+    }
+    std::size_t workspace_bytes() const override { return engine_->workspace_bytes(); }
+    void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
+        engine_->execute(in, out, ws, stream);
+    }
+
+  private:
+    std::unique_ptr<NttEngine> engine_;
+};
+
+}  // namespace
+
+std::unique_ptr<Executor> make_ntt_executor(const Request& r) { return std::make_unique<NttExecutor>(r); }
+
 }  // namespace cbw

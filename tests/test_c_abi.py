@@ -46,7 +46,7 @@ def test_fwht_plan_sizes_and_introspection(lib):
         assert plan.workspace_size() == 0
         assert plan.algorithm_name() == "fwht-fp32-resident-r16"
         mapping = json.loads(plan.mapping_json())
-        assert mapping["log_n"] == 12 and mapping["grid"] == 4096
+        assert mapping["log_n"] == 12 and mapping["tiles"] == 4096 and 1 <= mapping["grid"] <= 4096
         assert plan.selection_source() == cb.SelectionSource.STATIC_MODEL
         d = json.loads(plan.descriptor_json())
         assert d["shape"] == [4096] and d["batch"] == 4096 and d["operator"] == int(cb.Operator.FWHT)
