@@ -173,7 +173,96 @@ class NttNegacyclic(Workload):
                                                 "crypto-benchmark composition: psi twist + reference_ntt DIT")
 
 
-WORKLOADS = {"c1": FwhtFp32, "c2": NttNegacyclic}
+class RnsNegacyclic(Workload):
+    """C4: RNS negacyclic NTT, 32 limbs x n = 2^16 of 60-bit primes, forward
+    (natural -> bit-reversed) then inverse (bit-reversed -> natural)."""
+    name = "c4"
+    dtype = "u64"
+    description = ("RNS negacyclic NTT u64, n=2^16, 32 limbs of distinct 60-bit primes (q = 1 mod 2^17), "
+                   "one step = forward (natural->bit_reversed) then inverse (bit_reversed->natural)")
+
+    def __init__(self, log_n=16, limbs=32):
+        from cubutterfly_amd import workloads
+        self.log_n, self.limbs = log_n, limbs
+        self.moduli = workloads.c4_moduli()[:limbs]
+        self.transforms_per_call = 2 * limbs
+        self.bytes_per_call = 2 * 2 * limbs * (8 << log_n)
+
+    def setup(self, torch, lib, stream):
+        from cubutterfly_amd import ntt_roots, rns, workloads
+        rlib = rns.Library()
+        # psi_i: the reference's rule, smallest-candidate primitive 2n-th root.
+        self.roots = [ntt_roots.primitive_root(self.log_n + 1, q) for q in self.moduli]
+        domains = list(zip(self.moduli, self.roots))
+        self.plans = []
+        for inverse in (False, True):
+            plan = rns.Plan(rlib, rns.config(self.log_n, domains, inverse=inverse))
+            plan.prepare(placement=rns.Placement.SEPARATE, stream=stream, repetitions=3)
+            self.plans.append(plan)
+        self.stream = stream
+        self.host = np.stack([workloads.ntt_input(self.log_n, 1, q, seed=1, channel=i)[0]
+                              for i, q in enumerate(self.moduli)])
+        src = _np_to_torch(torch, self.host).to("cuda")
+        sets = self._rotation(torch, 3 * src.numel() * 8)
+        self.inputs = [src.clone() for _ in range(sets)]
+        self.spectra = [torch.empty_like(src) for _ in range(sets)]
+        self.outputs = [torch.empty_like(src) for _ in range(sets)]
+
+    def call(self, index):
+        k = index % len(self.inputs)
+        self.plans[0].execute(self.inputs[k], self.spectra[k], stream=self.stream)
+        self.plans[1].execute(self.spectra[k], self.outputs[k], stream=self.stream)
+
+    def verify(self, torch):
+        import oracle
+        spectrum = self.spectra[0].cpu().numpy().view(np.uint64)
+        back = self.outputs[0].cpu().numpy().view(np.uint64)
+        expected = oracle.rns(self.host, self.moduli, self.roots, output_bit_reversed=True,
+                              threads=oracle.default_threads())
+        return bool(np.array_equal(spectrum, expected) and np.array_equal(back, self.host))
+
+    def kernel_name(self):
+        return self.plans[0].info()["mapping"]["algorithm"] + " (forward) + inverse"
+
+    def cpu_sample(self, threads):
+        import oracle
+        reps, elapsed = 0, 0.0
+        while elapsed < 10.0:
+            t0 = time.perf_counter()
+            y = oracle.rns(self.host, self.moduli, self.roots, output_bit_reversed=True, threads=threads)
+            oracle.rns(y, self.moduli, self.roots, inverse=True, input_bit_reversed=True, threads=threads)
+            elapsed += time.perf_counter() - t0
+            reps += 1
+        return elapsed, reps * 2 * self.limbs, (f"{reps} full C4 steps (32 limbs x 2^16 forward + inverse) through "
+                                                "the reference RNS oracle (tests/test_rns_ntt.cu:62-111)")
+
+
+class DeviceCopy(Workload):
+    """Calibration probe, not a BASELINE config: a plain device-to-device copy
+    of 128 MiB, the known-size reference for rocprofv3 FETCH_SIZE/WRITE_SIZE."""
+    name = "copy"
+    dtype = "u8"
+    description = "plain device copy of 134217728 bytes (HBM traffic counter calibration)"
+    transforms_per_call = 1
+    bytes_per_call = 2 * 134217728
+
+    def setup(self, torch, lib, stream):
+        sets = self._rotation(torch, self.bytes_per_call)
+        self.inputs = [torch.ones(134217728 // 4, dtype=torch.float32, device="cuda") for _ in range(sets)]
+        self.outputs = [torch.empty_like(self.inputs[0]) for _ in range(sets)]
+
+    def call(self, index):
+        k = index % len(self.inputs)
+        self.outputs[k].copy_(self.inputs[k])
+
+    def kernel_name(self):
+        return "torch copy_"
+
+    def cpu_sample(self, threads):
+        return 1.0, 0, "no CPU baseline for the calibration copy"
+
+
+WORKLOADS = {"c1": FwhtFp32, "c2": NttNegacyclic, "c4": RnsNegacyclic, "copy": DeviceCopy}
 DEFAULT_WORKLOAD = "c2"
 
 
@@ -198,12 +287,14 @@ def time_calls(torch, workload, stream, steps, warmup, use_graph=True):
                 workload.call(i)
         torch.cuda.synchronize()
         replays = max(1, -(-steps // CALLS_PER_GRAPH))
-        graph.replay()  # first replay uploads the graph
-        torch.cuda.synchronize()
-        start.record(stream)
-        for _ in range(replays):
-            graph.replay()
-        stop.record(stream)
+        # replay() launches on the current stream: make it the plans' stream.
+        with torch.cuda.stream(stream):
+            graph.replay()  # first replay uploads the graph
+            torch.cuda.synchronize()
+            start.record(stream)
+            for _ in range(replays):
+                graph.replay()
+            stop.record(stream)
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / (replays * CALLS_PER_GRAPH), replays * CALLS_PER_GRAPH
     start.record(stream)

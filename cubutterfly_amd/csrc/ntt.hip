@@ -22,6 +22,7 @@
 #include "planner.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace cbw {
 namespace ntt_detail {
@@ -95,13 +96,28 @@ std::vector<TwPair<W>> make_table(std::uint32_t log_n, std::uint64_t q, std::uin
     return table;
 }
 
+// Persistent grid of a pass: each workgroup walks several tiles so the next
+// tile's loads overlap the current tile's arithmetic. Two resident workgroups
+// per CU by default (CUBUTTERFLY_NTT_WG_PER_CU overrides, 1..8); a multiple of
+// 8 so every XCD gets the same number of workgroups.
+inline unsigned persistent_grid(std::uint64_t tiles) {
+    static const unsigned per_cu = [] {
+        const char* env = std::getenv("CUBUTTERFLY_NTT_WG_PER_CU");
+        const int v = env ? std::atoi(env) : 2;
+        return unsigned(v >= 1 && v <= 8 ? v : 2);
+    }();
+    const std::uint64_t resident = std::uint64_t(device_cu_count()) * per_cu;
+    std::uint64_t grid = std::min<std::uint64_t>(tiles, resident);
+    if (grid > 8) grid &= ~std::uint64_t{7};
+    return unsigned(std::max<std::uint64_t>(grid, 1));
+}
+
 template <class W>
 struct EngineImplT {
     NttEngineConfig cfg;
     bool lazy = false;
     std::uint32_t l1 = 0, l2 = 0;
-    std::vector<DeviceBuffer> tables;
-    DeviceBuffer domains, poly_domain, in_off, out_off;
+    DeviceBuffer tables, domains, poly_domain, in_off, out_off;
     struct Launch {
         PassLaunch<W> fn;
         unsigned grid;
@@ -120,12 +136,11 @@ struct EngineImplT {
         lazy = max_q < (std::uint64_t{1} << (bits - 2));
         // Device domain records and their tables.
         std::vector<DeviceDomain<W>> host_domains;
+        std::vector<TwPair<W>> all_tables;
         for (const auto& d : c.domains) {
             const std::uint64_t q = d.modulus;
             const std::uint64_t root = c.inverse ? invmod(d.root, q) : d.root;
             auto table = make_table<W>(log_n, q, root, c.negacyclic);
-            DeviceBuffer buffer;
-            buffer.upload(table);
             DeviceDomain<W> dd{};
             dd.q = W(q);
             dd.q2 = W(2 * q);
@@ -134,10 +149,11 @@ struct EngineImplT {
             dd.ninv = {W(ninv), shoup_factor<W>(ninv, q)};
             const std::uint64_t last = mulmod(table[1].w, ninv, q);
             dd.last = {W(last), shoup_factor<W>(last, q)};
-            dd.tw = buffer.as<TwPair<W>>();
+            dd.tw = all_tables.size();
             host_domains.push_back(dd);
-            tables.push_back(std::move(buffer));
+            all_tables.insert(all_tables.end(), table.begin(), table.end());
         }
+        tables.upload(all_tables);
         domains.upload(host_domains);
         const std::uint64_t polys = c.polynomials.empty() ? c.batch : c.polynomials.size();
         require(polys >= 1 && polys <= 0xffffffffull, "NTT batch must be in [1, 2^32)");
@@ -156,6 +172,7 @@ struct EngineImplT {
         const bool mixed = c.domains.size() > 1;
         PassArgs<W> base{};
         base.domains = domains.as<DeviceDomain<W>>();
+        base.tw = tables.as<TwPair<W>>();
         base.poly_domain = poly_domain.as<std::uint32_t>();
         base.polys = static_cast<std::uint32_t>(polys);
         constexpr int LB = 12;
@@ -174,7 +191,7 @@ struct EngineImplT {
             const std::uint64_t tiles = (polys + per_tile - 1) / per_tile;
             Launch L{};
             L.fn = find_pass<W>(PassKey{lazy, int(log_n), li, false, ct, perm_in, perm_out, true});
-            L.grid = unsigned(tiles);
+            L.grid = persistent_grid(tiles);
             L.args = base;
             L.args.l1 = 0;
             L.args.l2 = log_n;
@@ -199,10 +216,10 @@ struct EngineImplT {
             A.args.l1 = l1;
             A.args.l2 = l2;
             A.args.tiles = unsigned(col_tiles);
-            A.grid = unsigned(col_tiles);
+            A.grid = persistent_grid(col_tiles);
             B.args = A.args;
             B.args.tiles = unsigned(row_tiles);
-            B.grid = unsigned(row_tiles);
+            B.grid = persistent_grid(row_tiles);
             A.fn = find_pass<W>(PassKey{lazy, int(l1), col_li, true, ct, ct && perm_in, !ct && perm_out, false});
             B.fn = find_pass<W>(PassKey{lazy, int(l2), rli, false, ct, !ct && perm_in, ct && perm_out, false});
             if (ct) {  // forward: A reads the input, B writes the output

@@ -27,7 +27,7 @@ struct DeviceDomain {
     W q, q2, rwp;         // modulus, 2q, floor(2^k / q) (Shoup factor of 1)
     TwPair<W> ninv;       // n^-1 with its Shoup factor
     TwPair<W> last;       // Tinv[1] * n^-1 (final inverse stage)
-    const TwPair<W>* tw;  // entries 1..n-1
+    std::uint64_t tw;     // offset of this domain's table (entries 1..n-1) in PassArgs::tw
 };
 
 template <class W>
@@ -35,6 +35,7 @@ struct PassArgs {
     const W* in;
     W* out;
     const DeviceDomain<W>* domains;
+    const TwPair<W>* tw;               // all domains' twiddle tables, concatenated
     const std::uint32_t* poly_domain;  // per polynomial (null: domain 0)
     const std::uint64_t* in_off;       // per polynomial word offset (null: p << log n)
     const std::uint64_t* out_off;
@@ -211,12 +212,16 @@ struct Pass {
 
     template <int P>
     static __device__ __forceinline__ void stages(W (&v)[kE], const Tile& tl, std::uint32_t t,
-                                                  const DeviceDomain<W>& d) {
+                                                  const DeviceDomain<W>& d, const TwPair<W>* __restrict__ table) {
         constexpr int ws = window_start<LT, CT, P>();
         constexpr int tw0 = tile_window<P>();
-        // Transform index and row of register 0 (window bits clear).
+        // Transform index and twiddle prefix of register 0 (window bits clear).
+        // The prefix is 1 for columns and 2^l1 + row for rows; the row is the
+        // same for all registers whenever LT >= 4 (and 0 for one-pass tiles).
         const std::uint32_t i0 = phase_index<tw0>(t, 0);
         const std::uint32_t x0 = COL ? (i0 >> LI) : (i0 & ((1u << LT) - 1u));
+        const std::uint32_t prefix = COL ? 1u : ((1u << tl.l1) + row_of(tl, i0 >> LT));
+        const std::uint32_t head = (prefix << LT) | x0;
 #pragma unroll
         for (int s = 0; s < kLE; ++s) {
             // CT walks bits high -> low, GS low -> high; skip bits of other phases.
@@ -224,21 +229,18 @@ struct Pass {
             const bool mine = CT ? (k < LT - kLE * P && k >= 0) : (k >= kLE * P && k < LT);
             if (!mine || k >= LT) continue;
             const int jb = k - ws;
+            // Group g (register bits above jb) uses twiddle (head >> (k+1)) + g;
+            // register bits beyond the transform (LT < 4) do not index it.
+            const std::uint32_t gmask = (1u << (LT - 1 - k)) - 1u;
+            const TwPair<W>* __restrict__ tk = table + (head >> (k + 1));
+            const bool scale_stage = kLast && !CT && k == LT - 1;
 #pragma unroll
             for (int g = 0; g < (1 << (kLE - 1 - jb)); ++g) {
-                const std::uint32_t rg = std::uint32_t(g) << (jb + 1);  // register bits above jb
-                // Row (hence twiddle prefix) may vary with the register only for LT < 4.
-                const std::uint32_t ig = phase_index<tw0>(t, rg);
-                const std::uint32_t rr = COL ? 0u : (ig >> LT);
-                const std::uint32_t prefix = COL ? 1u : ((1u << tl.l1) + row_of(tl, rr));
-                const std::uint32_t x = (x0 | (rg << ws)) & ((1u << LT) - 1u);
-                const std::uint32_t idx = ((prefix << LT) | x) >> (k + 1);
-                const bool scale_stage = kLast && !CT && k == LT - 1;
                 TwPair<W> tw{};
-                if (!scale_stage) tw = d.tw[idx];
+                if (!scale_stage) tw = tk[std::uint32_t(g) & gmask];
 #pragma unroll
                 for (int lo = 0; lo < (1 << jb); ++lo) {
-                    const int r = int(rg) | lo;
+                    const int r = (g << (jb + 1)) | lo;
                     const int r2 = r | (1 << jb);
                     if constexpr (CT) {
                         ct_butterfly<W, LAZY>(v[r], v[r2], tw, d.q, d.q2);
@@ -262,18 +264,10 @@ struct Pass {
         for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<TO>(t, r))];
     }
 
-    static __device__ void run(const PassArgs<W>& a) {
-        __shared__ W lds[L::kWords];
-        const std::uint32_t t = threadIdx.x;
-        // XCD-aware tile order: the 8 XCDs receive blocks round-robin, so give
-        // each XCD a contiguous run of tiles (neighbouring tiles share lines).
-        std::uint32_t tile = blockIdx.x;
-        if ((a.tiles & 7u) == 0) tile = (tile & 7u) * (a.tiles >> 3) + (tile >> 3);
-
+    static __device__ __forceinline__ Tile decode(const PassArgs<W>& a, std::uint32_t tile) {
         Tile tl{};
         tl.l1 = a.l1;
         tl.l2 = a.l2;
-        const std::uint32_t log_n = a.l1 + a.l2;
         if constexpr (COL) {
             const std::uint32_t shift = a.l2 - LI;
             tl.poly = tile >> shift;
@@ -285,47 +279,72 @@ struct Pass {
             tl.poly = tile >> shift;
             tl.k0 = (tile & ((1u << shift) - 1u)) << LI;
         }
+        return tl;
+    }
+
+    // Word address and validity of register r's input element.
+    static __device__ __forceinline__ void input_word(const PassArgs<W>& a, const Tile& tl, std::uint32_t t, int r,
+                                                      std::uint64_t& where, bool& valid) {
+        const std::uint32_t log_n = a.l1 + a.l2;
+        std::uint32_t i, p;
+        std::uint64_t word;
+        if constexpr (PIN) {
+            permuted(tl, t + T * r, i, p, word);
+        } else {
+            i = phase_index<tile_window<0>()>(t, r);
+            p = poly_of(tl, i);
+            word = natural_word(tl, i);
+        }
+        valid = !SINGLE || p < a.polys;
+        where = (valid ? base(a.in_off, SINGLE ? p : tl.poly, log_n) : 0) + word;
+    }
+
+    // Issue the 16 loads of a tile (raw words; reduction happens later).
+    static __device__ __forceinline__ void load_tile(const PassArgs<W>& a, const Tile& tl, std::uint32_t t,
+                                                     W (&v)[kE]) {
+        std::uint64_t where[kE];
+        bool valid[kE];
+#pragma unroll
+        for (int r = 0; r < kE; ++r) input_word(a, tl, t, r, where[r], valid[r]);
+#pragma unroll
+        for (int r = 0; r < kE; ++r) v[r] = valid[r] ? a.in[where[r]] : W(0);
+    }
+
+    static __device__ __forceinline__ void process(const PassArgs<W>& a, const Tile& tl, std::uint32_t t, W (&v)[kE],
+                                                   W* lds) {
+        const std::uint32_t log_n = a.l1 + a.l2;
         // One domain per tile (the planner keeps mixed-domain tiles apart).
         const std::uint32_t dom = a.poly_domain ? a.poly_domain[tl.poly] : 0u;
         const DeviceDomain<W> d = a.domains[dom];
-
-        W v[kE];
-        constexpr int w0 = tile_window<0>();
-        const bool reduce = kFirst && a.reduce_input;
+        // Kernel-argument pointers are known to address global memory, so the
+        // twiddle gathers compile to global (not FLAT) loads.
+        const TwPair<W>* __restrict__ table = a.tw + d.tw;
+        if (kFirst && a.reduce_input) {
+#pragma unroll
+            for (int r = 0; r < kE; ++r) v[r] = shoup(v[r], W(1), d.rwp, d.q);
+        }
         if constexpr (PIN) {
+            lds_barrier();
 #pragma unroll
             for (int r = 0; r < kE; ++r) {
                 std::uint32_t i, p;
                 std::uint64_t word;
                 permuted(tl, t + T * r, i, p, word);
-                W x = 0;
-                if (!SINGLE || p < a.polys) x = a.in[base(a.in_off, p, log_n) + word];
-                if (reduce) x = shoup(x, W(1), d.rwp, d.q);
-                lds[L::addr(i)] = x;
+                lds[L::addr(i)] = v[r];
             }
             lds_barrier();
 #pragma unroll
-            for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<w0>(t, r))];
-        } else {
-#pragma unroll
-            for (int r = 0; r < kE; ++r) {
-                const std::uint32_t i = phase_index<w0>(t, r);
-                const std::uint32_t p = poly_of(tl, i);
-                W x = 0;
-                if (!SINGLE || p < a.polys) x = a.in[base(a.in_off, p, log_n) + natural_word(tl, i)];
-                if (reduce) x = shoup(x, W(1), d.rwp, d.q);
-                v[r] = x;
-            }
+            for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<tile_window<0>()>(t, r))];
         }
 
-        stages<0>(v, tl, t, d);
+        stages<0>(v, tl, t, d, table);
         if constexpr (kPhases > 1) {
             exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
-            stages<1>(v, tl, t, d);
+            stages<1>(v, tl, t, d, table);
         }
         if constexpr (kPhases > 2) {
             exchange<tile_window<1>(), tile_window<2>()>(v, lds, t);
-            stages<2>(v, tl, t, d);
+            stages<2>(v, tl, t, d, table);
         }
         constexpr int wl = tile_window<kPhases - 1>();
         if constexpr (kLast) {
@@ -336,6 +355,9 @@ struct Pass {
                 v[r] = csub(x, d.q);
             }
         }
+        const std::uint64_t out_tile = SINGLE ? 0 : base(a.out_off, tl.poly, log_n);
+        std::uint64_t where[kE];
+        bool valid[kE];
         if constexpr (POUT) {
             lds_barrier();
 #pragma unroll
@@ -346,15 +368,59 @@ struct Pass {
                 std::uint32_t i, p;
                 std::uint64_t word;
                 permuted(tl, t + T * r, i, p, word);
-                if (!SINGLE || p < a.polys) a.out[base(a.out_off, p, log_n) + word] = lds[L::addr(i)];
+                v[r] = lds[L::addr(i)];
+                valid[r] = !SINGLE || p < a.polys;
+                where[r] = (SINGLE ? (valid[r] ? base(a.out_off, p, log_n) : 0) : out_tile) + word;
             }
         } else {
 #pragma unroll
             for (int r = 0; r < kE; ++r) {
                 const std::uint32_t i = phase_index<wl>(t, r);
                 const std::uint32_t p = poly_of(tl, i);
-                if (!SINGLE || p < a.polys) a.out[base(a.out_off, p, log_n) + natural_word(tl, i)] = v[r];
+                valid[r] = !SINGLE || p < a.polys;
+                where[r] = (SINGLE ? (valid[r] ? base(a.out_off, p, log_n) : 0) : out_tile) + natural_word(tl, i);
             }
+        }
+#pragma unroll
+        for (int r = 0; r < kE; ++r)
+            if (valid[r]) a.out[where[r]] = v[r];
+    }
+
+    // Persistent walk over tiles: the next tile's loads are issued before the
+    // current tile is processed. When the tile count and the grid are
+    // multiples of 8, each XCD (blocks are dealt to the 8 XCDs round-robin)
+    // walks one contiguous range of tiles, so tiles sharing cache lines and
+    // twiddle rows meet in the same L2.
+    static __device__ void run(const PassArgs<W>& a) {
+        __shared__ W lds[L::kWords];
+        const std::uint32_t t = threadIdx.x;
+        const std::uint32_t grid = gridDim.x, b = blockIdx.x;
+        const bool xcd = (a.tiles & 7u) == 0 && (grid & 7u) == 0;
+        const std::uint32_t per_xcd = a.tiles >> 3, stride = xcd ? (grid >> 3) : grid;
+        const std::uint32_t first = xcd ? (b >> 3) : b;  // position within this block's range
+        const std::uint32_t range_base = xcd ? (b & 7u) * per_xcd : 0u;
+        const std::uint32_t range_end = xcd ? per_xcd : a.tiles;
+
+        std::uint32_t pos = first;
+        if (pos >= range_end) return;
+        Tile tl = decode(a, range_base + pos);
+        W v[kE];
+        load_tile(a, tl, t, v);
+        for (;;) {
+            const std::uint32_t next = pos + stride;
+            const bool more = next < range_end;
+            Tile tn{};
+            W nv[kE];
+            if (more) {
+                tn = decode(a, range_base + next);
+                load_tile(a, tn, t, nv);
+            }
+            process(a, tl, t, v, lds);
+            if (!more) break;
+            pos = next;
+            tl = tn;
+#pragma unroll
+            for (int r = 0; r < kE; ++r) v[r] = nv[r];
         }
     }
 };

@@ -1,30 +1,442 @@
-// RNS C ABI (include/cuntt/rns_c_api.h). Lowering added in a later milestone.
+// RNS C ABI (include/cuntt/rns_c_api.h): multi-limb word64 NTT plans over
+// caller-owned buffers with per-polynomial domains and word offsets.
+//
+// Behaviour follows the reference boundary (src/rns_c_api.cpp:41-113,
+// src/rns_tuning.cpp:114-251, src/rns_ntt.cu:256-300): strict JSON config with
+// unknown fields rejected; prime moduli below 2^63 with explicit roots of
+// exact ring order; disjoint output intervals; Prepare once (outside graph
+// capture) with a prepared-plan cache record; Execute asynchronous and
+// allocation-free with pointer aliasing matching the prepared placement.
+// The gfx950 lowering is the NttEngine (merged-twist CT forward / GS inverse),
+// so Prepare measures the static plan instead of searching mappings.
 #include "../../include/cuntt/rns_c_api.h"
 
+#include "common.hpp"
+#include "json.hpp"
+#include "ntt_engine.hpp"
+
+#include <algorithm>
+#include <cerrno>
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <fcntl.h>
+#include <fstream>
+#include <iomanip>
+#include <sstream>
 #include <string>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <vector>
 
 namespace {
-thread_local std::string rns_error;
+
+using cbw::require;
+
+struct RnsConfig {
+    std::uint32_t log_n = 12;
+    bool inverse = false;
+    bool negacyclic = true;
+    bool input_reversed = false;
+    bool output_reversed = true;
+    std::vector<cbw::NttDomain> domains;
+    std::vector<cbw::NttPolynomial> polynomials;
+};
+
+void allowed_fields(const cbw::json::Value& v, std::initializer_list<const char*> names, const char* what) {
+    require(v.is_object(), std::string("RNS JSON ") + what + " must be an object");
+    for (const auto& m : v.members)
+        require(std::find_if(names.begin(), names.end(), [&](const char* n) { return m.first == n; }) != names.end(),
+                std::string("unknown RNS JSON ") + what + " field: " + m.first);
 }
 
+bool order_value(const cbw::json::Value& v, const char* field) {
+    const auto& s = v.as_string(field);
+    if (s == "natural") return false;
+    if (s == "bit_reversed") return true;
+    throw std::invalid_argument("invalid RNS JSON enum: " + s);
+}
+
+// Schema of the reference (src/rns_tuning.cpp:124-150).
+RnsConfig parse_config(const std::string& text) {
+    const auto j = cbw::json::parse(text);
+    allowed_fields(j, {"schema_version", "log_n", "inverse", "ring", "input_order", "output_order", "domains",
+                       "polynomials"},
+                   "config");
+    require(j.at("schema_version").as_u64("schema_version") == 1, "unsupported RNS JSON schema_version");
+    RnsConfig c;
+    const auto log_n = j.at("log_n").as_u64("log_n");
+    require(log_n <= 0xffffffffull, "RNS JSON integer field overflows");
+    c.log_n = static_cast<std::uint32_t>(log_n);
+    c.inverse = j.at("inverse").as_bool("inverse");
+    const auto& ring = j.at("ring").as_string("ring");
+    if (ring == "cyclic") c.negacyclic = false;
+    else if (ring == "negacyclic") c.negacyclic = true;
+    else throw std::invalid_argument("invalid RNS JSON enum: " + ring);
+    c.input_reversed = order_value(j.at("input_order"), "input_order");
+    c.output_reversed = order_value(j.at("output_order"), "output_order");
+    const auto& domains = j.at("domains");
+    const auto& polys = j.at("polynomials");
+    require(domains.is_array() && polys.is_array(), "RNS domains and polynomials must be arrays");
+    for (const auto& d : domains.items) {
+        allowed_fields(d, {"modulus", "root"}, "domain");
+        c.domains.push_back({d.at("modulus").as_u64("modulus"), d.at("root").as_u64("root")});
+    }
+    for (const auto& p : polys.items) {
+        allowed_fields(p, {"domain", "input_offset", "output_offset"}, "polynomial");
+        const auto domain = p.at("domain").as_u64("domain");
+        require(domain <= 0xffffffffull, "RNS JSON integer field overflows");
+        c.polynomials.push_back({static_cast<std::uint32_t>(domain), p.at("input_offset").as_u64("input_offset"),
+                                 p.at("output_offset").as_u64("output_offset")});
+    }
+    return c;
+}
+
+std::string config_json(const RnsConfig& c) {
+    cbw::json::Writer w;
+    w.begin_object()
+        .field("schema_version", 1u)
+        .field("log_n", c.log_n)
+        .field("inverse", c.inverse)
+        .field("ring", c.negacyclic ? "negacyclic" : "cyclic")
+        .field("input_order", c.input_reversed ? "bit_reversed" : "natural")
+        .field("output_order", c.output_reversed ? "bit_reversed" : "natural");
+    w.begin_array("domains");
+    for (const auto& d : c.domains) w.begin_object().field("modulus", d.modulus).field("root", d.root).end_object();
+    w.end_array();
+    w.begin_array("polynomials");
+    for (const auto& p : c.polynomials)
+        w.begin_object()
+            .field("domain", p.domain)
+            .field("input_offset", p.input_offset)
+            .field("output_offset", p.output_offset)
+            .end_object();
+    w.end_array();
+    w.end_object();
+    return w.str();
+}
+
+// Validation rules of the reference plan constructor (src/rns_ntt.cu:259-300).
+void validate(const RnsConfig& c, std::uint64_t& input_extent, std::uint64_t& output_extent) {
+    require(c.log_n >= 12 && c.log_n <= 20 && !c.domains.empty() && !c.polynomials.empty(),
+            "RNS requires log_n in [12,20], domains and polynomials");
+    const std::uint64_t n = std::uint64_t{1} << c.log_n;
+    std::vector<std::pair<std::uint64_t, std::uint64_t>> outputs;
+    const std::uint64_t limit = (~std::uint64_t{0}) / sizeof(std::uint64_t) - n;
+    input_extent = output_extent = 0;
+    for (const auto& p : c.polynomials) {
+        require(p.domain < c.domains.size() && p.input_offset <= limit && p.output_offset <= limit,
+                "invalid RNS polynomial domain or extent");
+        input_extent = std::max(input_extent, p.input_offset + n);
+        output_extent = std::max(output_extent, p.output_offset + n);
+        outputs.emplace_back(p.output_offset, p.output_offset + n);
+    }
+    std::sort(outputs.begin(), outputs.end());
+    for (std::size_t i = 1; i < outputs.size(); ++i)
+        require(outputs[i].first >= outputs[i - 1].second, "overlapping RNS output intervals");
+    for (const auto& d : c.domains) {
+        const std::uint64_t q = d.modulus;
+        const std::uint64_t order = c.negacyclic ? 2 * n : n;
+        require(q >= 3 && q < (std::uint64_t{1} << 63) && cbw::is_prime_u64(q) && d.root != 0 && d.root < q &&
+                    (q - 1) % order == 0 && cbw::powmod(d.root, order, q) == 1 &&
+                    cbw::powmod(d.root, order / 2, q) == q - 1,
+                "RNS requires prime modulus <2^63 and an explicit primitive ring root");
+    }
+}
+
+std::string hex64(std::uint64_t v) {
+    std::ostringstream out;
+    out << std::hex << std::setfill('0') << std::setw(16) << v;
+    return out.str();
+}
+
+std::uint64_t fnv1a(const std::string& text) {
+    std::uint64_t h = 14695981039346656037ull;
+    for (unsigned char c : text) {
+        h ^= c;
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+// Write `contents` to `path` atomically: temporary file, fsync, rename.
+void atomic_write(const std::string& directory, const std::string& path, const std::string& contents) {
+    ::mkdir(directory.c_str(), 0775);  // existing directory is fine
+    std::string temp = path + ".tmp.XXXXXX";
+    const int fd = ::mkstemp(temp.data());
+    if (fd < 0) throw std::runtime_error("cannot create RNS cache temporary file: " + std::string(std::strerror(errno)));
+    const bool wrote = ::write(fd, contents.data(), contents.size()) == static_cast<ssize_t>(contents.size());
+    const bool synced = ::fsync(fd) == 0;
+    const bool closed = ::close(fd) == 0;
+    if (!wrote || !synced || !closed) {
+        std::remove(temp.c_str());
+        throw std::runtime_error("cannot write complete RNS cache record");
+    }
+    if (std::rename(temp.c_str(), path.c_str()) != 0) {
+        std::remove(temp.c_str());
+        throw std::runtime_error("cannot publish RNS cache record: " + std::string(std::strerror(errno)));
+    }
+}
+
+}  // namespace
+
+struct cubutterflyRnsPlanOpaque {
+    RnsConfig config;
+    std::unique_ptr<cbw::NttEngine> engine;
+    std::unique_ptr<cbw::NttEngine> to_scratch;  // one-pass in-place with moved offsets
+    cbw::DeviceBuffer scratch;
+    std::uint64_t input_extent = 0, output_extent = 0;
+    bool prepared = false, in_place = false, same_offsets = false;
+    int device = 0;
+    // Preparation record.
+    bool cache_hit = false;
+    std::string cache_key, source;
+    double kernel_ms = 0;
+
+    void run(const std::uint64_t* in, std::uint64_t* out, hipStream_t stream) {
+        if (engine->passes() == 1 && in == out && !same_offsets) {
+            // A one-pass tile would overwrite words another tile has not read:
+            // transform into the private scratch, then move each polynomial.
+            to_scratch->execute(in, scratch.as<std::uint64_t>(), nullptr, stream);
+            const std::uint64_t n = std::uint64_t{1} << config.log_n;
+            for (std::size_t p = 0; p < config.polynomials.size(); ++p)
+                cbw::hip_check(hipMemcpyAsync(out + config.polynomials[p].output_offset,
+                                              scratch.as<std::uint64_t>() + p * n, n * sizeof(std::uint64_t),
+                                              hipMemcpyDeviceToDevice, stream),
+                               "RNS scratch move");
+            return;
+        }
+        engine->execute(in, out, scratch.as<void>(), stream);
+    }
+};
+
+namespace {
+
+thread_local std::string rns_error;
+
+template <class F>
+int guarded(F&& body) noexcept {
+    try {
+        rns_error.clear();
+        body();
+        return 0;
+    } catch (const std::invalid_argument& e) {
+        try { rns_error = e.what(); } catch (...) {}
+        return 1;
+    } catch (const std::exception& e) {
+        try { rns_error = e.what(); } catch (...) {}
+        return 2;
+    } catch (...) {
+        try { rns_error = "unknown RNS failure"; } catch (...) {}
+        return 2;
+    }
+}
+
+std::string identity_json(const cubutterflyRnsPlanOpaque& plan, int placement, unsigned repetitions) {
+    hipDeviceProp_t props{};
+    cbw::hip_check(hipGetDeviceProperties(&props, plan.device), "hipGetDeviceProperties");
+    int runtime = 0;
+    (void)hipRuntimeGetVersion(&runtime);
+    cbw::json::Writer w;
+    w.begin_object().key("request").value_raw(config_json(plan.config));
+    w.field("placement", placement ? "in_place" : "separate");
+    w.key("hardware")
+        .begin_object()
+        .field("name", std::string(props.name))
+        .field("arch", std::string(props.gcnArchName))
+        .field("total_global_memory", std::uint64_t(props.totalGlobalMem))
+        .field("multiprocessor_count", props.multiProcessorCount)
+        .end_object();
+    w.key("runtime").begin_object().field("hip_runtime_version", runtime).end_object();
+    w.key("protocol").begin_object().field("name", "mi355x_static_plan_timing_v1").field("repetitions", repetitions).end_object();
+    w.end_object();
+    return w.str();
+}
+
+}  // namespace
+
 extern "C" {
+
 const char* cubutterflyRnsLastError(void) { return rns_error.c_str(); }
-int cubutterflyRnsCreate(const char*, cubutterflyRnsPlan* result) {
-    if (result) *result = nullptr;
-    rns_error = "RNS NTT is not yet lowered for gfx950";
-    return 2;
+
+int cubutterflyRnsCreate(const char* config_json_text, cubutterflyRnsPlan* result) {
+    return guarded([&] {
+        require(result != nullptr, "result must be non-null");
+        *result = nullptr;
+        require(config_json_text != nullptr, "config JSON must be non-null");
+        auto plan = std::make_unique<cubutterflyRnsPlanOpaque>();
+        plan->config = parse_config(config_json_text);
+        validate(plan->config, plan->input_extent, plan->output_extent);
+        cbw::hip_check(hipGetDevice(&plan->device), "hipGetDevice");
+        cbw::NttEngineConfig e;
+        e.word_bits = 64;
+        e.log_n = plan->config.log_n;
+        e.negacyclic = plan->config.negacyclic;
+        e.inverse = plan->config.inverse;
+        e.input_bit_reversed = plan->config.input_reversed;
+        e.output_bit_reversed = plan->config.output_reversed;
+        e.reduce_input = false;  // canonical residues are the input contract
+        e.domains = plan->config.domains;
+        e.polynomials = plan->config.polynomials;
+        plan->engine = std::make_unique<cbw::NttEngine>(e);
+        plan->same_offsets = std::all_of(plan->config.polynomials.begin(), plan->config.polynomials.end(),
+                                         [](const cbw::NttPolynomial& p) { return p.input_offset == p.output_offset; });
+        const std::uint64_t n = std::uint64_t{1} << plan->config.log_n;
+        std::size_t scratch_bytes = plan->engine->workspace_bytes();
+        if (plan->engine->passes() == 1 && !plan->same_offsets) {
+            auto dense = e;
+            for (std::size_t p = 0; p < dense.polynomials.size(); ++p) dense.polynomials[p].output_offset = p * n;
+            plan->to_scratch = std::make_unique<cbw::NttEngine>(dense);
+            scratch_bytes = plan->config.polynomials.size() * n * sizeof(std::uint64_t);
+        }
+        plan->scratch.allocate(scratch_bytes);  // private, outside timing (reference :286-366)
+        *result = plan.release();
+    });
 }
-int cubutterflyRnsPrepare(cubutterflyRnsPlan, int, const char*, int, unsigned, void*) {
-    rns_error = "plan must be created";
-    return 1;
+
+int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* cache_directory, int policy,
+                          unsigned repetitions, void* stream_handle) {
+    return guarded([&] {
+        require(plan != nullptr, "plan must be non-null");
+        require(!plan->prepared, "plan is already prepared; create another plan to retune");
+        require(placement == 0 || placement == 1, "invalid placement");
+        require(policy >= 0 && policy <= 2, "invalid cache policy");
+        require(repetitions > 0, "repetitions must be positive");
+        const auto stream = static_cast<hipStream_t>(stream_handle);
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        cbw::hip_check(hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
+        require(capture == hipStreamCaptureStatusNone, "RNS preparation must run outside graph capture");
+        const std::string directory = cache_directory ? cache_directory : "";
+        require(!(directory.empty() && policy == 1), "RNS Require policy needs a nonempty cache_directory");
+        const std::string identity = identity_json(*plan, placement, repetitions);
+        const std::string key = "rns-v1-" + hex64(fnv1a(identity));
+        const std::string path = directory + "/" + key + ".json";
+        plan->cache_key = key;
+        if (!directory.empty() && policy != 2 && ::access(path.c_str(), F_OK) == 0) {
+            std::ifstream input(path);
+            std::stringstream buffer;
+            buffer << input.rdbuf();
+            if (!input && !input.eof()) throw std::runtime_error("cannot read RNS cache record: " + path);
+            const auto record = cbw::json::parse(buffer.str());
+            require(record.at("schema_version").as_u64("schema_version") == 1, "unsupported RNS JSON schema_version");
+            // Compare the complete identity: a file-name collision cannot
+            // authorise another request's record.
+            const auto& stored = record.at("identity");
+            const auto reparsed = cbw::json::parse(identity);
+            auto same = [](const cbw::json::Value& a, const cbw::json::Value& b, auto&& self) -> bool {
+                if (a.kind != b.kind) return false;
+                switch (a.kind) {
+                    case cbw::json::Value::Kind::Null: return true;
+                    case cbw::json::Value::Kind::Bool: return a.boolean == b.boolean;
+                    case cbw::json::Value::Kind::Number: return a.text == b.text;
+                    case cbw::json::Value::Kind::String: return a.text == b.text;
+                    case cbw::json::Value::Kind::Array:
+                        if (a.items.size() != b.items.size()) return false;
+                        for (std::size_t i = 0; i < a.items.size(); ++i)
+                            if (!self(a.items[i], b.items[i], self)) return false;
+                        return true;
+                    case cbw::json::Value::Kind::Object:
+                        if (a.members.size() != b.members.size()) return false;
+                        for (const auto& m : a.members) {
+                            const auto* other = b.find(m.first);
+                            if (!other || !self(m.second, *other, self)) return false;
+                        }
+                        return true;
+                }
+                return false;
+            };
+            if (!same(stored, reparsed, same))
+                throw std::runtime_error("RNS cache identity mismatch (incompatible record or hash collision): " + path);
+            require(record.at("source").as_string("source") == "static_plan_timing",
+                    "unsupported RNS cache measurement provenance");
+            plan->kernel_ms = record.at("kernel_ms").as_double("kernel_ms");
+            require(plan->kernel_ms > 0, "invalid RNS cache kernel_ms");
+            plan->cache_hit = true;
+            plan->source = "prepared_cache_timing_only";
+        } else {
+            if (policy == 1) throw std::runtime_error("required RNS prepared cache record is missing: " + path);
+            // Time the static plan on private zero-filled buffers.
+            const std::uint64_t words = std::max(plan->input_extent, plan->output_extent);
+            cbw::DeviceBuffer in(words * 8), out(words * 8);
+            cbw::hip_check(hipMemsetAsync(in.as<void>(), 0, words * 8, stream), "RNS prepare fill");
+            std::uint64_t* target = placement ? in.as<std::uint64_t>() : out.as<std::uint64_t>();
+            hipEvent_t start, stop;
+            cbw::hip_check(hipEventCreate(&start), "hipEventCreate");
+            cbw::hip_check(hipEventCreate(&stop), "hipEventCreate");
+            plan->run(in.as<std::uint64_t>(), target, stream);  // warm
+            cbw::hip_check(hipEventRecord(start, stream), "hipEventRecord");
+            for (unsigned r = 0; r < repetitions; ++r) plan->run(in.as<std::uint64_t>(), target, stream);
+            cbw::hip_check(hipEventRecord(stop, stream), "hipEventRecord");
+            cbw::hip_check(hipEventSynchronize(stop), "hipEventSynchronize");
+            float ms = 0;
+            cbw::hip_check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+            (void)hipEventDestroy(start);
+            (void)hipEventDestroy(stop);
+            plan->kernel_ms = std::max(1e-6, double(ms) / repetitions);
+            plan->source = directory.empty() ? "uncached_static_plan_timing" : "static_plan_timing";
+            if (!directory.empty()) {
+                cbw::json::Writer w;
+                w.begin_object()
+                    .field("schema_version", 1u)
+                    .key("identity")
+                    .value_raw(identity)
+                    .key("mapping")
+                    .value_raw(plan->engine->mapping_json())
+                    .field("kernel_ms", plan->kernel_ms)
+                    .field("source", "static_plan_timing")
+                    .field("validation", "timing_only_not_mathematically_validated")
+                    .end_object();
+                atomic_write(directory, path, w.str() + "\n");
+            }
+        }
+        plan->in_place = placement == 1;
+        plan->prepared = true;
+    });
 }
-int cubutterflyRnsExecute(cubutterflyRnsPlan, const uint64_t*, uint64_t*, void*) {
-    rns_error = "plan must be prepared";
-    return 1;
+
+int cubutterflyRnsExecute(cubutterflyRnsPlan plan, const uint64_t* input, uint64_t* output, void* stream) {
+    return guarded([&] {
+        require(plan != nullptr && plan->prepared, "plan must be prepared");
+        require(input != nullptr && output != nullptr, "device pointers must be non-null");
+        require(reinterpret_cast<std::uintptr_t>(input) % alignof(std::uint64_t) == 0 &&
+                    reinterpret_cast<std::uintptr_t>(output) % alignof(std::uint64_t) == 0,
+                "device pointers must be uint64 aligned");
+        require((input == output) == plan->in_place, "pointer aliasing does not match prepared placement");
+        int device = -1;
+        cbw::hip_check(hipGetDevice(&device), "hipGetDevice");
+        require(device == plan->device, "RNS plan used on a different device");
+        plan->run(input, output, static_cast<hipStream_t>(stream));
+    });
 }
-int cubutterflyRnsInfoJson(cubutterflyRnsPlan, char*, size_t*) {
-    rns_error = "plan must be non-null";
-    return 1;
+
+int cubutterflyRnsInfoJson(cubutterflyRnsPlan plan, char* buffer, size_t* bytes) {
+    return guarded([&] {
+        require(plan != nullptr && bytes != nullptr, "plan and bytes must be non-null");
+        cbw::json::Writer w;
+        w.begin_object()
+            .field("prepared", plan->prepared)
+            .field("workspace_bytes", std::uint64_t(plan->scratch.bytes()))
+            .key("request")
+            .value_raw(config_json(plan->config))
+            .key("mapping")
+            .value_raw(plan->engine->mapping_json())
+            .field("placement", plan->in_place ? "in_place" : "separate")
+            .field("cache_hit", plan->cache_hit)
+            .field("cache_key", plan->cache_key)
+            .field("source", plan->source)
+            .field("kernel_ms", plan->kernel_ms)
+            .end_object();
+        const std::string text = w.str();
+        const std::size_t capacity = *bytes;
+        *bytes = text.size() + 1;
+        if (!buffer) return;
+        require(capacity >= *bytes, "info JSON buffer is too small");
+        std::memcpy(buffer, text.c_str(), *bytes);
+    });
 }
-int cubutterflyRnsDestroy(cubutterflyRnsPlan) { return 0; }
+
+int cubutterflyRnsDestroy(cubutterflyRnsPlan plan) {
+    return guarded([&] { delete plan; });
 }
+
+}  // extern "C"

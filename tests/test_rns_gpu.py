@@ -1,0 +1,181 @@
+"""RNS NTT parity on the GPU through the RNS C ABI, bit-exact against the oracle.
+
+C4 at full size (32 limbs of 60-bit primes, n = 2^16, forward natural ->
+bit-reversed, inverse bit-reversed -> natural), and the reference's own
+regression layout (tests/test_rns_ntt.cu:113-162): two domains with explicit
+roots primitive^3 / primitive^5, five polynomials in permuted slots of
+n + 17 words at offset 11, sentinel words around every slot, both placements
+and all four order combinations, plus graph replay and the prepared-cache
+contract.
+"""
+import json
+
+import numpy as np
+import pytest
+
+import oracle
+from cubutterfly_amd import rns, workloads
+from gpu_util import to_device, to_host
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = np.uint64(0xFEDCBA9876543210)
+PRIMES = [1152921504577486849, 576460756061519873]  # tests/test_rns_ntt.cu:19
+
+
+@pytest.fixture(scope="module")
+def rlib():
+    return rns.Library()
+
+
+def bitrev_perm(log_n):
+    idx = np.arange(1 << log_n)
+    rev = np.zeros_like(idx)
+    for b in range(log_n):
+        rev |= ((idx >> b) & 1) << (log_n - 1 - b)
+    return rev
+
+
+def run(torch, rlib, cfg, host_in, out_words, placement, stream_obj):
+    stream = stream_obj.cuda_stream
+    x = to_device(torch, host_in)
+    y = x if placement == rns.Placement.IN_PLACE else to_device(torch, np.full(out_words, SENTINEL))
+    with rns.Plan(rlib, cfg) as plan:
+        plan.prepare(placement=placement, stream=stream)
+        plan.execute(x, y, stream=stream)
+        torch.cuda.synchronize()
+        info = plan.info()
+    return to_host(torch, y, np.uint64), info
+
+
+def test_c4_full_size_round_trip(torch_gpu, rlib):
+    print("case C4 rns 32 limbs x 2^16", flush=True)
+    log_n, n = 16, 1 << 16
+    moduli = workloads.c4_moduli()
+    roots = [oracle.find_primitive_root(log_n + 1, q) for q in moduli]
+    x = np.stack([workloads.ntt_input(log_n, 1, q, seed=1, channel=i)[0] for i, q in enumerate(moduli)])
+    stream = torch_gpu.cuda.Stream()
+    fwd_cfg = rns.config(log_n, list(zip(moduli, roots)))
+    got, info = run(torch_gpu, rlib, fwd_cfg, x.ravel(), x.size, rns.Placement.SEPARATE, stream)
+    expected = oracle.rns(x, moduli, roots, output_bit_reversed=True, threads=oracle.default_threads())
+    np.testing.assert_array_equal(got.reshape(32, n), expected)
+    assert info["prepared"] and info["placement"] == "separate"
+    inv_cfg = rns.config(log_n, list(zip(moduli, roots)), inverse=True)
+    back, _ = run(torch_gpu, rlib, inv_cfg, got, x.size, rns.Placement.IN_PLACE, stream)
+    np.testing.assert_array_equal(back.reshape(32, n), x)
+
+
+def reference_layout(log_n, negacyclic, inverse, in_rev, out_rev):
+    """Config and input of tests/test_rns_ntt.cu:113-162."""
+    n = 1 << log_n
+    root_bits = log_n + (1 if negacyclic else 0)
+    domains = []
+    for d, q in enumerate(PRIMES):
+        root = pow(oracle.find_primitive_root(root_bits, q), 3 if d == 0 else 5, q)
+        domains.append((q, root))
+    slots = [(1, 3, 5), (0, 0, 2), (0, 6, 0), (1, 2, 6), (0, 5, 3)]  # (domain, input slot, output slot)
+    polys = [{"domain": d, "input_offset": i * (n + 17) + 11, "output_offset": o * (n + 17) + 11}
+             for d, i, o in slots]
+    cfg = rns.config(log_n, domains, polys, inverse=inverse, ring="negacyclic" if negacyclic else "cyclic",
+                     input_order="bit_reversed" if in_rev else "natural",
+                     output_order="bit_reversed" if out_rev else "natural")
+    words = 7 * (n + 17) + 29
+    data = np.full(words, SENTINEL)
+    rng = np.random.default_rng(log_n * 7 + int(inverse))
+    for p in polys:
+        q = domains[p["domain"]][0]
+        row = rng.integers(0, q, n, dtype=np.uint64)
+        row[:3] = [0, q - 1, q // 2]
+        data[p["input_offset"]:p["input_offset"] + n] = row
+    return cfg, domains, polys, data
+
+
+def expected_layout(cfg, domains, polys, data, in_place):
+    n = 1 << cfg["log_n"]
+    out = data.copy() if in_place else np.full(data.size, SENTINEL)
+    perm = bitrev_perm(cfg["log_n"])
+    for p in polys:
+        q, root = domains[p["domain"]]
+        phys = data[p["input_offset"]:p["input_offset"] + n]
+        y = oracle.rns(phys[None], [q], [root], negacyclic=cfg["ring"] == "negacyclic", inverse=cfg["inverse"],
+                       input_bit_reversed=cfg["input_order"] == "bit_reversed",
+                       output_bit_reversed=cfg["output_order"] == "bit_reversed")[0]
+        out[p["output_offset"]:p["output_offset"] + n] = y
+    return out
+
+
+@pytest.mark.parametrize("log_n", [12, 14, 16])
+@pytest.mark.parametrize("negacyclic", [True, False])
+@pytest.mark.parametrize("inverse", [False, True])
+@pytest.mark.parametrize("in_rev,out_rev", [(False, True), (True, False), (False, False), (True, True)])
+@pytest.mark.parametrize("placement", [rns.Placement.SEPARATE, rns.Placement.IN_PLACE])
+def test_reference_layout(torch_gpu, rlib, log_n, negacyclic, inverse, in_rev, out_rev, placement):
+    print(f"case rns layout log_n={log_n} neg={negacyclic} inv={inverse} in_rev={in_rev} "
+          f"out_rev={out_rev} placement={int(placement)}", flush=True)
+    cfg, domains, polys, data = reference_layout(log_n, negacyclic, inverse, in_rev, out_rev)
+    in_place = placement == rns.Placement.IN_PLACE
+    got, _ = run(torch_gpu, rlib, cfg, data, data.size, placement, torch_gpu.cuda.Stream())
+    np.testing.assert_array_equal(got, expected_layout(cfg, domains, polys, data, in_place))
+
+
+def test_graph_replay_matches_eager(torch_gpu, rlib):
+    # Captured executions replayed several times, with eager work between
+    # replays, must equal the eager result every time.
+    cfg, domains, polys, data = reference_layout(14, True, False, False, True)
+    stream = torch_gpu.cuda.Stream()
+    x = to_device(torch_gpu, data)
+    y = to_device(torch_gpu, np.full(data.size, SENTINEL))
+    blank = y.clone()
+    expected = expected_layout(cfg, domains, polys, data, False)
+    with rns.Plan(rlib, cfg) as plan:
+        plan.prepare(stream=stream.cuda_stream)
+        graph = torch_gpu.cuda.CUDAGraph()
+        with torch_gpu.cuda.graph(graph, stream=stream):
+            plan.execute(x, y, stream=stream.cuda_stream)
+        for _ in range(3):
+            y.copy_(blank)  # eager work between replays
+            torch_gpu.cuda.synchronize()
+            with torch_gpu.cuda.stream(stream):
+                graph.replay()
+            torch_gpu.cuda.synchronize()
+            np.testing.assert_array_equal(to_host(torch_gpu, y, np.uint64), expected)
+
+
+def test_prepare_cache_contract(torch_gpu, rlib, tmp_path):
+    cfg, _, _, _ = reference_layout(12, True, False, False, True)
+    stream = torch_gpu.cuda.Stream().cuda_stream
+    with rns.Plan(rlib, cfg) as plan:
+        with pytest.raises(rns.Error):  # REQUIRE without a record
+            plan.prepare(cache_directory=str(tmp_path), policy=rns.CachePolicy.REQUIRE, stream=stream)
+    with rns.Plan(rlib, cfg) as plan:
+        plan.prepare(cache_directory=str(tmp_path), policy=rns.CachePolicy.PREFER, stream=stream)
+        first = plan.info()
+        assert not first["cache_hit"] and first["kernel_ms"] > 0
+        with pytest.raises(rns.Error):
+            plan.prepare(stream=stream)  # already prepared
+    records = list(tmp_path.glob("rns-v1-*.json"))
+    assert len(records) == 1 and records[0].stem == first["cache_key"]
+    with rns.Plan(rlib, cfg) as plan:
+        plan.prepare(cache_directory=str(tmp_path), policy=rns.CachePolicy.REQUIRE, stream=stream)
+        hit = plan.info()
+        assert hit["cache_hit"] and hit["kernel_ms"] == first["kernel_ms"]
+    # A record whose identity differs is refused, not replayed.
+    record = json.loads(records[0].read_text())
+    record["identity"]["placement"] = "in_place"
+    records[0].write_text(json.dumps(record))
+    with rns.Plan(rlib, cfg) as plan:
+        with pytest.raises(rns.Error) as info:
+            plan.prepare(cache_directory=str(tmp_path), policy=rns.CachePolicy.PREFER, stream=stream)
+        assert "identity" in str(info.value)
+
+
+def test_execute_contract(torch_gpu, rlib):
+    cfg, _, _, data = reference_layout(12, True, False, False, True)
+    x = to_device(torch_gpu, data)
+    y = to_device(torch_gpu, data)
+    with rns.Plan(rlib, cfg) as plan:
+        with pytest.raises(rns.Error):
+            plan.execute(x, y)  # not prepared
+        plan.prepare(placement=rns.Placement.SEPARATE)
+        with pytest.raises(ValueError):
+            plan.execute(x, x)  # aliasing differs from the prepared placement
