@@ -237,6 +237,110 @@ class RnsNegacyclic(Workload):
                                                 "the reference RNS oracle (tests/test_rns_ntt.cu:62-111)")
 
 
+class OnePlan(Workload):
+    """A configuration served by one plan: host input -> rotated device sets."""
+
+    elem_bytes = 0
+
+    def transform(self, cb):
+        raise NotImplementedError
+
+    def make_host(self):
+        raise NotImplementedError
+
+    def setup(self, torch, lib, stream):
+        import cubutterfly_amd as cb
+        self.plans = [cb.Plan(lib, self.transform(cb), stream=stream)]
+        ws_bytes = self.plans[0].workspace_size()
+        if ws_bytes:
+            self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+            self.plans[0].set_workspace(self.workspace, ws_bytes)
+        self.host = self.make_host()
+        src = _np_to_torch(torch, self.host).to("cuda")
+        sets = self._rotation(torch, self.bytes_per_call)
+        self.inputs = [src.clone() for _ in range(sets)]
+        self.outputs = [torch.empty_like(src) for _ in range(sets)]
+
+    def call(self, index):
+        k = index % len(self.inputs)
+        self.plans[0].execute(self.inputs[k], self.outputs[k])
+
+    def timed_cpu(self, fn, what):
+        reps, elapsed = 0, 0.0
+        while elapsed < 10.0:
+            t0 = time.perf_counter()
+            fn()
+            elapsed += time.perf_counter() - t0
+            reps += 1
+        return elapsed, reps * self.transforms_per_call, f"{reps} full batches ({what})"
+
+
+class FftC64(OnePlan):
+    """C3: complex64 FFT forward, 1 x 2^24 (c3a) or 1024 x 2^14 (c3b)."""
+    dtype = "c64"
+
+    def __init__(self, log_n, batch):
+        self.log_n, self.batch = log_n, batch
+        self.name = "c3a" if batch == 1 else "c3b"
+        self.description = f"complex FFT c64 forward, batch {batch} x n=2^{log_n}, N(0,1) real and imaginary parts"
+        self.transforms_per_call = batch
+        self.bytes_per_call = 2 * batch * (8 << log_n)
+
+    def transform(self, cb):
+        return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
+                            extents=[1 << self.log_n], batch=self.batch)
+
+    def make_host(self):
+        from cubutterfly_amd import workloads
+        return workloads.complex_input(self.log_n, self.batch, seed=3).reshape(self.batch, 1 << self.log_n)
+
+    def verify(self, torch):
+        got = self.outputs[0].cpu().numpy().astype(np.complex128)
+        ref = np.fft.fft(self.host.astype(np.complex128), axis=-1)
+        err = np.linalg.norm(got - ref, axis=-1) / np.linalg.norm(ref, axis=-1)
+        return bool(np.max(err) <= 1e-5)
+
+    def cpu_sample(self, threads):
+        import oracle
+        return self.timed_cpu(lambda: oracle.fft_c64(self.host, threads=threads),
+                              f"{self.batch} x 2^{self.log_n} through reference_fft, iterative radix-2")
+
+
+class FwhtFp16(OnePlan):
+    """C5: QuaRot-style FP16 FWHT, scale 1/sqrt(n), FP32 compute, one final
+    FP16 rounding: 16384 x 4096 (c5a) or 524288 x 128 (c5b)."""
+    dtype = "f16"
+
+    def __init__(self, rows, n):
+        self.rows, self.n = rows, n
+        self.name = "c5a" if n == 4096 else "c5b"
+        self.description = (f"FWHT fp16 storage / fp32 compute, {rows} x n={n}, output scale 1/sqrt(n), "
+                            "final-storage rounding, activations with outlier channels")
+        self.transforms_per_call = rows
+        self.bytes_per_call = 2 * rows * n * 2
+        self.scale = float(np.float32(1.0 / np.sqrt(n)))
+
+    def transform(self, cb):
+        return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
+                            extents=[self.n], batch=self.rows, output_scale=self.scale,
+                            output_rounding=cb.OutputRounding.FINAL_STORAGE)
+
+    def make_host(self):
+        from cubutterfly_amd import workloads
+        return workloads.quarot_input(self.rows, self.n, seed=5)
+
+    def verify(self, torch):
+        import oracle
+        got = self.outputs[0].cpu().numpy().view(np.float16).astype(np.float32)
+        ref = oracle.fwht_f16_final(self.host, self.scale, threads=oracle.default_threads()).astype(np.float32)
+        return bool(np.max(np.abs(got - ref)) <= 2e-3)
+
+    def cpu_sample(self, threads):
+        import oracle
+        return self.timed_cpu(lambda: oracle.fwht_f16_final(self.host, self.scale, threads=threads),
+                              f"{self.rows} x {self.n} through reference_fwht in fp32 + one fp16 rounding")
+
+
 class DeviceCopy(Workload):
     """Calibration probe, not a BASELINE config: a plain device-to-device copy
     of 128 MiB, the known-size reference for rocprofv3 FETCH_SIZE/WRITE_SIZE."""
@@ -262,7 +366,9 @@ class DeviceCopy(Workload):
         return 1.0, 0, "no CPU baseline for the calibration copy"
 
 
-WORKLOADS = {"c1": FwhtFp32, "c2": NttNegacyclic, "c4": RnsNegacyclic, "copy": DeviceCopy}
+WORKLOADS = {"c1": FwhtFp32, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1), "c3b": lambda: FftC64(14, 1024),
+             "c4": RnsNegacyclic, "c5a": lambda: FwhtFp16(16384, 4096), "c5b": lambda: FwhtFp16(524288, 128),
+             "copy": DeviceCopy}
 DEFAULT_WORKLOAD = "c2"
 
 

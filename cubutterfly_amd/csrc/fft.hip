@@ -1,10 +1,479 @@
-// Complex FFT kernels for gfx950 (lowering added in a later milestone).
+// Complex FFT (COMPLEX_FP32, natural order in and out) for gfx950.
+//
+// Decimation in frequency over 4-bit digits, top digit first. A workgroup
+// holds a tile of 2^LB complex values = 2^LT transform points x 2^LI lines,
+// 16 per thread. For each digit: an in-register radix-2^r DIF codelet with
+// compile-time twiddles (r = 4, the last digit r = 1..4), then every element
+// is multiplied by w_{2^h}^(j_low * c): j_low = the element's index bits below
+// the digit, c = its digit output, h = the digit's top bit + 1 (the four-step
+// twiddle of that level). LDS exchanges regroup the data between digits. The
+// result lands in bit-reversed position (digit reversal with each digit
+// bit-reversed), so the final pass stores through an LDS-staged
+// bit-reversal; two-pass lengths also transpose the 2^l1 x 2^l2 grid there.
+//
+// Level twiddles come from two 4096-entry tables (w^f = A[f >> 12] B[f & 4095],
+// entries rounded from double), so lengths up to 2^24 need 64 KB of tables.
+// Lengths <= 2^14 run in one pass; up to 2^24 in two.
 #include <hip/hip_runtime.h>
 
+#include "json.hpp"
 #include "planner.hpp"
 
+#include <algorithm>
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <tuple>
+
 namespace cbw {
-std::unique_ptr<Executor> make_fft_executor(const Request&) {
-    throw NotSupported("complex FFT is not yet lowered for gfx950");
+namespace {
+
+constexpr int kLE = 4;
+constexpr int kE = 16;
+
+struct FftArgs {
+    const float2* in;
+    float2* out;
+    const float2* twa;  // w^(4096 k), k < 4096
+    const float2* twb;  // w^k, k < 4096
+    std::uint32_t l1, l2;  // high / low index bits (l1 = 0: one pass)
+    std::uint32_t rows, tiles;
+    float scale;  // 1/n for the normalised inverse on the final store, else 1
+};
+
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+    return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
 }
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ std::uint32_t brev(std::uint32_t x, std::uint32_t bits) {
+    return bits ? __brev(x) >> (32 - bits) : 0u;
+}
+
+template <int S>
+__device__ __forceinline__ std::uint32_t phase_index(std::uint32_t t, std::uint32_t r) {
+    return (t & ((1u << S) - 1u)) | (r << S) | ((t >> S) << (S + kLE));
+}
+
+// cos / sin of 2 pi j / 16 for j = 0..15 (exact decimal expansions).
+constexpr double kCos16[16] = {1.0, 0.92387953251128676, 0.70710678118654752, 0.38268343236508977,
+                               0.0, -0.38268343236508977, -0.70710678118654752, -0.92387953251128676,
+                               -1.0, -0.92387953251128676, -0.70710678118654752, -0.38268343236508977,
+                               0.0, 0.38268343236508977, 0.70710678118654752, 0.92387953251128676};
+
+// x * w_len^j with w = exp(-+2 pi i / len) (forward / inverse), constants folded.
+template <int LEN, int J, bool INV>
+__device__ __forceinline__ float2 twiddle_const(float2 x) {
+    constexpr int e = (J * (16 / LEN)) & 15;  // angle index in sixteenths of a turn
+    if constexpr (e == 0) {
+        return x;
+    } else if constexpr (e == 4) {  // -i (forward) / +i (inverse)
+        return INV ? make_float2(-x.y, x.x) : make_float2(x.y, -x.x);
+    } else if constexpr (e == 8) {
+        return make_float2(-x.x, -x.y);
+    } else if constexpr (e == 12) {
+        return INV ? make_float2(x.y, -x.x) : make_float2(-x.y, x.x);
+    } else {
+        constexpr float c = float(kCos16[e]);
+        constexpr float s = float(INV ? kCos16[(e + 12) & 15] : -kCos16[(e + 12) & 15]);  // +-sin
+        return make_float2(x.x * c - x.y * s, x.x * s + x.y * c);
+    }
+}
+
+// Radix-2^DS DIF on register bits [0, DS) of each 2^DS group (bit-reversed out).
+template <int DS, bool INV>
+__device__ __forceinline__ void codelet(float2 (&v)[kE]) {
+#pragma unroll
+    for (int b = DS - 1; b >= 0; --b) {
+        const int half = 1 << b;
+#pragma unroll
+        for (int r = 0; r < kE; ++r) {
+            if (r & half) continue;
+            const float2 u = v[r], w = v[r + half];
+            v[r] = make_float2(u.x + w.x, u.y + w.y);
+            const float2 d = make_float2(u.x - w.x, u.y - w.y);
+            // twiddle w_{2 half}^(r mod half)
+            const int j = r & (half - 1);
+            float2 t = d;
+            switch (half) {
+                case 1: break;
+                case 2:
+                    if (j == 1) t = twiddle_const<4, 1, INV>(d);
+                    break;
+                case 4:
+                    if (j == 1) t = twiddle_const<8, 1, INV>(d);
+                    else if (j == 2) t = twiddle_const<8, 2, INV>(d);
+                    else if (j == 3) t = twiddle_const<8, 3, INV>(d);
+                    break;
+                default:
+                    switch (j) {
+                        case 1: t = twiddle_const<16, 1, INV>(d); break;
+                        case 2: t = twiddle_const<16, 2, INV>(d); break;
+                        case 3: t = twiddle_const<16, 3, INV>(d); break;
+                        case 4: t = twiddle_const<16, 4, INV>(d); break;
+                        case 5: t = twiddle_const<16, 5, INV>(d); break;
+                        case 6: t = twiddle_const<16, 6, INV>(d); break;
+                        case 7: t = twiddle_const<16, 7, INV>(d); break;
+                        default: break;
+                    }
+            }
+            v[r + half] = t;
+        }
+    }
+}
+
+// Padded LDS image (8-byte complex words), as in the NTT tiles.
+template <bool COL, int LT, int LI>
+struct FftLds {
+    static constexpr std::uint32_t kWords =
+        COL ? (1u << LT) * ((1u << LI) + 1u) : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
+    static __device__ __forceinline__ std::uint32_t addr(std::uint32_t i) {
+        if constexpr (COL) {
+            const std::uint32_t cc = i & ((1u << LI) - 1u), x = i >> LI;
+            return x * ((1u << LI) + 1u) + (cc ^ ((x >> 3) & ((1u << LI) - 1u)));
+        } else {
+            const std::uint32_t x = i & ((1u << LT) - 1u), rr = i >> LT;
+            return rr * ((1u << LT) + (1u << LT >> 4) + 1u) + x + (x >> 4);
+        }
+    }
+};
+
+// One FFT pass over LT transform bits. COL: high bits, tile of 2^LI columns;
+// ROW: low bits, tile of 2^LI rows (the final pass, storing in natural order).
+template <int LT, int LI, bool COL, bool INV>
+struct FftPass {
+    static constexpr int LB = LT + LI;
+    static constexpr std::uint32_t T = 1u << (LB - kLE);
+    static constexpr int kPhases = (LT + kLE - 1) / kLE;
+    using L = FftLds<COL, LT, LI>;
+
+    template <int P>
+    static constexpr int window() {  // transform-relative register window start
+        return LT - kLE * (P + 1) > 0 ? LT - kLE * (P + 1) : 0;
+    }
+    template <int P>
+    static constexpr int digit_bits() {
+        return LT - kLE * P < kLE ? LT - kLE * P : kLE;
+    }
+    template <int P>
+    static constexpr int tile_window() {
+        return (COL ? LI : 0) + window<P>();
+    }
+
+    // Digit P: codelet, then the level twiddle unless it is the very last digit.
+    template <int P>
+    static __device__ __forceinline__ void digit(float2 (&v)[kE], const FftArgs& a, std::uint32_t t,
+                                                 std::uint32_t c0, std::uint32_t m) {
+        constexpr int ws = window<P>(), ds = digit_bits<P>();
+        codelet<ds, INV>(v);
+        const std::uint32_t lo_rel = std::uint32_t(ws);  // digit's lowest transform bit
+        const std::uint32_t lo = COL ? a.l2 + lo_rel : lo_rel;  // global bit
+        if (lo == 0) return;  // last digit of the whole transform: no level twiddle
+        const std::uint32_t h = lo + ds;
+        const std::uint32_t i0 = phase_index<tile_window<P>()>(t, 0);
+        // Index bits below the digit: for columns, the column and the low
+        // transform bits; for rows, the low transform bits.
+        std::uint32_t x0 = COL ? (i0 >> LI) : (i0 & ((1u << LT) - 1u));
+        std::uint32_t jl = x0 & ((1u << lo_rel) - 1u);
+        if (COL) jl = (jl << a.l2) | (c0 + (i0 & ((1u << LI) - 1u)));
+#pragma unroll
+        for (int r = 0; r < kE; ++r) {
+            // register r holds digit output c = bitrev(r's digit bits); bits of r
+            // above the digit (only in a short last digit) are earlier digits.
+            const std::uint32_t c = brev(std::uint32_t(r) & ((1u << ds) - 1u), ds);
+            if (c == 0) continue;
+            const std::uint32_t f = (jl * c) << (m - h);
+            const float2 w = cmul(a.twa[f >> 12], a.twb[f & 4095u]);
+            v[r] = cmul(v[r], w);
+        }
+    }
+
+    template <int FROM, int TO>
+    static __device__ __forceinline__ void exchange(float2 (&v)[kE], float2* lds, std::uint32_t t) {
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < kE; ++r) lds[L::addr(phase_index<FROM>(t, r))] = v[r];
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<TO>(t, r))];
+    }
+
+    static __device__ void run(const FftArgs& a) {
+        extern __shared__ float2 lds[];
+        const std::uint32_t t = threadIdx.x;
+        const std::uint32_t m = a.l1 + a.l2;
+        const std::uint32_t b = blockIdx.x;
+        // XCD-contiguous tile order (tiles sharing cache lines meet in one L2).
+        const std::uint32_t tile = (a.tiles & 7u) == 0 && (gridDim.x & 7u) == 0
+                                       ? (b & 7u) * (a.tiles >> 3) + (b >> 3)
+                                       : b;
+        std::uint32_t row0 = 0, c0 = 0;
+        std::uint64_t base = 0;  // element offset of the tile's transform
+        const bool single = a.l1 == 0;
+        if constexpr (COL) {
+            const std::uint32_t shift = a.l2 - LI;
+            const std::uint32_t poly = tile >> shift;
+            c0 = (tile & ((1u << shift) - 1u)) << LI;
+            base = std::uint64_t(poly) << m;
+        } else {
+            row0 = tile << LI;  // global row (= transform for one pass)
+        }
+        float2 v[kE];
+        constexpr int w0 = tile_window<0>();
+#pragma unroll
+        for (int r = 0; r < kE; ++r) {
+            const std::uint32_t i = phase_index<w0>(t, r);
+            std::uint64_t where;
+            bool ok = true;
+            if constexpr (COL) {
+                where = base + c0 + (i & ((1u << LI) - 1u)) + (std::uint64_t(i >> LI) << a.l2);
+            } else if (single) {
+                const std::uint32_t g = row0 + (i >> LT);
+                ok = g < a.rows;
+                where = (std::uint64_t(g) << a.l2) + (i & ((1u << LT) - 1u));
+            } else {  // rows bitrev(k0 + rr) of one transform, matching the transposing store
+                const std::uint32_t per = a.l1 - LI;
+                const std::uint32_t poly = (row0 >> LI) >> per;
+                const std::uint32_t k0 = row0 & ((1u << a.l1) - 1u);
+                const std::uint32_t row = brev(k0 + (i >> LT), a.l1);
+                where = (std::uint64_t(poly) << m) + (std::uint64_t(row) << a.l2) + (i & ((1u << LT) - 1u));
+            }
+            v[r] = ok ? a.in[where] : make_float2(0.f, 0.f);
+        }
+        digit<0>(v, a, t, c0, m);
+        if constexpr (kPhases > 1) {
+            exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
+            digit<1>(v, a, t, c0, m);
+        }
+        if constexpr (kPhases > 2) {
+            exchange<tile_window<1>(), tile_window<2>()>(v, lds, t);
+            digit<2>(v, a, t, c0, m);
+        }
+        if constexpr (kPhases > 3) {
+            exchange<tile_window<2>(), tile_window<3>()>(v, lds, t);
+            digit<3>(v, a, t, c0, m);
+        }
+        constexpr int wl = tile_window<kPhases - 1>();
+        if constexpr (COL) {  // intermediate: same positions
+#pragma unroll
+            for (int r = 0; r < kE; ++r) {
+                const std::uint32_t i = phase_index<wl>(t, r);
+                a.out[base + c0 + (i & ((1u << LI) - 1u)) + (std::uint64_t(i >> LI) << a.l2)] = v[r];
+            }
+            return;
+        }
+        // Final pass: bit-reversed positions -> natural order through LDS.
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < kE; ++r) lds[L::addr(phase_index<wl>(t, r))] = v[r];
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < kE; ++r) {
+            const std::uint32_t g = t + T * r;
+            std::uint32_t i;
+            std::uint64_t where;
+            bool ok = true;
+            if (single) {  // rows are transforms: in-row bit reversal, lanes along the row
+                const std::uint32_t xp = g & ((1u << LT) - 1u), rr = g >> LT;
+                i = brev(xp, LT) | (rr << LT);
+                ok = row0 + rr < a.rows;
+                where = (std::uint64_t(row0 + rr) << LT) + xp;
+            } else {  // grid transpose: tile rows are bitrev(k0 + rr) of one transform
+                const std::uint32_t rr = g & ((1u << LI) - 1u), cp = g >> LI;
+                const std::uint32_t per = a.l1 - LI;  // tiles per transform = 2^per
+                const std::uint32_t poly = (row0 >> LI) >> per;
+                const std::uint32_t k0 = row0 & ((1u << a.l1) - 1u);
+                i = brev(cp, LT) | (rr << LT);
+                where = (std::uint64_t(poly) << m) + (std::uint64_t(cp) << a.l1) + k0 + rr;
+            }
+            const float2 x = lds[L::addr(i)];
+            if (ok) a.out[where] = make_float2(x.x * a.scale, x.y * a.scale);
+        }
+    }
+};
+
+template <int LT, int LI, bool COL, bool INV>
+__global__ __launch_bounds__(1 << (LT + LI - kLE)) void fft_pass_kernel(FftArgs a) {
+    FftPass<LT, LI, COL, INV>::run(a);
+}
+
+using Launch = void (*)(const FftArgs&, unsigned grid, hipStream_t);
+
+struct Key {
+    int lt, li;
+    bool col, inv;
+    bool operator<(const Key& o) const { return std::tie(lt, li, col, inv) < std::tie(o.lt, o.li, o.col, o.inv); }
+};
+
+template <int LT, int LI, bool COL, bool INV>
+void launch(const FftArgs& a, unsigned grid, hipStream_t stream) {
+    constexpr std::uint32_t bytes = FftLds<COL, LT, LI>::kWords * sizeof(float2);
+    static const bool configured = [] {
+        if (bytes > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, INV>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+        return true;
+    }();
+    (void)configured;
+    hipLaunchKernelGGL((fft_pass_kernel<LT, LI, COL, INV>), dim3(grid), dim3(1u << (LT + LI - kLE)), bytes, stream,
+                       a);
+}
+
+std::map<Key, Launch>& registry() {
+    static std::map<Key, Launch> table;
+    return table;
+}
+
+template <int LT, int LI, bool COL>
+void add() {
+    registry()[Key{LT, LI, COL, false}] = &launch<LT, LI, COL, false>;
+    registry()[Key{LT, LI, COL, true}] = &launch<LT, LI, COL, true>;
+}
+
+// Shapes: one pass for m <= 14 (2^12-point tiles, 2^14 for m = 13, 14);
+// two passes l1 = m / 2, l2 = m - l1 with 2^14-point tiles.
+constexpr int single_li(int m) { return m < 12 ? 12 - m : 0; }
+template <int M>
+void add_two() {
+    constexpr int l1 = M / 2, l2 = M - l1;
+    constexpr int col_li = 14 - l1 < l2 ? 14 - l1 : l2;
+    constexpr int row_li = 14 - l2 < l1 ? 14 - l2 : l1;
+    add<l1, col_li, true>();
+    add<l2, row_li, false>();
+}
+
+void register_all() {
+    add<1, single_li(1), false>();
+    add<2, single_li(2), false>();
+    add<3, single_li(3), false>();
+    add<4, single_li(4), false>();
+    add<5, single_li(5), false>();
+    add<6, single_li(6), false>();
+    add<7, single_li(7), false>();
+    add<8, single_li(8), false>();
+    add<9, single_li(9), false>();
+    add<10, single_li(10), false>();
+    add<11, single_li(11), false>();
+    add<12, single_li(12), false>();
+    add<13, 0, false>();
+    add<14, 0, false>();
+    add_two<15>();
+    add_two<16>();
+    add_two<17>();
+    add_two<18>();
+    add_two<19>();
+    add_two<20>();
+    add_two<21>();
+    add_two<22>();
+    add_two<23>();
+    add_two<24>();
+}
+
+Launch find(const Key& k) {
+    static std::once_flag once;
+    std::call_once(once, register_all);
+    auto it = registry().find(k);
+    if (it == registry().end()) throw NotSupported("FFT pass shape has no gfx950 kernel");
+    return it->second;
+}
+
+class FftExecutor final : public Executor {
+  public:
+    explicit FftExecutor(const Request& r) : r_(r) {
+        const std::uint32_t m = r.log_n;
+        supported(m >= 1 && m <= 24, "complex FFT lengths above 2^24 are not yet lowered for gfx950");
+        // Level twiddles: w^(4096 k) and w^k, w = exp(-+2 pi i / n), from double.
+        std::vector<float2> ta(4096), tb(4096);
+        const double sign = r.inverse ? 1.0 : -1.0;
+        const double n = std::ldexp(1.0, int(m));
+        for (int k = 0; k < 4096; ++k) {
+            const double fa = std::fmod(4096.0 * k, n), fb = std::fmod(double(k), n);
+            ta[k] = make_float2(float(std::cos(2 * M_PI * fa / n)), float(sign * std::sin(2 * M_PI * fa / n)));
+            tb[k] = make_float2(float(std::cos(2 * M_PI * fb / n)), float(sign * std::sin(2 * M_PI * fb / n)));
+        }
+        twa_.upload(ta);
+        twb_.upload(tb);
+        const float scale = r.normalize ? 1.0f / float(r.n) : 1.0f;
+        require(r.batch <= 0xffffffffull, "FFT batch exceeds 2^32 transforms");
+        FftArgs base{};
+        base.twa = twa_.as<float2>();
+        base.twb = twb_.as<float2>();
+        base.scale = scale;
+        if (m <= 14) {
+            const int li = single_li(int(m));
+            const std::uint64_t tiles = (r.batch + (1ull << li) - 1) >> li;
+            Step s{find(Key{int(m), li, false, r.inverse}), unsigned(tiles), base, false, false};
+            s.args.l1 = 0;
+            s.args.l2 = m;
+            s.args.rows = unsigned(r.batch);
+            s.args.tiles = unsigned(tiles);
+            steps_.push_back(s);
+            algorithm = "fft-c64-resident-r16";
+        } else {
+            const std::uint32_t l1 = m / 2, l2 = m - l1;
+            const int col_li = std::min<int>(14 - int(l1), int(l2));
+            const int row_li = std::min<int>(14 - int(l2), int(l1));
+            const std::uint64_t col_tiles = r.batch << (l2 - col_li);
+            const std::uint64_t row_tiles = r.batch << (l1 - row_li);
+            require(col_tiles <= 0xffffffffull && row_tiles <= 0xffffffffull, "FFT batch exceeds the grid");
+            Step a{find(Key{int(l1), col_li, true, r.inverse}), unsigned(col_tiles), base, false, true};
+            a.args.l1 = l1;
+            a.args.l2 = l2;
+            a.args.rows = unsigned(r.batch << l1);
+            a.args.tiles = unsigned(col_tiles);
+            a.args.scale = 1.0f;
+            Step b{find(Key{int(l2), row_li, false, r.inverse}), unsigned(row_tiles), base, true, false};
+            b.args.l1 = l1;
+            b.args.l2 = l2;
+            b.args.rows = unsigned(r.batch << l1);
+            b.args.tiles = unsigned(row_tiles);
+            steps_ = {a, b};
+            workspace_ = static_cast<std::size_t>(r.batch << m) * sizeof(float2);
+            algorithm = "fft-c64-two-pass-r16";
+        }
+        reason = "decimation in frequency over 4-bit digits: in-register radix-16 codelets, level twiddles from "
+                 "two 4096-entry tables, LDS-staged bit-reversal (and grid transpose) on the final store";
+        json::Writer w;
+        w.begin_object()
+            .field("schema_version", 1u)
+            .field("operator", "fft")
+            .field("algorithm", algorithm)
+            .field("log_n", m)
+            .field("batch", r.batch)
+            .field("direction", r.inverse ? "inverse" : "forward")
+            .field("passes", unsigned(steps_.size()))
+            .field("workspace_bytes", std::uint64_t(workspace_))
+            .end_object();
+        mapping_json = w.str();
+    }
+    std::size_t workspace_bytes() const override { return workspace_; }
+    void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
+        require(steps_.size() < 2 || ws != nullptr, "two-pass FFT needs a workspace");
+        for (const auto& s : steps_) {
+            FftArgs a = s.args;
+            a.in = static_cast<const float2*>(s.reads_ws ? ws : in);
+            a.out = static_cast<float2*>(s.writes_ws ? ws : out);
+            s.fn(a, s.grid, stream);
+            hip_check(hipGetLastError(), "FFT pass launch");
+        }
+    }
+
+  private:
+    struct Step {
+        Launch fn;
+        unsigned grid;
+        FftArgs args;
+        bool reads_ws, writes_ws;
+    };
+    Request r_;
+    DeviceBuffer twa_, twb_;
+    std::vector<Step> steps_;
+    std::size_t workspace_ = 0;
+};
+
+}  // namespace
+
+std::unique_ptr<Executor> make_fft_executor(const Request& r) { return std::make_unique<FftExecutor>(r); }
+
 }  // namespace cbw
