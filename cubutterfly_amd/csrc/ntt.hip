@@ -22,7 +22,6 @@
 #include "planner.hpp"
 
 #include <algorithm>
-#include <cstdlib>
 
 namespace cbw {
 namespace ntt_detail {
@@ -96,22 +95,6 @@ std::vector<TwPair<W>> make_table(std::uint32_t log_n, std::uint64_t q, std::uin
     return table;
 }
 
-// Persistent grid of a pass: each workgroup walks several tiles so the next
-// tile's loads overlap the current tile's arithmetic. Two resident workgroups
-// per CU by default (CUBUTTERFLY_NTT_WG_PER_CU overrides, 1..8); a multiple of
-// 8 so every XCD gets the same number of workgroups.
-inline unsigned persistent_grid(std::uint64_t tiles) {
-    static const unsigned per_cu = [] {
-        const char* env = std::getenv("CUBUTTERFLY_NTT_WG_PER_CU");
-        const int v = env ? std::atoi(env) : 2;
-        return unsigned(v >= 1 && v <= 8 ? v : 2);
-    }();
-    const std::uint64_t resident = std::uint64_t(device_cu_count()) * per_cu;
-    std::uint64_t grid = std::min<std::uint64_t>(tiles, resident);
-    if (grid > 8) grid &= ~std::uint64_t{7};
-    return unsigned(std::max<std::uint64_t>(grid, 1));
-}
-
 template <class W>
 struct EngineImplT {
     NttEngineConfig cfg;
@@ -123,6 +106,8 @@ struct EngineImplT {
         unsigned grid;
         PassArgs<W> args;
         bool reads_workspace, writes_workspace;
+        int lt, prefix_bits;
+        bool last;
     };
     std::vector<Launch> launches;
     std::string json_shape;
@@ -134,30 +119,10 @@ struct EngineImplT {
         std::uint64_t max_q = 0;
         for (const auto& d : c.domains) max_q = std::max(max_q, d.modulus);
         lazy = max_q < (std::uint64_t{1} << (bits - 2));
-        // Device domain records and their tables.
-        std::vector<DeviceDomain<W>> host_domains;
-        std::vector<TwPair<W>> all_tables;
-        for (const auto& d : c.domains) {
-            const std::uint64_t q = d.modulus;
-            const std::uint64_t root = c.inverse ? invmod(d.root, q) : d.root;
-            auto table = make_table<W>(log_n, q, root, c.negacyclic);
-            DeviceDomain<W> dd{};
-            dd.q = W(q);
-            dd.q2 = W(2 * q);
-            dd.rwp = shoup_factor<W>(1, q);
-            const std::uint64_t ninv = invmod(n % q, q);
-            dd.ninv = {W(ninv), shoup_factor<W>(ninv, q)};
-            const std::uint64_t last = mulmod(table[1].w, ninv, q);
-            dd.last = {W(last), shoup_factor<W>(last, q)};
-            dd.tw = all_tables.size();
-            host_domains.push_back(dd);
-            all_tables.insert(all_tables.end(), table.begin(), table.end());
-        }
-        tables.upload(all_tables);
-        domains.upload(host_domains);
         const std::uint64_t polys = c.polynomials.empty() ? c.batch : c.polynomials.size();
         require(polys >= 1 && polys <= 0xffffffffull, "NTT batch must be in [1, 2^32)");
-        if (!c.polynomials.empty()) {
+        const bool offsets = !c.polynomials.empty();
+        if (offsets) {
             std::vector<std::uint32_t> pd;
             std::vector<std::uint64_t> io, oo;
             for (const auto& p : c.polynomials) {
@@ -171,57 +136,62 @@ struct EngineImplT {
         }
         const bool mixed = c.domains.size() > 1;
         PassArgs<W> base{};
-        base.domains = domains.as<DeviceDomain<W>>();
-        base.tw = tables.as<TwPair<W>>();
-        base.poly_domain = poly_domain.as<std::uint32_t>();
         base.polys = static_cast<std::uint32_t>(polys);
-        constexpr int LB = 12;
+        constexpr int LB = kTileLog;
         const bool ct = !c.inverse;
         // Which physical boundaries differ from the algorithm's native order
         // (forward: natural in / bit-reversed out; inverse: the opposite).
         const bool perm_in = ct ? c.input_bit_reversed : !c.input_bit_reversed;
         const bool perm_out = ct ? !c.output_bit_reversed : c.output_bit_reversed;
         if (log_n <= 12) {
-            // One pass: whole polynomials per workgroup (one per tile if domains mix).
+            // One pass: whole polynomials per workgroup (one per tile if
+            // domains mix or polynomials sit at explicit offsets).
             const int li = LB - int(log_n);
-            supported(!mixed || li == 0, "mixed-domain batches need log n >= 12");
+            supported((!mixed && !offsets) || li == 0, "mixed-domain or offset batches need log n >= 12");
             l1 = 0;
             l2 = log_n;
             const std::uint64_t per_tile = std::uint64_t{1} << li;
             const std::uint64_t tiles = (polys + per_tile - 1) / per_tile;
             Launch L{};
-            L.fn = find_pass<W>(PassKey{lazy, int(log_n), li, false, ct, perm_in, perm_out, true});
-            L.grid = persistent_grid(tiles);
+            L.fn = find_pass<W>(PassKey{lazy, int(log_n), int(log_n), li, false, ct, perm_in, perm_out, true});
+            L.grid = unsigned(tiles);
             L.args = base;
-            L.args.l1 = 0;
-            L.args.l2 = log_n;
             L.args.tiles = unsigned(tiles);
             L.args.in_off = in_off.as<std::uint64_t>();
             L.args.out_off = out_off.as<std::uint64_t>();
             L.args.reduce_input = c.reduce_input;
+            L.lt = int(log_n);
+            L.prefix_bits = 0;
+            L.last = true;
             launches.push_back(L);
             json_shape = "{\"passes\":1,\"tile_log\":" + std::to_string(LB) + "}";
         } else {
             supported(log_n <= 20, "NTT lengths above 2^20 are not yet lowered for gfx950");
-            l1 = std::min<std::uint32_t>(8, log_n / 2);
+            l1 = std::uint32_t(split_l1(int(log_n)));
             l2 = log_n - l1;
-            const int col_li = 4;
-            const int rli = std::min<int>(int(l1), LB - int(l2));
+            const int col_li = kColLines;
+            const int rli = row_lines(int(l1), int(l2));
             const std::uint64_t col_tiles = polys << (l2 - col_li);
             const std::uint64_t row_tiles = polys << (l1 - rli);
             require(col_tiles <= 0xffffffffull && row_tiles <= 0xffffffffull, "NTT batch exceeds the grid");
             Launch A{}, B{};
             // Pass A: high bits (columns); pass B: low bits (rows).
             A.args = base;
-            A.args.l1 = l1;
-            A.args.l2 = l2;
             A.args.tiles = unsigned(col_tiles);
-            A.grid = persistent_grid(col_tiles);
-            B.args = A.args;
+            A.grid = unsigned(col_tiles);
+            A.lt = int(l1);
+            A.prefix_bits = 0;
+            A.last = !ct;
+            B.args = base;
             B.args.tiles = unsigned(row_tiles);
-            B.grid = persistent_grid(row_tiles);
-            A.fn = find_pass<W>(PassKey{lazy, int(l1), col_li, true, ct, ct && perm_in, !ct && perm_out, false});
-            B.fn = find_pass<W>(PassKey{lazy, int(l2), rli, false, ct, !ct && perm_in, ct && perm_out, false});
+            B.grid = unsigned(row_tiles);
+            B.lt = int(l2);
+            B.prefix_bits = int(l1);
+            B.last = ct;
+            A.fn = find_pass<W>(
+                PassKey{lazy, int(log_n), int(l1), col_li, true, ct, ct && perm_in, !ct && perm_out, false});
+            B.fn = find_pass<W>(
+                PassKey{lazy, int(log_n), int(l2), rli, false, ct, !ct && perm_in, ct && perm_out, false});
             if (ct) {  // forward: A reads the input, B writes the output
                 A.args.in_off = in_off.as<std::uint64_t>();
                 A.args.reduce_input = c.reduce_input;
@@ -240,6 +210,38 @@ struct EngineImplT {
             json_shape = "{\"passes\":2,\"high_bits\":" + std::to_string(l1) + ",\"low_bits\":" +
                          std::to_string(l2) + ",\"column_tile_lines\":" + std::to_string(1 << col_li) +
                          ",\"row_tile_lines\":" + std::to_string(1 << rli) + "}";
+        }
+        // Device domain records and their twiddle chunks (one layout for all
+        // domains, so the phase offsets are shared).
+        std::vector<DeviceDomain<W>> host_domains;
+        std::vector<TwPair<W>> all_tables;
+        for (const auto& d : c.domains) {
+            const std::uint64_t q = d.modulus;
+            const std::uint64_t root = c.inverse ? invmod(d.root, q) : d.root;
+            const auto table = make_table<W>(log_n, q, root, c.negacyclic);
+            DeviceDomain<W> dd{};
+            dd.q = W(q);
+            dd.q2 = W(2 * q);
+            dd.rwp = shoup_factor<W>(1, q);
+            const std::uint64_t ninv = invmod(n % q, q);
+            dd.ninv = {W(ninv), shoup_factor<W>(ninv, q)};
+            const std::uint64_t last = mulmod(table[1].w, ninv, q);
+            dd.last = {W(last), shoup_factor<W>(last, q)};
+            dd.tw = all_tables.size();
+            for (auto& L : launches)
+                append_pass_chunks<W>(all_tables, std::size_t(dd.tw), table, L.lt, L.prefix_bits, ct, L.last,
+                                      L.args.phase_off);
+            host_domains.push_back(dd);
+        }
+        require(all_tables.size() * sizeof(TwPair<W>) < 0x7fffffffull, "NTT twiddle tables exceed 2 GiB");
+        tables.upload(all_tables);
+        domains.upload(host_domains);
+        const std::size_t per_domain = all_tables.size() / c.domains.size();
+        for (auto& L : launches) {
+            L.args.tw_bytes = static_cast<std::uint32_t>(per_domain * sizeof(TwPair<W>));
+            L.args.domains = domains.as<DeviceDomain<W>>();
+            L.args.tw = tables.as<TwPair<W>>();
+            L.args.poly_domain = poly_domain.as<std::uint32_t>();
         }
     }
 

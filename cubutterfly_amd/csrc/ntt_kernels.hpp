@@ -1,15 +1,31 @@
-// Device code of the NTT engine: the templated pass kernel, Shoup arithmetic
-// and the registry of instantiated pass shapes. Included by ntt.hip (host side)
-// and by the ntt_u{32,64}_{lazy,strict}.hip translation units, which
-// instantiate the kernels in parallel builds.
+// Device code of the NTT engine: the templated pass kernel, Shoup arithmetic,
+// the twiddle-chunk geometry shared with the host table builder, and the
+// registry of instantiated pass shapes. Included by ntt.hip (host side) and by
+// the ntt_u{32,64}_{lazy,strict}.hip translation units, which instantiate the
+// kernels in parallel builds.
+//
+// Memory access: every tile addresses one polynomial (or, for one-pass tiles,
+// one run of dense polynomials) through a buffer resource whose base and
+// range are that span, so each load and store is a 32-bit lane offset from a
+// uniform base (no 64-bit address arithmetic), and an access outside the span
+// reads 0 / is dropped by the hardware range check instead of touching other
+// memory.
+//
+// Twiddles: a radix-16 phase of the merged-twist transform needs, per thread,
+// the 15 (or fewer) table entries of one block of the stage tree. The host
+// lays those entries out contiguously per block ("chunks", in stage execution
+// order, padded to 16 bytes), so a thread fetches its phase twiddles with a
+// few 16-byte loads from one address.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
 #include "ntt_engine.hpp"
 
+#include <cstddef>
 #include <map>
 #include <tuple>
+#include <vector>
 
 namespace cbw {
 namespace ntt_detail {
@@ -27,7 +43,7 @@ struct DeviceDomain {
     W q, q2, rwp;         // modulus, 2q, floor(2^k / q) (Shoup factor of 1)
     TwPair<W> ninv;       // n^-1 with its Shoup factor
     TwPair<W> last;       // Tinv[1] * n^-1 (final inverse stage)
-    std::uint64_t tw;     // offset of this domain's table (entries 1..n-1) in PassArgs::tw
+    std::uint64_t tw;     // offset of this domain's chunk tables in PassArgs::tw (TwPairs)
 };
 
 template <class W>
@@ -35,14 +51,98 @@ struct PassArgs {
     const W* in;
     W* out;
     const DeviceDomain<W>* domains;
-    const TwPair<W>* tw;               // all domains' twiddle tables, concatenated
+    const TwPair<W>* tw;               // all domains' chunk tables, concatenated
     const std::uint32_t* poly_domain;  // per polynomial (null: domain 0)
     const std::uint64_t* in_off;       // per polynomial word offset (null: p << log n)
     const std::uint64_t* out_off;
-    std::uint32_t l1, l2;  // high / low index bits of the two-pass split (l1 = 0: one pass)
     std::uint32_t polys, tiles;
     std::uint32_t reduce_input;
+    std::uint32_t phase_off[3];  // chunk array of each phase, TwPairs from the domain's table start
+    std::uint32_t tw_bytes;      // bytes of one domain's chunk tables (buffer range of the twiddle reads)
 };
+
+// ---- phase geometry (host and device) ---------------------------------------
+//
+// A pass butterflies LT transform bits in phases of a 4-bit register window.
+// Cooley-Tukey (CT) walks the bits high -> low, windows [LT-4(P+1), LT-4P)
+// clamped at 0; Gentleman-Sande (GS) walks low -> high, windows [4P, 4P+4)
+// clamped at LT-4. A clamped window re-covers bits of its neighbour; only the
+// bits not yet done ("active" stages) are butterflied there.
+
+constexpr int num_phases(int lt) { return (lt + kLE - 1) / kLE; }
+constexpr int imin(int a, int b) { return a < b ? a : b; }
+constexpr int imax(int a, int b) { return a > b ? a : b; }
+
+constexpr int window_start(int lt, bool ct, int p) {
+    return ct ? imax(lt - kLE * (p + 1), 0) : (kLE * p < lt - kLE ? kLE * p : imax(lt - kLE, 0));
+}
+constexpr int stage_hi(int lt, bool ct, int p) {
+    const int ws = window_start(lt, ct, p);
+    return ct ? imin(imin(ws + 3, lt - 1), lt - kLE * p - 1) : imin(ws + 3, lt - 1);
+}
+constexpr int stage_lo(int lt, bool ct, int p) {
+    const int ws = window_start(lt, ct, p);
+    return ct ? ws : imax(ws, kLE * p);
+}
+// Stage k of the phase at window ws: its twiddle for register group g is
+// table[(head >> (k+1)) + (g & gmask)], head = (prefix << lt) | (window bits
+// clear). Distinct entries per thread: 2^min(ws+3-k, lt-1-k). All of a
+// phase's entries hang off the block index head >> chunk_shift.
+constexpr int stage_count(int lt, int ws, int k) { return 1 << imin(ws + 3 - k, lt - 1 - k); }
+constexpr int chunk_shift(int lt, bool ct, int p) { return imin(window_start(lt, ct, p) + kLE, lt); }
+// The final GS stage of a transform multiplies by n^-1 (no table entries).
+constexpr bool scale_stage(int lt, bool ct, bool last, int k) { return !ct && last && k == lt - 1; }
+// k of the s-th executed stage of a phase.
+constexpr int exec_stage(int lt, bool ct, int p, int s) { return ct ? stage_hi(lt, ct, p) - s : stage_lo(lt, ct, p) + s; }
+constexpr int active_stages(int lt, bool ct, int p) { return stage_hi(lt, ct, p) - stage_lo(lt, ct, p) + 1; }
+// Entry offset of the s-th executed stage within the chunk, and the chunk size.
+constexpr int chunk_offset(int lt, bool ct, bool last, int p, int s) {
+    int off = 0;
+    for (int e = 0; e < s; ++e) {
+        const int k = exec_stage(lt, ct, p, e);
+        if (!scale_stage(lt, ct, last, k)) off += stage_count(lt, window_start(lt, ct, p), k);
+    }
+    return off;
+}
+constexpr int chunk_entries(int lt, bool ct, bool last, int p) {
+    return chunk_offset(lt, ct, last, p, active_stages(lt, ct, p));
+}
+// Chunk stride in TwPairs: a multiple of 16 bytes.
+constexpr int chunk_stride(int lt, bool ct, bool last, int p, int pair_bytes) {
+    const int per16 = 16 / pair_bytes > 0 ? 16 / pair_bytes : 1;
+    const int e = chunk_entries(lt, ct, last, p);
+    return (e + per16 - 1) / per16 * per16;
+}
+
+// Appends one pass's twiddle chunks (layout above) to `out` and
+// records each phase's offset from `base`. prefix_bits: 0 for column and
+// one-pass tiles, l1 for row tiles (their block index carries 2^l1 + row).
+template <class W>
+void append_pass_chunks(std::vector<TwPair<W>>& out, std::size_t base, const std::vector<TwPair<W>>& table, int lt,
+                        int prefix_bits, bool ct, bool last, std::uint32_t (&phase_off)[3]) {
+    for (int p = 0; p < num_phases(lt); ++p) {
+        phase_off[p] = static_cast<std::uint32_t>(out.size() - base);
+        const int entries = chunk_entries(lt, ct, last, p);
+        if (entries == 0) continue;
+        const int shift = chunk_shift(lt, ct, p);
+        const int stride = chunk_stride(lt, ct, last, p, int(sizeof(TwPair<W>)));
+        const int ws = window_start(lt, ct, p);
+        const std::uint64_t first = (std::uint64_t{1} << (prefix_bits + lt)) >> shift;
+        for (std::uint64_t idx = first; idx < 2 * first; ++idx) {
+            std::vector<TwPair<W>> chunk(std::size_t(stride), TwPair<W>{W(0), W(0)});
+            int e = 0;
+            for (int s = 0; s < active_stages(lt, ct, p); ++s) {
+                const int k = exec_stage(lt, ct, p, s);
+                if (scale_stage(lt, ct, last, k)) continue;
+                for (int j = 0; j < stage_count(lt, ws, k); ++j)
+                    chunk[std::size_t(e++)] = table.at((idx << (shift - k - 1)) + std::uint64_t(j));
+            }
+            out.insert(out.end(), chunk.begin(), chunk.end());
+        }
+    }
+}
+
+// ---- arithmetic -------------------------------------------------------------
 
 __device__ __forceinline__ std::uint32_t mulhi(std::uint32_t a, std::uint32_t b) { return __umulhi(a, b); }
 __device__ __forceinline__ std::uint64_t mulhi(std::uint64_t a, std::uint64_t b) { return __umul64hi(a, b); }
@@ -55,14 +155,20 @@ template <class W>
 __device__ __forceinline__ W shoup(W a, W w, W wp, W q) {
     return a * w - mulhi(a, wp) * q;  // [0, 2q) for any a
 }
+// -(shoup(a, w, wp, q)) modulo the word: lets the butterfly fold the sign
+// into one three-input add.
+template <class W>
+__device__ __forceinline__ W neg_shoup(W a, W w, W wp, W q) {
+    return mulhi(a, wp) * q - a * w;
+}
 
 template <class W, bool LAZY>
 __device__ __forceinline__ void ct_butterfly(W& x, W& y, TwPair<W> t, W q, W q2) {
     if constexpr (LAZY) {  // x, y in [0, 4q)
         const W u = csub(x, q2);
-        const W v = shoup(y, t.w, t.wp, q);
-        x = u + v;
-        y = u - v + q2;
+        const W nv = neg_shoup(y, t.w, t.wp, q);  // -v, v in [0, 2q)
+        x = u - nv;
+        y = u + q2 + nv;
     } else {  // x, y in [0, 2q)
         const W u = csub(x, q);
         const W v = csub(shoup(y, t.w, t.wp, q), q);
@@ -97,6 +203,38 @@ __device__ __forceinline__ void gs_scale_butterfly(W& x, W& y, const DeviceDomai
     y = shoup(u - v + span, d.last.w, d.last.wp, d.q);
 }
 
+// ---- buffer access ----------------------------------------------------------
+
+constexpr int kBufferWord3 = 0x00020000;  // raw 32-bit buffer, gfx9 family
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, std::uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             kBufferWord3);
+}
+
+template <class W>
+__device__ __forceinline__ W buffer_load(__amdgpu_buffer_rsrc_t r, std::uint32_t byte_off) {
+    if constexpr (sizeof(W) == 4) {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(byte_off), 0, 0);
+    } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), 0, 0);
+        return (std::uint64_t(v[1]) << 32) | v[0];
+    }
+}
+
+template <class W>
+__device__ __forceinline__ void buffer_store(W x, __amdgpu_buffer_rsrc_t r, std::uint32_t byte_off) {
+    if constexpr (sizeof(W) == 4) {
+        __builtin_amdgcn_raw_buffer_store_b32(x, r, static_cast<int>(byte_off), 0, 0);
+    } else {
+        using V2 = __attribute__((ext_vector_type(2))) std::uint32_t;
+        V2 v;
+        v[0] = static_cast<std::uint32_t>(x);
+        v[1] = static_cast<std::uint32_t>(x >> 32);
+        __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(byte_off), 0, 0);
+    }
+}
+
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ std::uint32_t brev(std::uint32_t x, std::uint32_t bits) {
@@ -110,16 +248,22 @@ __device__ __forceinline__ std::uint32_t phase_index(std::uint32_t t, std::uint3
     return lo | (r << S) | ((t >> S) << (S + kLE));
 }
 
-// Padded / swizzled LDS image of a tile (bank-conflict avoidance for the
-// phase layouts and for the lane-over-line staged transposes).
-template <bool COL, int LT, int LI>
+// Padded LDS image of a tile. Column tiles that stage a bit-reversed boundary
+// also swizzle the column by the top transform bits (lanes then walk rows in
+// bit-reversed order, which a plain stride maps onto few banks).
+template <bool COL, bool SWZ, int LT, int LI>
 struct Lds {
     static constexpr std::uint32_t kWords =
         COL ? (1u << LT) * ((1u << LI) + 1u) : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
     static __device__ __forceinline__ std::uint32_t addr(std::uint32_t i) {
         if constexpr (COL) {
             const std::uint32_t cc = i & ((1u << LI) - 1u), x = i >> LI;
-            return x * ((1u << LI) + 1u) + (cc ^ ((x >> 3) & ((1u << LI) - 1u)));
+            if constexpr (SWZ) {
+                constexpr int top = LT > LI ? LT - LI : 0;
+                return x * ((1u << LI) + 1u) + (cc ^ ((x >> top) & ((1u << LI) - 1u)));
+            } else {
+                return x * ((1u << LI) + 1u) + cc;
+            }
         } else {
             const std::uint32_t x = i & ((1u << LT) - 1u), rr = i >> LT;
             return rr * ((1u << LT) + (1u << LT >> 4) + 1u) + x + (x >> 4);
@@ -127,127 +271,179 @@ struct Lds {
     }
 };
 
-// Transform-relative window start of phase P.
-template <int LT, bool CT, int P>
-constexpr int window_start() {
-    if constexpr (CT) {
-        return LT - kLE * (P + 1) > 0 ? LT - kLE * (P + 1) : 0;
-    } else {
-        return kLE * P < LT - kLE ? kLE * P : (LT - kLE > 0 ? LT - kLE : 0);
-    }
-}
-
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE>
+// ---- the pass ---------------------------------------------------------------
+//
+// A workgroup owns a tile of 2^(LT+LI) words = 2^LT transform points x 2^LI
+// lines, 16 words per thread. COL tiles hold 2^LI adjacent columns (stride
+// 2^L2) of the high L1 bits; ROW tiles hold 2^LI rows of the low L2 bits; one
+// -pass (SINGLE) tiles hold 2^LI whole polynomials (L1 = 0, L2 = LT).
+template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
 struct Pass {
     static constexpr int LB = LT + LI;
     static constexpr std::uint32_t T = 1u << (LB - kLE);
-    static constexpr int kPhases = (LT + kLE - 1) / kLE;
+    static constexpr int kPhases = num_phases(LT);
+    static constexpr int kLogN = L1 + L2;
     static constexpr bool kFirst = SINGLE || (COL == CT);
     static constexpr bool kLast = SINGLE || (COL != CT);
     // Rows of a permuted two-pass ROW tile are bitrev(k0 + rr).
     static constexpr bool kPermRows = !COL && !SINGLE && (PIN || POUT);
-    using L = Lds<COL, LT, LI>;
+    static constexpr std::uint32_t kPolyBytes = std::uint32_t(sizeof(W)) << kLogN;
+    using L = Lds<COL, COL && (PIN || POUT), LT, LI>;
+    static_assert(SINGLE ? (L1 == 0 && L2 == LT) : (COL ? LT == L1 : LT == L2), "pass bits");
+    static_assert(LT >= 1 && LB >= kLE && LB <= 12, "tile shape");
 
     template <int P>
     static constexpr int tile_window() {
-        return (COL ? LI : 0) + window_start<LT, CT, P>();
+        return (COL ? LI : 0) + window_start(LT, CT, P);
     }
 
     struct Tile {
-        std::uint32_t poly;  // COL / two-pass ROW: the polynomial
+        std::uint32_t poly;  // COL / two-pass ROW: the polynomial; SINGLE: the first polynomial
         std::uint32_t c0;    // COL: first column
         std::uint32_t k0;    // ROW: first row (or bit-reversed row index)
-        std::uint32_t l1, l2;
+        std::uint32_t lines; // SINGLE: polynomials in this tile
     };
 
-    static __device__ __forceinline__ std::uint64_t base(const std::uint64_t* off, std::uint32_t p,
-                                                         std::uint32_t log_n) {
-        return off ? off[p] : std::uint64_t(p) << log_n;
+    static __device__ __forceinline__ Tile decode(const PassArgs<W>& a, std::uint32_t tile) {
+        Tile tl{};
+        if constexpr (COL) {
+            constexpr int shift = L2 - LI;
+            tl.poly = tile >> shift;
+            tl.c0 = (tile & ((1u << shift) - 1u)) << LI;
+        } else if constexpr (SINGLE) {
+            tl.poly = tile << LI;
+            tl.lines = min(1u << LI, a.polys - tl.poly);
+        } else {
+            constexpr int shift = L1 - LI;
+            tl.poly = tile >> shift;
+            tl.k0 = (tile & ((1u << shift) - 1u)) << LI;
+        }
+        return tl;
+    }
+
+    // Buffer over the tile's span: its polynomial (two-pass, or one-pass with
+    // explicit offsets, where a tile holds one polynomial) or its run of dense
+    // polynomials (one-pass).
+    static __device__ __forceinline__ __amdgpu_buffer_rsrc_t span(const W* base, const std::uint64_t* off,
+                                                                  const Tile& tl) {
+        if constexpr (SINGLE) {
+            if (off) return make_rsrc(base + off[tl.poly], kPolyBytes);
+            return make_rsrc(base + (std::uint64_t(tl.poly) << kLogN), tl.lines * kPolyBytes);
+        } else {
+            return make_rsrc(base + (off ? off[tl.poly] : std::uint64_t(tl.poly) << kLogN), kPolyBytes);
+        }
     }
 
     // Logical row of line rr in a ROW tile.
     static __device__ __forceinline__ std::uint32_t row_of(const Tile& tl, std::uint32_t rr) {
         if constexpr (SINGLE) return 0;
-        else if constexpr (kPermRows) return brev(tl.k0 + rr, tl.l1);
+        else if constexpr (kPermRows) return brev(tl.k0 + rr, L1);
         else return tl.k0 + rr;
     }
 
-    // Physical word (relative to the polynomial base) of tile element i, natural side.
-    static __device__ __forceinline__ std::uint64_t natural_word(const Tile& tl, std::uint32_t i) {
+    // Word (relative to the span) of tile element i, natural side.
+    static __device__ __forceinline__ std::uint32_t natural_word(const Tile& tl, std::uint32_t i) {
         if constexpr (COL) {
             const std::uint32_t cc = i & ((1u << LI) - 1u), x = i >> LI;
-            return tl.c0 + cc + (std::uint64_t(x) << tl.l2);
+            return tl.c0 + cc + (x << L2);
+        } else if constexpr (SINGLE) {
+            return i;  // rows are consecutive polynomials of 2^LT words
         } else {
             const std::uint32_t x = i & ((1u << LT) - 1u), rr = i >> LT;
-            return (std::uint64_t(row_of(tl, rr)) << tl.l2) + x;
+            return (row_of(tl, rr) << L2) + x;
         }
     }
 
     // Staged (permuted) enumeration: element g of the tile in physical
-    // contiguity order -> (tile index, polynomial, word within polynomial).
+    // contiguity order -> (tile index i, word relative to the span).
     static __device__ __forceinline__ void permuted(const Tile& tl, std::uint32_t g, std::uint32_t& i,
-                                                    std::uint32_t& poly, std::uint64_t& word) {
-        if constexpr (COL) {  // each column is a contiguous bit-reversed block of 2^l1 words
+                                                    std::uint32_t& word) {
+        if constexpr (COL) {  // each column is a contiguous bit-reversed block of 2^L1 words
             const std::uint32_t rp = g & ((1u << LT) - 1u), cc = g >> LT;
             i = cc | (brev(rp, LT) << LI);
-            poly = tl.poly;
-            word = (std::uint64_t(brev(tl.c0 + cc, tl.l2)) << tl.l1) + rp;
+            word = (brev(tl.c0 + cc, L2) << L1) + rp;
         } else if constexpr (SINGLE) {  // in-row bit reversal, rows are polynomials
             const std::uint32_t xp = g & ((1u << LT) - 1u), rr = g >> LT;
             i = brev(xp, LT) | (rr << LT);
-            poly = tl.poly + rr;
-            word = xp;
+            word = (rr << LT) + xp;
         } else {  // rows bitrev(k0 + rr): lanes over rr are contiguous words
             const std::uint32_t rr = g & ((1u << LI) - 1u), cp = g >> LI;
             i = brev(cp, LT) | (rr << LT);
-            poly = tl.poly;
-            word = (std::uint64_t(cp) << tl.l1) + tl.k0 + rr;
+            word = (cp << L1) + tl.k0 + rr;
         }
     }
 
-    static __device__ __forceinline__ std::uint32_t poly_of(const Tile& tl, std::uint32_t i) {
-        if constexpr (SINGLE) return tl.poly + (i >> LT);
-        else return tl.poly;
+    // Block index of this thread's phase-P twiddle chunk.
+    template <int P>
+    static __device__ __forceinline__ std::uint32_t chunk_index(const Tile& tl, std::uint32_t t) {
+        const std::uint32_t i0 = phase_index<tile_window<P>()>(t, 0);
+        const std::uint32_t x0 = COL ? (i0 >> LI) : (i0 & ((1u << LT) - 1u));
+        // Prefix: 1 for columns and one-pass rows, 2^L1 + row for two-pass
+        // rows (the row is the same for all registers since LT >= 4 there).
+        const std::uint32_t prefix = (COL || SINGLE) ? 1u : ((1u << L1) + row_of(tl, i0 >> LT));
+        const std::uint32_t head = (prefix << LT) | x0;
+        constexpr int shift = chunk_shift(LT, CT, P);
+        constexpr std::uint32_t first = ((COL || SINGLE) ? (1u << LT) : (1u << (L1 + LT))) >> shift;
+        return (head >> shift) - first;
+    }
+
+    using V4 = __attribute__((ext_vector_type(4))) std::uint32_t;
+    // 16-byte loads that hold one phase's chunk.
+    template <int P>
+    static constexpr int chunk_loads() {
+        return (chunk_entries(LT, CT, kLast, P) * int(sizeof(TwPair<W>)) + 15) / 16;
+    }
+    template <int P>
+    struct Chunk {
+        V4 raw[chunk_loads<P>() > 0 ? chunk_loads<P>() : 1];
+    };
+
+    template <int P>
+    static __device__ __forceinline__ void load_chunk(Chunk<P>& c, const PassArgs<W>& a, const Tile& tl,
+                                                      std::uint32_t t, __amdgpu_buffer_rsrc_t tw) {
+        if constexpr (P < kPhases) {
+            constexpr int stride = chunk_stride(LT, CT, kLast, P, int(sizeof(TwPair<W>)));
+            const std::uint32_t base = (a.phase_off[P] + chunk_index<P>(tl, t) * std::uint32_t(stride)) *
+                                       std::uint32_t(sizeof(TwPair<W>));
+#pragma unroll
+            for (int e = 0; e < chunk_loads<P>(); ++e)
+                c.raw[e] = __builtin_amdgcn_raw_buffer_load_b128(tw, int(base + 16u * e), 0, 0);
+        }
     }
 
     template <int P>
-    static __device__ __forceinline__ void stages(W (&v)[kE], const Tile& tl, std::uint32_t t,
-                                                  const DeviceDomain<W>& d, const TwPair<W>* __restrict__ table) {
-        constexpr int ws = window_start<LT, CT, P>();
-        constexpr int tw0 = tile_window<P>();
-        // Transform index and twiddle prefix of register 0 (window bits clear).
-        // The prefix is 1 for columns and 2^l1 + row for rows; the row is the
-        // same for all registers whenever LT >= 4 (and 0 for one-pass tiles).
-        const std::uint32_t i0 = phase_index<tw0>(t, 0);
-        const std::uint32_t x0 = COL ? (i0 >> LI) : (i0 & ((1u << LT) - 1u));
-        const std::uint32_t prefix = COL ? 1u : ((1u << tl.l1) + row_of(tl, i0 >> LT));
-        const std::uint32_t head = (prefix << LT) | x0;
+    static __device__ __forceinline__ void stages(W (&v)[kE], const Chunk<P>& c, const DeviceDomain<W>& d) {
+        constexpr int ws = window_start(LT, CT, P);
 #pragma unroll
-        for (int s = 0; s < kLE; ++s) {
-            // CT walks bits high -> low, GS low -> high; skip bits of other phases.
-            const int k = CT ? (ws + kLE - 1 - s) : (ws + s);
-            const bool mine = CT ? (k < LT - kLE * P && k >= 0) : (k >= kLE * P && k < LT);
-            if (!mine || k >= LT) continue;
+        for (int s = 0; s < active_stages(LT, CT, P); ++s) {
+            const int k = exec_stage(LT, CT, P, s);
             const int jb = k - ws;
-            // Group g (register bits above jb) uses twiddle (head >> (k+1)) + g;
-            // register bits beyond the transform (LT < 4) do not index it.
             const std::uint32_t gmask = (1u << (LT - 1 - k)) - 1u;
-            const TwPair<W>* __restrict__ tk = table + (head >> (k + 1));
-            const bool scale_stage = kLast && !CT && k == LT - 1;
+            const bool scale = scale_stage(LT, CT, kLast, k);
+            const int off = chunk_offset(LT, CT, kLast, P, s);
 #pragma unroll
             for (int g = 0; g < (1 << (kLE - 1 - jb)); ++g) {
-                TwPair<W> tw{};
-                if (!scale_stage) tw = tk[std::uint32_t(g) & gmask];
+                TwPair<W> tp{};
+                if (!scale) {
+                    const int e = off + int(std::uint32_t(g) & gmask);
+                    if constexpr (sizeof(W) == 4) {
+                        tp.w = c.raw[e >> 1][(e & 1) * 2];
+                        tp.wp = c.raw[e >> 1][(e & 1) * 2 + 1];
+                    } else {
+                        tp.w = (std::uint64_t(c.raw[e][1]) << 32) | c.raw[e][0];
+                        tp.wp = (std::uint64_t(c.raw[e][3]) << 32) | c.raw[e][2];
+                    }
+                }
 #pragma unroll
                 for (int lo = 0; lo < (1 << jb); ++lo) {
                     const int r = (g << (jb + 1)) | lo;
                     const int r2 = r | (1 << jb);
                     if constexpr (CT) {
-                        ct_butterfly<W, LAZY>(v[r], v[r2], tw, d.q, d.q2);
-                    } else if (scale_stage) {
+                        ct_butterfly<W, LAZY>(v[r], v[r2], tp, d.q, d.q2);
+                    } else if (scale) {
                         gs_scale_butterfly<W, LAZY>(v[r], v[r2], d);
                     } else {
-                        gs_butterfly<W, LAZY>(v[r], v[r2], tw, d.q, d.q2);
+                        gs_butterfly<W, LAZY>(v[r], v[r2], tp, d.q, d.q2);
                     }
                 }
             }
@@ -264,87 +460,74 @@ struct Pass {
         for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<TO>(t, r))];
     }
 
-    static __device__ __forceinline__ Tile decode(const PassArgs<W>& a, std::uint32_t tile) {
-        Tile tl{};
-        tl.l1 = a.l1;
-        tl.l2 = a.l2;
-        if constexpr (COL) {
-            const std::uint32_t shift = a.l2 - LI;
-            tl.poly = tile >> shift;
-            tl.c0 = (tile & ((1u << shift) - 1u)) << LI;
-        } else if constexpr (SINGLE) {
-            tl.poly = tile << LI;
-        } else {
-            const std::uint32_t shift = a.l1 - LI;
-            tl.poly = tile >> shift;
-            tl.k0 = (tile & ((1u << shift) - 1u)) << LI;
-        }
-        return tl;
-    }
-
-    // Word address and validity of register r's input element.
-    static __device__ __forceinline__ void input_word(const PassArgs<W>& a, const Tile& tl, std::uint32_t t, int r,
-                                                      std::uint64_t& where, bool& valid) {
-        const std::uint32_t log_n = a.l1 + a.l2;
-        std::uint32_t i, p;
-        std::uint64_t word;
-        if constexpr (PIN) {
-            permuted(tl, t + T * r, i, p, word);
-        } else {
-            i = phase_index<tile_window<0>()>(t, r);
-            p = poly_of(tl, i);
-            word = natural_word(tl, i);
-        }
-        valid = !SINGLE || p < a.polys;
-        where = (valid ? base(a.in_off, SINGLE ? p : tl.poly, log_n) : 0) + word;
-    }
-
-    // Issue the 16 loads of a tile (raw words; reduction happens later).
-    static __device__ __forceinline__ void load_tile(const PassArgs<W>& a, const Tile& tl, std::uint32_t t,
-                                                     W (&v)[kE]) {
-        std::uint64_t where[kE];
-        bool valid[kE];
-#pragma unroll
-        for (int r = 0; r < kE; ++r) input_word(a, tl, t, r, where[r], valid[r]);
-#pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = valid[r] ? a.in[where[r]] : W(0);
-    }
-
-    static __device__ __forceinline__ void process(const PassArgs<W>& a, const Tile& tl, std::uint32_t t, W (&v)[kE],
-                                                   W* lds) {
-        const std::uint32_t log_n = a.l1 + a.l2;
+    static __device__ void run(const PassArgs<W>& a) {
+        __shared__ W lds[L::kWords];
+        const std::uint32_t t = threadIdx.x;
+        const std::uint32_t b = blockIdx.x;
+        // XCD-contiguous tile order: blocks are dealt to the 8 XCDs
+        // round-robin, so block b walks tile (b mod 8) * tiles/8 + b/8 and the
+        // tiles sharing cache lines and twiddle rows meet in one L2.
+        const std::uint32_t tile =
+            (a.tiles & 7u) == 0 && (gridDim.x & 7u) == 0 ? (b & 7u) * (a.tiles >> 3) + (b >> 3) : b;
+        const Tile tl = decode(a, tile);
         // One domain per tile (the planner keeps mixed-domain tiles apart).
         const std::uint32_t dom = a.poly_domain ? a.poly_domain[tl.poly] : 0u;
         const DeviceDomain<W> d = a.domains[dom];
-        // Kernel-argument pointers are known to address global memory, so the
-        // twiddle gathers compile to global (not FLAT) loads.
-        const TwPair<W>* __restrict__ table = a.tw + d.tw;
-        if (kFirst && a.reduce_input) {
-#pragma unroll
-            for (int r = 0; r < kE; ++r) v[r] = shoup(v[r], W(1), d.rwp, d.q);
-        }
+        const __amdgpu_buffer_rsrc_t src = span(a.in, a.in_off, tl);
+        const __amdgpu_buffer_rsrc_t dst = span(a.out, a.out_off, tl);
+        const __amdgpu_buffer_rsrc_t tw = make_rsrc(a.tw + d.tw, a.tw_bytes);
+
+        W v[kE];
         if constexpr (PIN) {
+            W raw[kE];
+#pragma unroll
+            for (int r = 0; r < kE; ++r) {
+                std::uint32_t i, word;
+                permuted(tl, t + T * r, i, word);
+                raw[r] = buffer_load<W>(src, word * std::uint32_t(sizeof(W)));
+            }
             lds_barrier();
 #pragma unroll
             for (int r = 0; r < kE; ++r) {
-                std::uint32_t i, p;
-                std::uint64_t word;
-                permuted(tl, t + T * r, i, p, word);
-                lds[L::addr(i)] = v[r];
+                std::uint32_t i, word;
+                permuted(tl, t + T * r, i, word);
+                lds[L::addr(i)] = raw[r];
             }
             lds_barrier();
 #pragma unroll
             for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<tile_window<0>()>(t, r))];
+        } else {
+#pragma unroll
+            for (int r = 0; r < kE; ++r)
+                v[r] = buffer_load<W>(src, natural_word(tl, phase_index<tile_window<0>()>(t, r)) *
+                                               std::uint32_t(sizeof(W)));
+        }
+        // Every phase's twiddles are requested up front, so no phase waits on
+        // a fresh load after an exchange.
+        Chunk<0> c0;
+        Chunk<1> c1;
+        Chunk<2> c2;
+        load_chunk<0>(c0, a, tl, t, tw);
+        load_chunk<1>(c1, a, tl, t, tw);
+        load_chunk<2>(c2, a, tl, t, tw);
+        if (kFirst && a.reduce_input) {
+            // Arbitrary input words -> [0, 2q). A Cooley-Tukey first stage
+            // multiplies its upper operands by twiddles (any word is fine
+            // there), so only the lower half needs it.
+            constexpr int top = CT ? stage_hi(LT, CT, 0) - window_start(LT, CT, 0) : kLE;
+#pragma unroll
+            for (int r = 0; r < kE; ++r)
+                if (!CT || LT < kLE || !((r >> top) & 1)) v[r] = shoup(v[r], W(1), d.rwp, d.q);
         }
 
-        stages<0>(v, tl, t, d, table);
+        stages<0>(v, c0, d);
         if constexpr (kPhases > 1) {
             exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
-            stages<1>(v, tl, t, d, table);
+            stages<1>(v, c1, d);
         }
         if constexpr (kPhases > 2) {
             exchange<tile_window<1>(), tile_window<2>()>(v, lds, t);
-            stages<2>(v, tl, t, d, table);
+            stages<2>(v, c2, d);
         }
         constexpr int wl = tile_window<kPhases - 1>();
         if constexpr (kLast) {
@@ -355,9 +538,6 @@ struct Pass {
                 v[r] = csub(x, d.q);
             }
         }
-        const std::uint64_t out_tile = SINGLE ? 0 : base(a.out_off, tl.poly, log_n);
-        std::uint64_t where[kE];
-        bool valid[kE];
         if constexpr (POUT) {
             lds_barrier();
 #pragma unroll
@@ -365,69 +545,21 @@ struct Pass {
             lds_barrier();
 #pragma unroll
             for (int r = 0; r < kE; ++r) {
-                std::uint32_t i, p;
-                std::uint64_t word;
-                permuted(tl, t + T * r, i, p, word);
-                v[r] = lds[L::addr(i)];
-                valid[r] = !SINGLE || p < a.polys;
-                where[r] = (SINGLE ? (valid[r] ? base(a.out_off, p, log_n) : 0) : out_tile) + word;
+                std::uint32_t i, word;
+                permuted(tl, t + T * r, i, word);
+                buffer_store<W>(lds[L::addr(i)], dst, word * std::uint32_t(sizeof(W)));
             }
         } else {
 #pragma unroll
-            for (int r = 0; r < kE; ++r) {
-                const std::uint32_t i = phase_index<wl>(t, r);
-                const std::uint32_t p = poly_of(tl, i);
-                valid[r] = !SINGLE || p < a.polys;
-                where[r] = (SINGLE ? (valid[r] ? base(a.out_off, p, log_n) : 0) : out_tile) + natural_word(tl, i);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < kE; ++r)
-            if (valid[r]) a.out[where[r]] = v[r];
-    }
-
-    // Persistent walk over tiles: the next tile's loads are issued before the
-    // current tile is processed. When the tile count and the grid are
-    // multiples of 8, each XCD (blocks are dealt to the 8 XCDs round-robin)
-    // walks one contiguous range of tiles, so tiles sharing cache lines and
-    // twiddle rows meet in the same L2.
-    static __device__ void run(const PassArgs<W>& a) {
-        __shared__ W lds[L::kWords];
-        const std::uint32_t t = threadIdx.x;
-        const std::uint32_t grid = gridDim.x, b = blockIdx.x;
-        const bool xcd = (a.tiles & 7u) == 0 && (grid & 7u) == 0;
-        const std::uint32_t per_xcd = a.tiles >> 3, stride = xcd ? (grid >> 3) : grid;
-        const std::uint32_t first = xcd ? (b >> 3) : b;  // position within this block's range
-        const std::uint32_t range_base = xcd ? (b & 7u) * per_xcd : 0u;
-        const std::uint32_t range_end = xcd ? per_xcd : a.tiles;
-
-        std::uint32_t pos = first;
-        if (pos >= range_end) return;
-        Tile tl = decode(a, range_base + pos);
-        W v[kE];
-        load_tile(a, tl, t, v);
-        for (;;) {
-            const std::uint32_t next = pos + stride;
-            const bool more = next < range_end;
-            Tile tn{};
-            W nv[kE];
-            if (more) {
-                tn = decode(a, range_base + next);
-                load_tile(a, tn, t, nv);
-            }
-            process(a, tl, t, v, lds);
-            if (!more) break;
-            pos = next;
-            tl = tn;
-#pragma unroll
-            for (int r = 0; r < kE; ++r) v[r] = nv[r];
+            for (int r = 0; r < kE; ++r)
+                buffer_store<W>(v[r], dst, natural_word(tl, phase_index<wl>(t, r)) * std::uint32_t(sizeof(W)));
         }
     }
 };
 
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE>
+template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
 __global__ __launch_bounds__(1 << (LT + LI - kLE)) void ntt_pass_kernel(PassArgs<W> a) {
-    Pass<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE>::run(a);
+    Pass<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>::run(a);
 }
 
 // ---- launcher registry -----------------------------------------------------
@@ -437,17 +569,17 @@ using PassLaunch = void (*)(const PassArgs<W>&, unsigned grid, hipStream_t);
 
 struct PassKey {
     bool lazy;
-    int lt, li;
+    int log_n, lt, li;
     bool col, ct, pin, pout, single;
     bool operator<(const PassKey& o) const {
-        return std::tie(lazy, lt, li, col, ct, pin, pout, single) <
-               std::tie(o.lazy, o.lt, o.li, o.col, o.ct, o.pin, o.pout, o.single);
+        return std::tie(lazy, log_n, lt, li, col, ct, pin, pout, single) <
+               std::tie(o.lazy, o.log_n, o.lt, o.li, o.col, o.ct, o.pin, o.pout, o.single);
     }
 };
 
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE>
+template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
 void launch_pass(const PassArgs<W>& a, unsigned grid, hipStream_t stream) {
-    hipLaunchKernelGGL((ntt_pass_kernel<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE>), dim3(grid),
+    hipLaunchKernelGGL((ntt_pass_kernel<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>), dim3(grid),
                        dim3(1u << (LT + LI - kLE)), 0, stream, a);
 }
 
@@ -459,50 +591,51 @@ std::map<PassKey, PassLaunch<std::uint32_t>>& registry<std::uint32_t>();
 template <>
 std::map<PassKey, PassLaunch<std::uint64_t>>& registry<std::uint64_t>();
 
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE>
+template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
 void add() {
-    registry<W>()[PassKey{LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE}] =
-        &launch_pass<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE>;
+    registry<W>()[PassKey{LAZY, L1 + L2, LT, LI, COL, CT, PIN, POUT, SINGLE}] =
+        &launch_pass<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>;
 }
 
 // Boundary-permutation variants of one pass shape: a first pass may permute
 // its input, a last pass its output.
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool SINGLE>
+template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool SINGLE, int L1, int L2>
 void add_variants() {
     constexpr bool first = SINGLE || (COL == CT);
     constexpr bool last = SINGLE || (COL != CT);
-    add<W, LAZY, LT, LI, COL, CT, false, false, SINGLE>();
-    if constexpr (first) add<W, LAZY, LT, LI, COL, CT, true, false, SINGLE>();
-    if constexpr (last) add<W, LAZY, LT, LI, COL, CT, false, true, SINGLE>();
-    if constexpr (first && last) add<W, LAZY, LT, LI, COL, CT, true, true, SINGLE>();
+    add<W, LAZY, LT, LI, COL, CT, false, false, SINGLE, L1, L2>();
+    if constexpr (first) add<W, LAZY, LT, LI, COL, CT, true, false, SINGLE, L1, L2>();
+    if constexpr (last) add<W, LAZY, LT, LI, COL, CT, false, true, SINGLE, L1, L2>();
+    if constexpr (first && last) add<W, LAZY, LT, LI, COL, CT, true, true, SINGLE, L1, L2>();
 }
 
 template <class W, bool LAZY, int LT, int LB>
 void add_single() {
-    add_variants<W, LAZY, LT, LB - LT, false, true, true>();
-    add_variants<W, LAZY, LT, LB - LT, false, false, true>();
+    add_variants<W, LAZY, LT, LB - LT, false, true, true, 0, LT>();
+    add_variants<W, LAZY, LT, LB - LT, false, false, true, 0, LT>();
 }
 
-// Two-pass split used by the planner: l1 = min(8, log n / 2) high bits.
+// Two-pass split used by the planner: l1 = min(8, log n / 2) high bits;
+// column tiles of 2^COL_LI lines, row tiles of as many rows as fit 2^LB words.
 constexpr int split_l1(int log_n) { return log_n / 2 < 8 ? log_n / 2 : 8; }
-template <int LB>
-constexpr int row_li(int l1, int l2) { return l1 < LB - l2 ? l1 : LB - l2; }
+constexpr int kTileLog = 12;
+constexpr int kColLines = 4;
+constexpr int row_lines(int l1, int l2) { return l1 < kTileLog - l2 ? l1 : kTileLog - l2; }
 
-template <class W, bool LAZY, int LOG_N, int LB, int COL_LI>
+template <class W, bool LAZY, int LOG_N>
 void add_two_pass() {
     constexpr int l1 = split_l1(LOG_N), l2 = LOG_N - l1;
-    constexpr int rli = row_li<LB>(l1, l2);
-    add_variants<W, LAZY, l1, COL_LI, true, true, false>();
-    add_variants<W, LAZY, l1, COL_LI, true, false, false>();
-    add_variants<W, LAZY, l2, rli, false, true, false>();
-    add_variants<W, LAZY, l2, rli, false, false, false>();
+    constexpr int rli = row_lines(l1, l2);
+    add_variants<W, LAZY, l1, kColLines, true, true, false, l1, l2>();
+    add_variants<W, LAZY, l1, kColLines, true, false, false, l1, l2>();
+    add_variants<W, LAZY, l2, rli, false, true, false, l1, l2>();
+    add_variants<W, LAZY, l2, rli, false, false, false, l1, l2>();
 }
 
-// Word-size specific shapes: 4 KiWord tiles; columns of 64 B (u32) / 128 B (u64).
+// 4 KiWord tiles; columns of 64 B (u32) / 128 B (u64).
 template <class W, bool LAZY>
 void register_all() {
-    constexpr int LB = 12;
-    constexpr int COL_LI = sizeof(W) == 4 ? 4 : 4;
+    constexpr int LB = kTileLog;
     add_single<W, LAZY, 1, LB>();
     add_single<W, LAZY, 2, LB>();
     add_single<W, LAZY, 3, LB>();
@@ -515,16 +648,15 @@ void register_all() {
     add_single<W, LAZY, 10, LB>();
     add_single<W, LAZY, 11, LB>();
     add_single<W, LAZY, 12, LB>();
-    add_two_pass<W, LAZY, 13, LB, COL_LI>();
-    add_two_pass<W, LAZY, 14, LB, COL_LI>();
-    add_two_pass<W, LAZY, 15, LB, COL_LI>();
-    add_two_pass<W, LAZY, 16, LB, COL_LI>();
-    add_two_pass<W, LAZY, 17, LB, COL_LI>();
-    add_two_pass<W, LAZY, 18, LB, COL_LI>();
-    add_two_pass<W, LAZY, 19, LB, COL_LI>();
-    add_two_pass<W, LAZY, 20, LB, COL_LI>();
+    add_two_pass<W, LAZY, 13>();
+    add_two_pass<W, LAZY, 14>();
+    add_two_pass<W, LAZY, 15>();
+    add_two_pass<W, LAZY, 16>();
+    add_two_pass<W, LAZY, 17>();
+    add_two_pass<W, LAZY, 18>();
+    add_two_pass<W, LAZY, 19>();
+    add_two_pass<W, LAZY, 20>();
 }
-
 
 void register_u32_lazy();
 void register_u32_strict();
