@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Headline benchmark of the MI355X butterfly path (one GPU).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--operators]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c2|c3a|c3b|c4|c5a|c5b|copy]
+                [--no-cpu] [--verify] [--eager]
 
 A step is one call of the hot path over one batch of the named BASELINE
 configuration, with inputs already resident in HBM. W untimed steps, then K
@@ -373,6 +374,22 @@ DEFAULT_WORKLOAD = "c2"
 
 
 CALLS_PER_GRAPH = 20
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+
+
+def measured_traffic(name):
+    """HBM bytes per call (read + write) for a workload, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary in profiles/ (scaled by the copy-kernel
+    calibration recorded there), or None when no measurement exists."""
+    try:
+        with open(TRAFFIC_TABLE) as f:
+            for line in f:
+                fields = line.split()
+                if len(fields) == 3 and fields[0] == name:
+                    return int(fields[1]) + int(fields[2])
+    except OSError:
+        pass
+    return None
 
 
 def time_calls(torch, workload, stream, steps, warmup, use_graph=True):
@@ -462,7 +479,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(workload.name),
             "algorithmic_bytes_per_call": workload.bytes_per_call,
         },
         "timing": "hip graph of %d calls, replayed" % CALLS_PER_GRAPH if not args.eager else "eager calls",
