@@ -25,6 +25,10 @@
 #include <mutex>
 #include <tuple>
 
+// Complex products may fuse into FMAs here: FFT accuracy is specified as a
+// relative L2 bound, and fused products are the more accurate ones.
+#pragma clang fp contract(fast)
+
 namespace cbw {
 namespace {
 
@@ -49,6 +53,12 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 __device__ __forceinline__ std::uint32_t brev(std::uint32_t x, std::uint32_t bits) {
     return bits ? __brev(x) >> (32 - bits) : 0u;
+}
+
+constexpr std::uint32_t brev_const(std::uint32_t x, int bits) {
+    std::uint32_t r = 0;
+    for (int i = 0; i < bits; ++i) r |= ((x >> i) & 1u) << (bits - 1 - i);
+    return r;
 }
 
 template <int S>
@@ -140,12 +150,17 @@ struct FftLds {
 };
 
 // One FFT pass over LT transform bits. COL: high bits, tile of 2^LI columns;
-// ROW: low bits, tile of 2^LI rows (the final pass, storing in natural order).
-template <int LT, int LI, bool COL, bool INV>
+// ROW: low bits, tile of 2^LI rows (the final pass, storing in natural order);
+// SINGLE: a one-pass transform, 2^LI whole rows per tile.
+template <int LT, int LI, bool COL, bool SINGLE, bool INV>
 struct FftPass {
     static constexpr int LB = LT + LI;
     static constexpr std::uint32_t T = 1u << (LB - kLE);
     static constexpr int kPhases = (LT + kLE - 1) / kLE;
+    // Prefetching the next tile into registers fits the 128-VGPR budget for
+    // up to two digits; deeper passes run one tile per workgroup (a finished
+    // workgroup's stores then overlap the next one's loads).
+    static constexpr bool kPrefetch = kPhases <= 2;
     using L = FftLds<COL, LT, LI>;
 
     template <int P>
@@ -161,32 +176,78 @@ struct FftPass {
         return (COL ? LI : 0) + window<P>();
     }
 
-    // Digit P: codelet, then the level twiddle unless it is the very last digit.
+    // Whether digit P is followed by a level twiddle (not for the last digit
+    // of the whole transform, whose lowest bit is bit 0).
     template <int P>
-    static __device__ __forceinline__ void digit(float2 (&v)[kE], const FftArgs& a, std::uint32_t t,
-                                                 std::uint32_t c0, std::uint32_t m) {
-        constexpr int ws = window<P>(), ds = digit_bits<P>();
-        codelet<ds, INV>(v);
-        const std::uint32_t lo_rel = std::uint32_t(ws);  // digit's lowest transform bit
-        const std::uint32_t lo = COL ? a.l2 + lo_rel : lo_rel;  // global bit
-        if (lo == 0) return;  // last digit of the whole transform: no level twiddle
-        const std::uint32_t h = lo + ds;
-        const std::uint32_t i0 = phase_index<tile_window<P>()>(t, 0);
-        // Index bits below the digit: for columns, the column and the low
-        // transform bits; for rows, the low transform bits.
-        std::uint32_t x0 = COL ? (i0 >> LI) : (i0 & ((1u << LT) - 1u));
-        std::uint32_t jl = x0 & ((1u << lo_rel) - 1u);
-        if (COL) jl = (jl << a.l2) | (c0 + (i0 & ((1u << LI) - 1u)));
-#pragma unroll
-        for (int r = 0; r < kE; ++r) {
-            // register r holds digit output c = bitrev(r's digit bits); bits of r
-            // above the digit (only in a short last digit) are earlier digits.
-            const std::uint32_t c = brev(std::uint32_t(r) & ((1u << ds) - 1u), ds);
-            if (c == 0) continue;
-            const std::uint32_t f = (jl * c) << (m - h);
-            const float2 w = cmul(a.twa[f >> 12], a.twb[f & 4095u]);
-            v[r] = cmul(v[r], w);
+    static constexpr bool twiddled() {
+        return COL || window<P>() > 0;
+    }
+
+    // Level twiddle base of digit P for thread t: register r (digit output
+    // c = bitrev(r)) is multiplied by base^c, base = w^(j_low << (m - h)),
+    // j_low = the element's index bits below the digit, h = the digit's top
+    // bit + 1 (the four-step twiddle of that level). One table pair per
+    // thread and digit: w^f = A[f >> 12] * B[f & 4095].
+    template <int P>
+    static __device__ __forceinline__ float2 level_base(const FftArgs& a, std::uint32_t t, std::uint32_t c0,
+                                                        std::uint32_t m) {
+        if constexpr (!twiddled<P>()) {
+            return make_float2(1.f, 0.f);
+        } else {
+            constexpr int ws = window<P>(), ds = digit_bits<P>();
+            const std::uint32_t lo_rel = std::uint32_t(ws);
+            const std::uint32_t lo = COL ? a.l2 + lo_rel : lo_rel;
+            const std::uint32_t h = lo + ds;
+            const std::uint32_t i0 = phase_index<tile_window<P>()>(t, 0);
+            // Index bits below the digit: for columns, the low transform bits
+            // of the column index and the column; for rows, the low bits.
+            const std::uint32_t x0 = COL ? (i0 >> LI) : (i0 & ((1u << LT) - 1u));
+            std::uint32_t jl = x0 & ((1u << lo_rel) - 1u);
+            if (COL) jl = (jl << a.l2) | (c0 + (i0 & ((1u << LI) - 1u)));
+            const std::uint32_t f = jl << (m - h);
+            return cmul(a.twa[f >> 12], a.twb[f & 4095u]);
         }
+    }
+
+    // Digit P: codelet, then the level twiddle base^c on each register.
+    template <int P>
+    static __device__ __forceinline__ void digit(float2 (&v)[kE], float2 base) {
+        constexpr int ds = digit_bits<P>();
+        codelet<ds, INV>(v);
+        if constexpr (twiddled<P>()) {
+            // base^c for c = 1 .. 2^ds - 1, streamed: only base^1,2,3,4,8 stay
+            // live; every other power is one or two products of those (product
+            // depth <= 4), applied as soon as it is formed.
+            const float2 p1 = base;
+            const float2 p2 = ds > 1 ? cmul(p1, p1) : p1;
+            const float2 p3 = ds > 1 ? cmul(p2, p1) : p1;
+            const float2 p4 = ds > 2 ? cmul(p2, p2) : p1;
+            const float2 p8 = ds > 3 ? cmul(p4, p4) : p1;
+            apply_powers<0, ds>(v, p1, p2, p3, p4, p8);
+        }
+    }
+
+    // v[R] *= base^c, c = bitrev(R's digit bits) known at compile time; bits of
+    // R above the digit (only in a short last digit) are earlier digits.
+    template <int R, int DS>
+    static __device__ __forceinline__ void apply_powers(float2 (&v)[kE], float2 p1, float2 p2, float2 p3, float2 p4,
+                                                        float2 p8) {
+        constexpr int c = int(brev_const(std::uint32_t(R) & ((1u << DS) - 1u), DS));
+        if constexpr (c != 0) {
+            constexpr int lo = c & 7;
+            float2 w;
+            if constexpr (lo == 0) w = p8;
+            else if constexpr (lo == 1) w = p1;
+            else if constexpr (lo == 2) w = p2;
+            else if constexpr (lo == 3) w = p3;
+            else if constexpr (lo == 4) w = p4;
+            else if constexpr (lo == 5) w = cmul(p4, p1);
+            else if constexpr (lo == 6) w = cmul(p4, p2);
+            else w = cmul(p4, p3);
+            if constexpr (c > 8) w = cmul(p8, w);
+            v[R] = cmul(v[R], w);
+        }
+        if constexpr (R + 1 < kE) apply_powers<R + 1, DS>(v, p1, p2, p3, p4, p8);
     }
 
     template <int FROM, int TO>
@@ -199,68 +260,82 @@ struct FftPass {
         for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<TO>(t, r))];
     }
 
-    static __device__ void run(const FftArgs& a) {
-        extern __shared__ float2 lds[];
-        const std::uint32_t t = threadIdx.x;
-        const std::uint32_t m = a.l1 + a.l2;
-        const std::uint32_t b = blockIdx.x;
-        // XCD-contiguous tile order (tiles sharing cache lines meet in one L2).
-        const std::uint32_t tile = (a.tiles & 7u) == 0 && (gridDim.x & 7u) == 0
-                                       ? (b & 7u) * (a.tiles >> 3) + (b >> 3)
-                                       : b;
-        std::uint32_t row0 = 0, c0 = 0;
-        std::uint64_t base = 0;  // element offset of the tile's transform
-        const bool single = a.l1 == 0;
+    struct Tile {
+        std::uint32_t row0;  // ROW: first global row (= transform for one pass)
+        std::uint32_t c0;    // COL: first column
+        std::uint64_t base;  // COL: element offset of the tile's transform
+    };
+
+    static __device__ __forceinline__ Tile decode(const FftArgs& a, std::uint32_t tile, std::uint32_t m) {
+        Tile tl{};
         if constexpr (COL) {
             const std::uint32_t shift = a.l2 - LI;
-            const std::uint32_t poly = tile >> shift;
-            c0 = (tile & ((1u << shift) - 1u)) << LI;
-            base = std::uint64_t(poly) << m;
+            tl.c0 = (tile & ((1u << shift) - 1u)) << LI;
+            tl.base = std::uint64_t(tile >> shift) << m;
         } else {
-            row0 = tile << LI;  // global row (= transform for one pass)
+            tl.row0 = tile << LI;
         }
-        float2 v[kE];
+        return tl;
+    }
+
+    // Uniform base of the tile's span and the 32-bit element offset of tile
+    // element i on the natural (load) side.
+    static __device__ __forceinline__ std::uint64_t span_base(const FftArgs& a, const Tile& tl, std::uint32_t m) {
+        if constexpr (COL) return tl.base;
+        else if constexpr (SINGLE) return std::uint64_t(tl.row0) << LT;
+        else return std::uint64_t((tl.row0 >> LI) >> (a.l1 - LI)) << m;  // the transform of the tile's rows
+    }
+    static __device__ __forceinline__ std::uint32_t natural_offset(const FftArgs& a, const Tile& tl, std::uint32_t i) {
+        if constexpr (COL) {
+            return tl.c0 + (i & ((1u << LI) - 1u)) + ((i >> LI) << a.l2);
+        } else if constexpr (SINGLE) {
+            return i;  // rows are consecutive transforms of 2^LT points
+        } else {  // rows bitrev(k0 + rr) of one transform, matching the transposing store
+            const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
+            return (brev(k0 + (i >> LT), a.l1) << a.l2) + (i & ((1u << LT) - 1u));
+        }
+    }
+
+    static __device__ __forceinline__ void load(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
+                                                float2 (&v)[kE]) {
         constexpr int w0 = tile_window<0>();
+        const float2* __restrict__ src = a.in + span_base(a, tl, m);
 #pragma unroll
         for (int r = 0; r < kE; ++r) {
             const std::uint32_t i = phase_index<w0>(t, r);
-            std::uint64_t where;
-            bool ok = true;
-            if constexpr (COL) {
-                where = base + c0 + (i & ((1u << LI) - 1u)) + (std::uint64_t(i >> LI) << a.l2);
-            } else if (single) {
-                const std::uint32_t g = row0 + (i >> LT);
-                ok = g < a.rows;
-                where = (std::uint64_t(g) << a.l2) + (i & ((1u << LT) - 1u));
-            } else {  // rows bitrev(k0 + rr) of one transform, matching the transposing store
-                const std::uint32_t per = a.l1 - LI;
-                const std::uint32_t poly = (row0 >> LI) >> per;
-                const std::uint32_t k0 = row0 & ((1u << a.l1) - 1u);
-                const std::uint32_t row = brev(k0 + (i >> LT), a.l1);
-                where = (std::uint64_t(poly) << m) + (std::uint64_t(row) << a.l2) + (i & ((1u << LT) - 1u));
-            }
-            v[r] = ok ? a.in[where] : make_float2(0.f, 0.f);
+            const bool ok = !SINGLE || tl.row0 + (i >> LT) < a.rows;
+            v[r] = ok ? src[natural_offset(a, tl, i)] : make_float2(0.f, 0.f);
         }
-        digit<0>(v, a, t, c0, m);
+    }
+
+    static __device__ __forceinline__ void bases_of(float2 (&bs)[4], const FftArgs& a, std::uint32_t t,
+                                                    std::uint32_t c0, std::uint32_t m) {
+        bs[0] = level_base<0>(a, t, c0, m);
+        if constexpr (kPhases > 1) bs[1] = level_base<1>(a, t, c0, m);
+        if constexpr (kPhases > 2) bs[2] = level_base<2>(a, t, c0, m);
+        if constexpr (kPhases > 3) bs[3] = level_base<3>(a, t, c0, m);
+    }
+
+    static __device__ __forceinline__ void process(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
+                                                   float2 (&v)[kE], const float2 (&bs)[4], float2* lds) {
+        digit<0>(v, bs[0]);
         if constexpr (kPhases > 1) {
             exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
-            digit<1>(v, a, t, c0, m);
+            digit<1>(v, bs[1]);
         }
         if constexpr (kPhases > 2) {
             exchange<tile_window<1>(), tile_window<2>()>(v, lds, t);
-            digit<2>(v, a, t, c0, m);
+            digit<2>(v, bs[2]);
         }
         if constexpr (kPhases > 3) {
             exchange<tile_window<2>(), tile_window<3>()>(v, lds, t);
-            digit<3>(v, a, t, c0, m);
+            digit<3>(v, bs[3]);
         }
         constexpr int wl = tile_window<kPhases - 1>();
+        float2* __restrict__ dst = a.out + span_base(a, tl, m);
         if constexpr (COL) {  // intermediate: same positions
 #pragma unroll
-            for (int r = 0; r < kE; ++r) {
-                const std::uint32_t i = phase_index<wl>(t, r);
-                a.out[base + c0 + (i & ((1u << LI) - 1u)) + (std::uint64_t(i >> LI) << a.l2)] = v[r];
-            }
+            for (int r = 0; r < kE; ++r) dst[natural_offset(a, tl, phase_index<wl>(t, r))] = v[r];
             return;
         }
         // Final pass: bit-reversed positions -> natural order through LDS.
@@ -271,53 +346,113 @@ struct FftPass {
 #pragma unroll
         for (int r = 0; r < kE; ++r) {
             const std::uint32_t g = t + T * r;
-            std::uint32_t i;
-            std::uint64_t where;
+            std::uint32_t i, off;
             bool ok = true;
-            if (single) {  // rows are transforms: in-row bit reversal, lanes along the row
+            if constexpr (SINGLE) {  // rows are transforms: in-row bit reversal, lanes along the row
                 const std::uint32_t xp = g & ((1u << LT) - 1u), rr = g >> LT;
                 i = brev(xp, LT) | (rr << LT);
-                ok = row0 + rr < a.rows;
-                where = (std::uint64_t(row0 + rr) << LT) + xp;
+                ok = tl.row0 + rr < a.rows;
+                off = (rr << LT) + xp;
             } else {  // grid transpose: tile rows are bitrev(k0 + rr) of one transform
                 const std::uint32_t rr = g & ((1u << LI) - 1u), cp = g >> LI;
-                const std::uint32_t per = a.l1 - LI;  // tiles per transform = 2^per
-                const std::uint32_t poly = (row0 >> LI) >> per;
-                const std::uint32_t k0 = row0 & ((1u << a.l1) - 1u);
+                const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
                 i = brev(cp, LT) | (rr << LT);
-                where = (std::uint64_t(poly) << m) + (std::uint64_t(cp) << a.l1) + k0 + rr;
+                off = (cp << a.l1) + k0 + rr;
             }
             const float2 x = lds[L::addr(i)];
-            if (ok) a.out[where] = make_float2(x.x * a.scale, x.y * a.scale);
+            if (ok) dst[off] = make_float2(x.x * a.scale, x.y * a.scale);
+        }
+    }
+
+    // Persistent walk over tiles: the next tile's loads are issued before the
+    // current tile is processed, and no global load sits between them and
+    // their use (level-twiddle bases are fetched before the prefetch). When
+    // the tile count and the grid are multiples of 8, each XCD (blocks are
+    // dealt to the 8 XCDs round-robin) walks one contiguous range of tiles,
+    // so tiles sharing cache lines meet in one L2.
+    static __device__ void run(const FftArgs& a) {
+        extern __shared__ float2 lds[];
+        const std::uint32_t t = threadIdx.x;
+        const std::uint32_t m = a.l1 + a.l2;
+        const std::uint32_t grid = gridDim.x, b = blockIdx.x;
+        const bool xcd = (a.tiles & 7u) == 0 && (grid & 7u) == 0;
+        const std::uint32_t stride = xcd ? (grid >> 3) : grid;
+        const std::uint32_t range_base = xcd ? (b & 7u) * (a.tiles >> 3) : 0u;
+        const std::uint32_t range_end = xcd ? (a.tiles >> 3) : a.tiles;
+        std::uint32_t pos = xcd ? (b >> 3) : b;
+        if (pos >= range_end) return;
+        Tile tl = decode(a, range_base + pos, m);
+        float2 bs[4];
+        if constexpr (!COL) bases_of(bs, a, t, 0, m);  // row passes: the bases depend on the thread only
+        float2 v[kE];
+        load(a, tl, t, m, v);
+        if constexpr (!kPrefetch) {  // one tile per workgroup (the grid covers every tile)
+            if constexpr (COL) bases_of(bs, a, t, tl.c0, m);
+            process(a, tl, t, m, v, bs, lds);
+            return;
+        }
+        for (;;) {
+            // Per-thread addresses depend on t only; hiding t from the
+            // optimiser here keeps them from being hoisted out of the loop
+            // (and held in registers across it).
+            std::uint32_t tt = t;
+            asm volatile("" : "+v"(tt));
+            const std::uint32_t next = pos + stride;
+            const bool more = next < range_end;
+            if constexpr (COL) bases_of(bs, a, tt, tl.c0, m);
+            Tile tn{};
+            float2 nv[kE];
+            if (more) {
+                tn = decode(a, range_base + next, m);
+                load(a, tn, tt, m, nv);
+            }
+            process(a, tl, tt, m, v, bs, lds);
+            if (!more) break;
+            pos = next;
+            tl = tn;
+#pragma unroll
+            for (int r = 0; r < kE; ++r) v[r] = nv[r];
         }
     }
 };
 
-template <int LT, int LI, bool COL, bool INV>
-__global__ __launch_bounds__(1 << (LT + LI - kLE)) void fft_pass_kernel(FftArgs a) {
-    FftPass<LT, LI, COL, INV>::run(a);
+template <int LT, int LI, bool COL, bool SINGLE, bool INV>
+__global__ __launch_bounds__(1 << (LT + LI - kLE)) __attribute__((amdgpu_waves_per_eu(4)))
+void fft_pass_kernel(FftArgs a) {
+    FftPass<LT, LI, COL, SINGLE, INV>::run(a);
 }
 
-using Launch = void (*)(const FftArgs&, unsigned grid, hipStream_t);
+using Launch = void (*)(const FftArgs&, hipStream_t);
 
 struct Key {
     int lt, li;
-    bool col, inv;
-    bool operator<(const Key& o) const { return std::tie(lt, li, col, inv) < std::tie(o.lt, o.li, o.col, o.inv); }
+    bool col, single, inv;
+    bool operator<(const Key& o) const {
+        return std::tie(lt, li, col, single, inv) < std::tie(o.lt, o.li, o.col, o.single, o.inv);
+    }
 };
 
-template <int LT, int LI, bool COL, bool INV>
-void launch(const FftArgs& a, unsigned grid, hipStream_t stream) {
+// Prefetching passes run a persistent grid: as many workgroups as can be
+// resident (occupancy of this kernel with its LDS), at most one per tile, a
+// multiple of 8 when larger. Other passes launch one workgroup per tile.
+template <int LT, int LI, bool COL, bool SINGLE, bool INV>
+void launch(const FftArgs& a, hipStream_t stream) {
     constexpr std::uint32_t bytes = FftLds<COL, LT, LI>::kWords * sizeof(float2);
-    static const bool configured = [] {
-        if (bytes > 65536)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, INV>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
-        return true;
+    constexpr int threads = 1 << (LT + LI - kLE);
+    static const std::uint64_t resident = [] {
+        const void* fn = reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, SINGLE, INV>);
+        if (bytes > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, bytes) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        return std::uint64_t(per_cu) * std::uint64_t(device_cu_count());
     }();
-    (void)configured;
-    hipLaunchKernelGGL((fft_pass_kernel<LT, LI, COL, INV>), dim3(grid), dim3(1u << (LT + LI - kLE)), bytes, stream,
-                       a);
+    std::uint64_t grid = a.tiles;
+    if (FftPass<LT, LI, COL, SINGLE, INV>::kPrefetch) {
+        grid = std::min<std::uint64_t>(grid, resident);
+        if (grid > 8) grid &= ~std::uint64_t{7};
+    }
+    hipLaunchKernelGGL((fft_pass_kernel<LT, LI, COL, SINGLE, INV>), dim3(unsigned(grid)), dim3(threads), bytes, stream, a);
 }
 
 std::map<Key, Launch>& registry() {
@@ -325,10 +460,10 @@ std::map<Key, Launch>& registry() {
     return table;
 }
 
-template <int LT, int LI, bool COL>
+template <int LT, int LI, bool COL, bool SINGLE>
 void add() {
-    registry()[Key{LT, LI, COL, false}] = &launch<LT, LI, COL, false>;
-    registry()[Key{LT, LI, COL, true}] = &launch<LT, LI, COL, true>;
+    registry()[Key{LT, LI, COL, SINGLE, false}] = &launch<LT, LI, COL, SINGLE, false>;
+    registry()[Key{LT, LI, COL, SINGLE, true}] = &launch<LT, LI, COL, SINGLE, true>;
 }
 
 // Shapes: one pass for m <= 14 (2^12-point tiles, 2^14 for m = 13, 14);
@@ -339,25 +474,25 @@ void add_two() {
     constexpr int l1 = M / 2, l2 = M - l1;
     constexpr int col_li = 14 - l1 < l2 ? 14 - l1 : l2;
     constexpr int row_li = 14 - l2 < l1 ? 14 - l2 : l1;
-    add<l1, col_li, true>();
-    add<l2, row_li, false>();
+    add<l1, col_li, true, false>();
+    add<l2, row_li, false, false>();
 }
 
 void register_all() {
-    add<1, single_li(1), false>();
-    add<2, single_li(2), false>();
-    add<3, single_li(3), false>();
-    add<4, single_li(4), false>();
-    add<5, single_li(5), false>();
-    add<6, single_li(6), false>();
-    add<7, single_li(7), false>();
-    add<8, single_li(8), false>();
-    add<9, single_li(9), false>();
-    add<10, single_li(10), false>();
-    add<11, single_li(11), false>();
-    add<12, single_li(12), false>();
-    add<13, 0, false>();
-    add<14, 0, false>();
+    add<1, single_li(1), false, true>();
+    add<2, single_li(2), false, true>();
+    add<3, single_li(3), false, true>();
+    add<4, single_li(4), false, true>();
+    add<5, single_li(5), false, true>();
+    add<6, single_li(6), false, true>();
+    add<7, single_li(7), false, true>();
+    add<8, single_li(8), false, true>();
+    add<9, single_li(9), false, true>();
+    add<10, single_li(10), false, true>();
+    add<11, single_li(11), false, true>();
+    add<12, single_li(12), false, true>();
+    add<13, 0, false, true>();
+    add<14, 0, false, true>();
     add_two<15>();
     add_two<16>();
     add_two<17>();
@@ -403,7 +538,7 @@ class FftExecutor final : public Executor {
         if (m <= 14) {
             const int li = single_li(int(m));
             const std::uint64_t tiles = (r.batch + (1ull << li) - 1) >> li;
-            Step s{find(Key{int(m), li, false, r.inverse}), unsigned(tiles), base, false, false};
+            Step s{find(Key{int(m), li, false, true, r.inverse}), base, false, false};
             s.args.l1 = 0;
             s.args.l2 = m;
             s.args.rows = unsigned(r.batch);
@@ -417,13 +552,13 @@ class FftExecutor final : public Executor {
             const std::uint64_t col_tiles = r.batch << (l2 - col_li);
             const std::uint64_t row_tiles = r.batch << (l1 - row_li);
             require(col_tiles <= 0xffffffffull && row_tiles <= 0xffffffffull, "FFT batch exceeds the grid");
-            Step a{find(Key{int(l1), col_li, true, r.inverse}), unsigned(col_tiles), base, false, true};
+            Step a{find(Key{int(l1), col_li, true, false, r.inverse}), base, false, true};
             a.args.l1 = l1;
             a.args.l2 = l2;
             a.args.rows = unsigned(r.batch << l1);
             a.args.tiles = unsigned(col_tiles);
             a.args.scale = 1.0f;
-            Step b{find(Key{int(l2), row_li, false, r.inverse}), unsigned(row_tiles), base, true, false};
+            Step b{find(Key{int(l2), row_li, false, false, r.inverse}), base, true, false};
             b.args.l1 = l1;
             b.args.l2 = l2;
             b.args.rows = unsigned(r.batch << l1);
@@ -454,7 +589,7 @@ class FftExecutor final : public Executor {
             FftArgs a = s.args;
             a.in = static_cast<const float2*>(s.reads_ws ? ws : in);
             a.out = static_cast<float2*>(s.writes_ws ? ws : out);
-            s.fn(a, s.grid, stream);
+            s.fn(a, stream);
             hip_check(hipGetLastError(), "FFT pass launch");
         }
     }
@@ -462,7 +597,6 @@ class FftExecutor final : public Executor {
   private:
     struct Step {
         Launch fn;
-        unsigned grid;
         FftArgs args;
         bool reads_ws, writes_ws;
     };
