@@ -235,6 +235,15 @@ __device__ __forceinline__ void buffer_store(W x, __amdgpu_buffer_rsrc_t r, std:
     }
 }
 
+// Wave-uniform copies (readfirstlane returns int: go through uint32 so the
+// low half of a 64-bit value is not sign-extended).
+__device__ __forceinline__ std::uint32_t uniform(std::uint32_t x) {
+    return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+}
+__device__ __forceinline__ std::uint64_t uniform(std::uint64_t x) {
+    return (std::uint64_t(uniform(std::uint32_t(x >> 32))) << 32) | std::uint64_t(uniform(std::uint32_t(x)));
+}
+
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ std::uint32_t brev(std::uint32_t x, std::uint32_t bits) {
@@ -305,6 +314,10 @@ struct Pass {
     };
 
     static __device__ __forceinline__ Tile decode(const PassArgs<W>& a, std::uint32_t tile) {
+        // A tile is wave-uniform; saying so keeps its fields (and the buffer
+        // resources and domain record derived from them) in scalar registers
+        // inside the persistent loop.
+        tile = uniform(tile);
         Tile tl{};
         if constexpr (COL) {
             constexpr int shift = L2 - LI;
@@ -326,11 +339,12 @@ struct Pass {
     // polynomials (one-pass).
     static __device__ __forceinline__ __amdgpu_buffer_rsrc_t span(const W* base, const std::uint64_t* off,
                                                                   const Tile& tl) {
+        // Offsets are read back into scalar registers (see domain_of).
         if constexpr (SINGLE) {
-            if (off) return make_rsrc(base + off[tl.poly], kPolyBytes);
+            if (off) return make_rsrc(base + uniform(off[tl.poly]), kPolyBytes);
             return make_rsrc(base + (std::uint64_t(tl.poly) << kLogN), tl.lines * kPolyBytes);
         } else {
-            return make_rsrc(base + (off ? off[tl.poly] : std::uint64_t(tl.poly) << kLogN), kPolyBytes);
+            return make_rsrc(base + (off ? uniform(off[tl.poly]) : std::uint64_t(tl.poly) << kLogN), kPolyBytes);
         }
     }
 
@@ -460,56 +474,51 @@ struct Pass {
         for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<TO>(t, r))];
     }
 
-    static __device__ void run(const PassArgs<W>& a) {
-        __shared__ W lds[L::kWords];
-        const std::uint32_t t = threadIdx.x;
-        const std::uint32_t b = blockIdx.x;
-        // XCD-contiguous tile order: blocks are dealt to the 8 XCDs
-        // round-robin, so block b walks tile (b mod 8) * tiles/8 + b/8 and the
-        // tiles sharing cache lines and twiddle rows meet in one L2.
-        const std::uint32_t tile =
-            (a.tiles & 7u) == 0 && (gridDim.x & 7u) == 0 ? (b & 7u) * (a.tiles >> 3) + (b >> 3) : b;
-        const Tile tl = decode(a, tile);
-        // One domain per tile (the planner keeps mixed-domain tiles apart).
-        const std::uint32_t dom = a.poly_domain ? a.poly_domain[tl.poly] : 0u;
-        const DeviceDomain<W> d = a.domains[dom];
+    // The tile's 16 input words, raw (boundary permutation and reduction
+    // happen in process()).
+    static __device__ __forceinline__ void load_tile(const PassArgs<W>& a, const Tile& tl, std::uint32_t t,
+                                                     W (&v)[kE]) {
         const __amdgpu_buffer_rsrc_t src = span(a.in, a.in_off, tl);
-        const __amdgpu_buffer_rsrc_t dst = span(a.out, a.out_off, tl);
-        const __amdgpu_buffer_rsrc_t tw = make_rsrc(a.tw + d.tw, a.tw_bytes);
-
-        W v[kE];
-        if constexpr (PIN) {
-            W raw[kE];
 #pragma unroll
-            for (int r = 0; r < kE; ++r) {
-                std::uint32_t i, word;
+        for (int r = 0; r < kE; ++r) {
+            std::uint32_t i, word;
+            if constexpr (PIN) {
                 permuted(tl, t + T * r, i, word);
-                raw[r] = buffer_load<W>(src, word * std::uint32_t(sizeof(W)));
+            } else {
+                word = natural_word(tl, phase_index<tile_window<0>()>(t, r));
             }
+            v[r] = buffer_load<W>(src, word * std::uint32_t(sizeof(W)));
+        }
+    }
+
+    struct Chunks {
+        Chunk<0> c0;
+        Chunk<1> c1;
+        Chunk<2> c2;
+    };
+
+    static __device__ __forceinline__ void load_chunks(Chunks& c, const PassArgs<W>& a, const Tile& tl,
+                                                       std::uint32_t t, const DeviceDomain<W>& d) {
+        const __amdgpu_buffer_rsrc_t tw = make_rsrc(a.tw + d.tw, a.tw_bytes);
+        load_chunk<0>(c.c0, a, tl, t, tw);
+        load_chunk<1>(c.c1, a, tl, t, tw);
+        load_chunk<2>(c.c2, a, tl, t, tw);
+    }
+
+    static __device__ __forceinline__ void process(const PassArgs<W>& a, const Tile& tl, std::uint32_t t, W (&v)[kE],
+                                                   const Chunks& c, const DeviceDomain<W>& d, W* lds) {
+        if constexpr (PIN) {  // physical order -> phase-0 layout through LDS
             lds_barrier();
 #pragma unroll
             for (int r = 0; r < kE; ++r) {
                 std::uint32_t i, word;
                 permuted(tl, t + T * r, i, word);
-                lds[L::addr(i)] = raw[r];
+                lds[L::addr(i)] = v[r];
             }
             lds_barrier();
 #pragma unroll
             for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<tile_window<0>()>(t, r))];
-        } else {
-#pragma unroll
-            for (int r = 0; r < kE; ++r)
-                v[r] = buffer_load<W>(src, natural_word(tl, phase_index<tile_window<0>()>(t, r)) *
-                                               std::uint32_t(sizeof(W)));
         }
-        // Every phase's twiddles are requested up front, so no phase waits on
-        // a fresh load after an exchange.
-        Chunk<0> c0;
-        Chunk<1> c1;
-        Chunk<2> c2;
-        load_chunk<0>(c0, a, tl, t, tw);
-        load_chunk<1>(c1, a, tl, t, tw);
-        load_chunk<2>(c2, a, tl, t, tw);
         if (kFirst && a.reduce_input) {
             // Arbitrary input words -> [0, 2q). A Cooley-Tukey first stage
             // multiplies its upper operands by twiddles (any word is fine
@@ -519,15 +528,14 @@ struct Pass {
             for (int r = 0; r < kE; ++r)
                 if (!CT || LT < kLE || !((r >> top) & 1)) v[r] = shoup(v[r], W(1), d.rwp, d.q);
         }
-
-        stages<0>(v, c0, d);
+        stages<0>(v, c.c0, d);
         if constexpr (kPhases > 1) {
             exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
-            stages<1>(v, c1, d);
+            stages<1>(v, c.c1, d);
         }
         if constexpr (kPhases > 2) {
             exchange<tile_window<1>(), tile_window<2>()>(v, lds, t);
-            stages<2>(v, c2, d);
+            stages<2>(v, c.c2, d);
         }
         constexpr int wl = tile_window<kPhases - 1>();
         if constexpr (kLast) {
@@ -538,6 +546,7 @@ struct Pass {
                 v[r] = csub(x, d.q);
             }
         }
+        const __amdgpu_buffer_rsrc_t dst = span(a.out, a.out_off, tl);
         if constexpr (POUT) {
             lds_barrier();
 #pragma unroll
@@ -554,6 +563,43 @@ struct Pass {
             for (int r = 0; r < kE; ++r)
                 buffer_store<W>(v[r], dst, natural_word(tl, phase_index<wl>(t, r)) * std::uint32_t(sizeof(W)));
         }
+    }
+
+    // One domain per tile (the planner keeps mixed-domain tiles apart). The
+    // record is wave-uniform; it comes back through vector loads (the
+    // kernel's stores could alias it as far as the compiler knows), so each
+    // field is read back into a scalar register.
+    static __device__ __forceinline__ DeviceDomain<W> domain_of(const PassArgs<W>& a, const Tile& tl) {
+        const std::uint32_t dom = a.poly_domain ? uniform(a.poly_domain[tl.poly]) : 0u;
+        const DeviceDomain<W> d = a.domains[dom];
+        DeviceDomain<W> u;
+        u.q = uniform(d.q);
+        u.q2 = uniform(d.q2);
+        u.rwp = uniform(d.rwp);
+        u.ninv = {uniform(d.ninv.w), uniform(d.ninv.wp)};
+        u.last = {uniform(d.last.w), uniform(d.last.wp)};
+        u.tw = uniform(d.tw);
+        return u;
+    }
+
+    // One tile per workgroup. (Every tile of a 2^16 x 64 pass is resident at
+    // once on 256 CUs; persistent prefetching variants measured slower.)
+    static __device__ void run(const PassArgs<W>& a) {
+        __shared__ W lds[L::kWords];
+        const std::uint32_t t = threadIdx.x;
+        const std::uint32_t b = blockIdx.x;
+        // XCD-contiguous tile order: blocks are dealt to the 8 XCDs
+        // round-robin, so block b walks tile (b mod 8) * tiles/8 + b/8 and the
+        // tiles sharing cache lines and twiddle rows meet in one L2.
+        const std::uint32_t tile =
+            (a.tiles & 7u) == 0 && (gridDim.x & 7u) == 0 ? (b & 7u) * (a.tiles >> 3) + (b >> 3) : b;
+        const Tile tl = decode(a, tile);
+        W v[kE];
+        load_tile(a, tl, t, v);
+        const DeviceDomain<W> d = domain_of(a, tl);
+        Chunks c;
+        load_chunks(c, a, tl, t, d);
+        process(a, tl, t, v, c, d, lds);
     }
 };
 
