@@ -42,8 +42,7 @@ std::map<PassKey, PassLaunch<std::uint64_t>>& registry<std::uint64_t>() {
 namespace {
 using namespace ntt_detail;
 
-template <class W>
-PassLaunch<W> find_pass(const PassKey& key) {
+void ensure_registered() {
     static const bool once = [] {
         register_u32_lazy();
         register_u32_strict();
@@ -52,6 +51,11 @@ PassLaunch<W> find_pass(const PassKey& key) {
         return true;
     }();
     (void)once;
+}
+
+template <class W>
+PassLaunch<W> find_pass(const PassKey& key) {
+    ensure_registered();
     auto it = registry<W>().find(key);
     if (it == registry<W>().end()) throw NotSupported("NTT pass shape has no gfx950 kernel");
     return it->second;

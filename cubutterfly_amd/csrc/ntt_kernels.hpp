@@ -582,24 +582,30 @@ struct Pass {
         return u;
     }
 
-    // One tile per workgroup. (Every tile of a 2^16 x 64 pass is resident at
-    // once on 256 CUs; persistent prefetching variants measured slower.)
-    static __device__ void run(const PassArgs<W>& a) {
-        __shared__ W lds[L::kWords];
+    // One tile: its words, its twiddle chunks, the butterflies and the
+    // store. `lds` holds at least L::kWords words.
+    static __device__ __forceinline__ void tile(const PassArgs<W>& a, std::uint32_t index, W* lds) {
         const std::uint32_t t = threadIdx.x;
-        const std::uint32_t b = blockIdx.x;
-        // XCD-contiguous tile order: blocks are dealt to the 8 XCDs
-        // round-robin, so block b walks tile (b mod 8) * tiles/8 + b/8 and the
-        // tiles sharing cache lines and twiddle rows meet in one L2.
-        const std::uint32_t tile =
-            (a.tiles & 7u) == 0 && (gridDim.x & 7u) == 0 ? (b & 7u) * (a.tiles >> 3) + (b >> 3) : b;
-        const Tile tl = decode(a, tile);
+        const Tile tl = decode(a, index);
         W v[kE];
         load_tile(a, tl, t, v);
         const DeviceDomain<W> d = domain_of(a, tl);
         Chunks c;
         load_chunks(c, a, tl, t, d);
         process(a, tl, t, v, c, d, lds);
+    }
+
+    // One tile per workgroup. (Every tile of a 2^16 x 64 pass is resident at
+    // once on 256 CUs; persistent prefetching variants measured slower.)
+    static __device__ void run(const PassArgs<W>& a) {
+        __shared__ W lds[L::kWords];
+        const std::uint32_t b = blockIdx.x;
+        // XCD-contiguous tile order: blocks are dealt to the 8 XCDs
+        // round-robin, so block b walks tile (b mod 8) * tiles/8 + b/8 and the
+        // tiles sharing cache lines and twiddle rows meet in one L2.
+        const std::uint32_t index =
+            (a.tiles & 7u) == 0 && (gridDim.x & 7u) == 0 ? (b & 7u) * (a.tiles >> 3) + (b >> 3) : b;
+        tile(a, index, lds);
     }
 };
 
