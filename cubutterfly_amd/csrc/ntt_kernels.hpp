@@ -212,26 +212,31 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, st
                                              kBufferWord3);
 }
 
+// byte_off: per-lane offset; scalar_off: a wave-uniform offset carried in
+// the instruction's scalar operand (outside the range check: callers use it
+// only where every access lies inside the resource's range).
 template <class W>
-__device__ __forceinline__ W buffer_load(__amdgpu_buffer_rsrc_t r, std::uint32_t byte_off) {
+__device__ __forceinline__ W buffer_load(__amdgpu_buffer_rsrc_t r, std::uint32_t byte_off, std::uint32_t scalar_off = 0) {
     if constexpr (sizeof(W) == 4) {
-        return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(byte_off), 0, 0);
+        return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0);
     } else {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), 0, 0);
+        const auto v =
+            __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0);
         return (std::uint64_t(v[1]) << 32) | v[0];
     }
 }
 
 template <class W>
-__device__ __forceinline__ void buffer_store(W x, __amdgpu_buffer_rsrc_t r, std::uint32_t byte_off) {
+__device__ __forceinline__ void buffer_store(W x, __amdgpu_buffer_rsrc_t r, std::uint32_t byte_off,
+                                             std::uint32_t scalar_off = 0) {
     if constexpr (sizeof(W) == 4) {
-        __builtin_amdgcn_raw_buffer_store_b32(x, r, static_cast<int>(byte_off), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(x, r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0);
     } else {
         using V2 = __attribute__((ext_vector_type(2))) std::uint32_t;
         V2 v;
         v[0] = static_cast<std::uint32_t>(x);
         v[1] = static_cast<std::uint32_t>(x >> 32);
-        __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(byte_off), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0);
     }
 }
 
@@ -262,6 +267,9 @@ __device__ __forceinline__ std::uint32_t phase_index(std::uint32_t t, std::uint3
 // bit-reversed order, which a plain stride maps onto few banks).
 template <bool COL, bool SWZ, int LT, int LI>
 struct Lds {
+    // Without the swizzle, addr() is a sum of terms over disjoint index bit
+    // fields, so addr(a | b) = addr(a) + addr(b) for disjoint a, b.
+    static constexpr bool kLinear = !(COL && SWZ);
     static constexpr std::uint32_t kWords =
         COL ? (1u << LT) * ((1u << LI) + 1u) : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
     static __device__ __forceinline__ std::uint32_t addr(std::uint32_t i) {
@@ -277,6 +285,13 @@ struct Lds {
             const std::uint32_t x = i & ((1u << LT) - 1u), rr = i >> LT;
             return rr * ((1u << LT) + (1u << LT >> 4) + 1u) + x + (x >> 4);
         }
+    }
+    // Address of element phase_index<S>(t, r): a per-thread base plus a
+    // compile-time offset per register where the layout is linear.
+    template <int S>
+    static __device__ __forceinline__ std::uint32_t at(std::uint32_t t, int r) {
+        if constexpr (kLinear) return addr(phase_index<S>(t, 0)) + addr(phase_index<S>(0, std::uint32_t(r)));
+        else return addr(phase_index<S>(t, std::uint32_t(r)));
     }
 };
 
@@ -368,6 +383,36 @@ struct Pass {
         }
     }
 
+    // natural_word of element phase_index<S>(t, r) as a per-thread word plus
+    // a per-register word: every natural_word layout is a sum of terms over
+    // disjoint index bit fields (row bit reversal included, as k0 is a
+    // multiple of 2^LI), and the tile's own origin sits in the thread part.
+    template <int S>
+    static __device__ __forceinline__ std::uint32_t thread_word(const Tile& tl, std::uint32_t t) {
+        return natural_word(tl, phase_index<S>(t, 0));
+    }
+    template <int S>
+    static __device__ __forceinline__ std::uint32_t register_word(int r) {
+        return natural_word(Tile{}, phase_index<S>(0, std::uint32_t(r)));
+    }
+
+    // Access of the word at lane_bytes + reg_bytes (reg_bytes compile-time
+    // per register). Small register offsets stay in the lane offset, where
+    // they fold into the instruction's immediate and neighbouring registers
+    // merge into wide accesses; large ones go to the scalar offset. A
+    // one-pass tile may be partial and relies on the range check, which
+    // sees only the lane offset, so it never uses the scalar offset.
+    static __device__ __forceinline__ W load_at(__amdgpu_buffer_rsrc_t src, std::uint32_t lane_bytes,
+                                                std::uint32_t reg_bytes) {
+        if (SINGLE || reg_bytes < 4096u) return buffer_load<W>(src, lane_bytes + reg_bytes);
+        return buffer_load<W>(src, lane_bytes, reg_bytes);
+    }
+    static __device__ __forceinline__ void store_at(W x, __amdgpu_buffer_rsrc_t dst, std::uint32_t lane_bytes,
+                                                    std::uint32_t reg_bytes) {
+        if (SINGLE || reg_bytes < 4096u) buffer_store<W>(x, dst, lane_bytes + reg_bytes);
+        else buffer_store<W>(x, dst, lane_bytes, reg_bytes);
+    }
+
     // Staged (permuted) enumeration: element g of the tile in physical
     // contiguity order -> (tile index i, word relative to the span).
     static __device__ __forceinline__ void permuted(const Tile& tl, std::uint32_t g, std::uint32_t& i,
@@ -385,6 +430,31 @@ struct Pass {
             i = brev(cp, LT) | (rr << LT);
             word = (cp << L1) + tl.k0 + rr;
         }
+    }
+
+    // permuted() of g = t + T * r, split like thread_word / register_word:
+    // each output is a sum over disjoint bit fields of g, and the tile origin
+    // enters only through the thread part.
+    struct Staged {
+        std::uint32_t i, word;  // thread part
+        std::uint32_t lds;      // LDS address of the thread part (linear layouts)
+    };
+    static __device__ __forceinline__ Staged staged_base(const Tile& tl, std::uint32_t t) {
+        Staged b;
+        permuted(tl, t, b.i, b.word);
+        b.lds = L::addr(b.i);
+        return b;
+    }
+    static __device__ __forceinline__ std::uint32_t staged_lds(const Staged& b, int r) {
+        std::uint32_t i, word;
+        permuted(Tile{}, T * std::uint32_t(r), i, word);
+        if constexpr (L::kLinear) return b.lds + L::addr(i);
+        else return L::addr(b.i + i);
+    }
+    static __device__ __forceinline__ std::uint32_t staged_word(int r) {
+        std::uint32_t i, word;
+        permuted(Tile{}, T * std::uint32_t(r), i, word);
+        return word;
     }
 
     // Block index of this thread's phase-P twiddle chunk.
@@ -468,10 +538,10 @@ struct Pass {
     static __device__ __forceinline__ void exchange(W (&v)[kE], W* lds, std::uint32_t t) {
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kE; ++r) lds[L::addr(phase_index<FROM>(t, r))] = v[r];
+        for (int r = 0; r < kE; ++r) lds[L::template at<FROM>(t, r)] = v[r];
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<TO>(t, r))];
+        for (int r = 0; r < kE; ++r) v[r] = lds[L::template at<TO>(t, r)];
     }
 
     // The tile's 16 input words, raw (boundary permutation and reduction
@@ -479,15 +549,13 @@ struct Pass {
     static __device__ __forceinline__ void load_tile(const PassArgs<W>& a, const Tile& tl, std::uint32_t t,
                                                      W (&v)[kE]) {
         const __amdgpu_buffer_rsrc_t src = span(a.in, a.in_off, tl);
+        constexpr int S = tile_window<0>();
+        constexpr std::uint32_t B = sizeof(W);
+        const std::uint32_t tw = PIN ? staged_base(tl, t).word : thread_word<S>(tl, t);
 #pragma unroll
         for (int r = 0; r < kE; ++r) {
-            std::uint32_t i, word;
-            if constexpr (PIN) {
-                permuted(tl, t + T * r, i, word);
-            } else {
-                word = natural_word(tl, phase_index<tile_window<0>()>(t, r));
-            }
-            v[r] = buffer_load<W>(src, word * std::uint32_t(sizeof(W)));
+            const std::uint32_t rw = PIN ? staged_word(r) : register_word<S>(r);
+            v[r] = load_at(src, tw * B, rw * B);
         }
     }
 
@@ -509,15 +577,12 @@ struct Pass {
                                                    const Chunks& c, const DeviceDomain<W>& d, W* lds) {
         if constexpr (PIN) {  // physical order -> phase-0 layout through LDS
             lds_barrier();
+            const Staged b = staged_base(tl, t);
 #pragma unroll
-            for (int r = 0; r < kE; ++r) {
-                std::uint32_t i, word;
-                permuted(tl, t + T * r, i, word);
-                lds[L::addr(i)] = v[r];
-            }
+            for (int r = 0; r < kE; ++r) lds[staged_lds(b, r)] = v[r];
             lds_barrier();
 #pragma unroll
-            for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<tile_window<0>()>(t, r))];
+            for (int r = 0; r < kE; ++r) v[r] = lds[L::template at<tile_window<0>()>(t, r)];
         }
         if (kFirst && a.reduce_input) {
             // Arbitrary input words -> [0, 2q). A Cooley-Tukey first stage
@@ -550,18 +615,19 @@ struct Pass {
         if constexpr (POUT) {
             lds_barrier();
 #pragma unroll
-            for (int r = 0; r < kE; ++r) lds[L::addr(phase_index<wl>(t, r))] = v[r];
+            for (int r = 0; r < kE; ++r) lds[L::template at<wl>(t, r)] = v[r];
             lds_barrier();
+            constexpr std::uint32_t B = sizeof(W);
+            const Staged b = staged_base(tl, t);
 #pragma unroll
             for (int r = 0; r < kE; ++r) {
-                std::uint32_t i, word;
-                permuted(tl, t + T * r, i, word);
-                buffer_store<W>(lds[L::addr(i)], dst, word * std::uint32_t(sizeof(W)));
+                store_at(lds[staged_lds(b, r)], dst, b.word * B, staged_word(r) * B);
             }
         } else {
+            constexpr std::uint32_t B = sizeof(W);
+            const std::uint32_t tw = thread_word<wl>(tl, t);
 #pragma unroll
-            for (int r = 0; r < kE; ++r)
-                buffer_store<W>(v[r], dst, natural_word(tl, phase_index<wl>(t, r)) * std::uint32_t(sizeof(W)));
+            for (int r = 0; r < kE; ++r) store_at(v[r], dst, tw * B, register_word<wl>(r) * B);
         }
     }
 
