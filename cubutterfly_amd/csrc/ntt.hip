@@ -222,15 +222,18 @@ struct EngineImplT {
         for (const auto& d : c.domains) {
             const std::uint64_t q = d.modulus;
             const std::uint64_t root = c.inverse ? invmod(d.root, q) : d.root;
-            const auto table = make_table<W>(log_n, q, root, c.negacyclic);
+            auto table = make_table<W>(log_n, q, root, c.negacyclic);
             DeviceDomain<W> dd{};
             dd.q = W(q);
             dd.q2 = W(2 * q);
+            dd.nq = W(0) - W(q);
             dd.rwp = shoup_factor<W>(1, q);
             const std::uint64_t ninv = invmod(n % q, q);
             dd.ninv = {W(ninv), shoup_factor<W>(ninv, q)};
             const std::uint64_t last = mulmod(table[1].w, ninv, q);
             dd.last = {W(last), shoup_factor<W>(last, q)};
+            if (ct && lazy)  // lazy Cooley-Tukey butterflies take -w (ct_butterfly)
+                for (auto& e : table) e.w = W(0) - e.w;
             dd.tw = all_tables.size();
             for (auto& L : launches)
                 append_pass_chunks<W>(all_tables, std::size_t(dd.tw), table, L.lt, L.prefix_bits, ct, L.last,

@@ -33,6 +33,8 @@ namespace ntt_detail {
 constexpr int kLE = 4;
 constexpr int kE = 1 << kLE;
 
+// A twiddle and its Shoup factor floor(w 2^k / q). Tables of lazy
+// Cooley-Tukey passes hold -w mod 2^k in place of w (see ct_butterfly).
 template <class W>
 struct alignas(2 * sizeof(W)) TwPair {
     W w, wp;
@@ -40,7 +42,7 @@ struct alignas(2 * sizeof(W)) TwPair {
 
 template <class W>
 struct DeviceDomain {
-    W q, q2, rwp;         // modulus, 2q, floor(2^k / q) (Shoup factor of 1)
+    W q, q2, nq, rwp;     // modulus, 2q, -q mod 2^k, floor(2^k / q) (Shoup factor of 1)
     TwPair<W> ninv;       // n^-1 with its Shoup factor
     TwPair<W> last;       // Tinv[1] * n^-1 (final inverse stage)
     std::uint64_t tw;     // offset of this domain's chunk tables in PassArgs::tw (TwPairs)
@@ -151,42 +153,55 @@ __device__ __forceinline__ std::uint64_t mulhi(std::uint64_t a, std::uint64_t b)
 __device__ __forceinline__ std::uint32_t csub(std::uint32_t x, std::uint32_t m) { return min(x, x - m); }
 __device__ __forceinline__ std::uint64_t csub(std::uint64_t x, std::uint64_t m) { return x >= m ? x - m : x; }
 
-template <class W>
-__device__ __forceinline__ W shoup(W a, W w, W wp, W q) {
-    return a * w - mulhi(a, wp) * q;  // [0, 2q) for any a
+// (a b + c) mod 2^k as one multiply-add (v_mad_u64_u32 for 32-bit words,
+// where a 32-bit multiply and a separate add would take two instructions).
+__device__ __forceinline__ std::uint32_t mul_add(std::uint32_t a, std::uint32_t b, std::uint32_t c) {
+    return static_cast<std::uint32_t>(std::uint64_t(a) * b + c);
 }
-// -(shoup(a, w, wp, q)) modulo the word: lets the butterfly fold the sign
-// into one three-input add.
-template <class W>
-__device__ __forceinline__ W neg_shoup(W a, W w, W wp, W q) {
-    return mulhi(a, wp) * q - a * w;
+__device__ __forceinline__ std::uint64_t mul_add(std::uint64_t a, std::uint64_t b, std::uint64_t c) {
+    return a * b + c;
 }
 
+// Shoup: a w - floor(a wp / 2^k) q, in [0, 2q) for any word a; written with
+// nq = -q so the subtraction folds into the multiply-add.
+template <class W>
+__device__ __forceinline__ W shoup(W a, W w, W wp, W nq) {
+    return mul_add(mulhi(a, wp), nq, a * w);
+}
+// -shoup(a, w, ...) modulo the word, from nw = -w: the lazy butterfly then
+// folds the sign into its subtraction and three-input add.
+template <class W>
+__device__ __forceinline__ W neg_shoup(W a, W nw, W wp, W q) {
+    return mul_add(mulhi(a, wp), q, a * nw);
+}
+
+// Lazy: x, y in [0, 4q) -> [0, 4q), table entries hold -w. Strict: [0, 2q)
+// -> [0, 2q), entries hold w.
 template <class W, bool LAZY>
-__device__ __forceinline__ void ct_butterfly(W& x, W& y, TwPair<W> t, W q, W q2) {
-    if constexpr (LAZY) {  // x, y in [0, 4q)
-        const W u = csub(x, q2);
-        const W nv = neg_shoup(y, t.w, t.wp, q);  // -v, v in [0, 2q)
+__device__ __forceinline__ void ct_butterfly(W& x, W& y, TwPair<W> t, const DeviceDomain<W>& d) {
+    if constexpr (LAZY) {
+        const W u = csub(x, d.q2);
+        const W nv = neg_shoup(y, t.w, t.wp, d.q);  // -v, v in [0, 2q)
         x = u - nv;
-        y = u + q2 + nv;
-    } else {  // x, y in [0, 2q)
-        const W u = csub(x, q);
-        const W v = csub(shoup(y, t.w, t.wp, q), q);
+        y = u + d.q2 + nv;
+    } else {
+        const W u = csub(x, d.q);
+        const W v = csub(shoup(y, t.w, t.wp, d.nq), d.q);
         x = u + v;
-        y = u - v + q;
+        y = u - v + d.q;
     }
 }
 
 template <class W, bool LAZY>
-__device__ __forceinline__ void gs_butterfly(W& x, W& y, TwPair<W> t, W q, W q2) {
+__device__ __forceinline__ void gs_butterfly(W& x, W& y, TwPair<W> t, const DeviceDomain<W>& d) {
     if constexpr (LAZY) {  // x, y in [0, 2q)
         const W u = x, v = y;
-        x = csub(u + v, q2);
-        y = shoup(u - v + q2, t.w, t.wp, q);
+        x = csub(u + v, d.q2);
+        y = shoup(u - v + d.q2, t.w, t.wp, d.nq);
     } else {
-        const W u = csub(x, q), v = csub(y, q);
+        const W u = csub(x, d.q), v = csub(y, d.q);
         x = u + v;
-        y = shoup(u - v + q, t.w, t.wp, q);
+        y = shoup(u - v + d.q, t.w, t.wp, d.nq);
     }
 }
 
@@ -199,8 +214,8 @@ __device__ __forceinline__ void gs_scale_butterfly(W& x, W& y, const DeviceDomai
         v = csub(v, d.q);
     }
     const W span = LAZY ? d.q2 : d.q;
-    x = shoup(u + v, d.ninv.w, d.ninv.wp, d.q);
-    y = shoup(u - v + span, d.last.w, d.last.wp, d.q);
+    x = shoup(u + v, d.ninv.w, d.ninv.wp, d.nq);
+    y = shoup(u - v + span, d.last.w, d.last.wp, d.nq);
 }
 
 // ---- buffer access ----------------------------------------------------------
@@ -523,11 +538,11 @@ struct Pass {
                     const int r = (g << (jb + 1)) | lo;
                     const int r2 = r | (1 << jb);
                     if constexpr (CT) {
-                        ct_butterfly<W, LAZY>(v[r], v[r2], tp, d.q, d.q2);
+                        ct_butterfly<W, LAZY>(v[r], v[r2], tp, d);
                     } else if (scale) {
                         gs_scale_butterfly<W, LAZY>(v[r], v[r2], d);
                     } else {
-                        gs_butterfly<W, LAZY>(v[r], v[r2], tp, d.q, d.q2);
+                        gs_butterfly<W, LAZY>(v[r], v[r2], tp, d);
                     }
                 }
             }
@@ -591,7 +606,7 @@ struct Pass {
             constexpr int top = CT ? stage_hi(LT, CT, 0) - window_start(LT, CT, 0) : kLE;
 #pragma unroll
             for (int r = 0; r < kE; ++r)
-                if (!CT || LT < kLE || !((r >> top) & 1)) v[r] = shoup(v[r], W(1), d.rwp, d.q);
+                if (!CT || LT < kLE || !((r >> top) & 1)) v[r] = shoup(v[r], W(1), d.rwp, d.nq);
         }
         stages<0>(v, c.c0, d);
         if constexpr (kPhases > 1) {
@@ -641,6 +656,7 @@ struct Pass {
         DeviceDomain<W> u;
         u.q = uniform(d.q);
         u.q2 = uniform(d.q2);
+        u.nq = uniform(d.nq);
         u.rwp = uniform(d.rwp);
         u.ninv = {uniform(d.ninv.w), uniform(d.ninv.wp)};
         u.last = {uniform(d.last.w), uniform(d.last.wp)};
