@@ -241,17 +241,18 @@ __device__ __forceinline__ W buffer_load(__amdgpu_buffer_rsrc_t r, std::uint32_t
     }
 }
 
-template <class W>
+// AUX: the instruction's cache-policy bits.
+template <class W, int AUX = 0>
 __device__ __forceinline__ void buffer_store(W x, __amdgpu_buffer_rsrc_t r, std::uint32_t byte_off,
                                              std::uint32_t scalar_off = 0) {
     if constexpr (sizeof(W) == 4) {
-        __builtin_amdgcn_raw_buffer_store_b32(x, r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0);
+        __builtin_amdgcn_raw_buffer_store_b32(x, r, static_cast<int>(byte_off), static_cast<int>(scalar_off), AUX);
     } else {
         using V2 = __attribute__((ext_vector_type(2))) std::uint32_t;
         V2 v;
         v[0] = static_cast<std::uint32_t>(x);
         v[1] = static_cast<std::uint32_t>(x >> 32);
-        __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0);
+        __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(byte_off), static_cast<int>(scalar_off), AUX);
     }
 }
 
@@ -328,6 +329,12 @@ struct Pass {
     static constexpr bool kPermRows = !COL && !SINGLE && (PIN || POUT);
     static constexpr std::uint32_t kPolyBytes = std::uint32_t(sizeof(W)) << kLogN;
     using L = Lds<COL, COL && (PIN || POUT), LT, LI>;
+    // Stores of two-pass inverse (Gentleman-Sande) tiles write through the L2
+    // (sc0 sc1), so the end-of-kernel write-back has little left to flush;
+    // measured 5-6% faster per C2 / C4 step. Forward passes keep write-back
+    // stores: write-through made them slower (partial-line segments that
+    // the L2 would otherwise merge).
+    static constexpr int kStoreAux = (!CT && !SINGLE) ? 17 : 0;
     static_assert(SINGLE ? (L1 == 0 && L2 == LT) : (COL ? LT == L1 : LT == L2), "pass bits");
     static_assert(LT >= 1 && LB >= kLE && LB <= 12, "tile shape");
 
@@ -424,8 +431,8 @@ struct Pass {
     }
     static __device__ __forceinline__ void store_at(W x, __amdgpu_buffer_rsrc_t dst, std::uint32_t lane_bytes,
                                                     std::uint32_t reg_bytes) {
-        if (SINGLE || reg_bytes < 4096u) buffer_store<W>(x, dst, lane_bytes + reg_bytes);
-        else buffer_store<W>(x, dst, lane_bytes, reg_bytes);
+        if (SINGLE || reg_bytes < 4096u) buffer_store<W, kStoreAux>(x, dst, lane_bytes + reg_bytes);
+        else buffer_store<W, kStoreAux>(x, dst, lane_bytes, reg_bytes);
     }
 
     // Staged (permuted) enumeration: element g of the tile in physical
