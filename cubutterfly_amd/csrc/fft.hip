@@ -16,6 +16,7 @@
 // Lengths <= 2^14 run in one pass; up to 2^24 in two.
 #include <hip/hip_runtime.h>
 
+#include "buffer.hpp"
 #include "json.hpp"
 #include "planner.hpp"
 
@@ -136,6 +137,10 @@ __device__ __forceinline__ void codelet(float2 (&v)[kE]) {
 // Padded LDS image (8-byte complex words), as in the NTT tiles.
 template <bool COL, int LT, int LI>
 struct FftLds {
+    // The row layout is a sum of terms over disjoint index bit fields, so
+    // addr(a | b) = addr(a) + addr(b) for disjoint a, b; the column layout's
+    // swizzle is not.
+    static constexpr bool kLinear = !COL;
     static constexpr std::uint32_t kWords =
         COL ? (1u << LT) * ((1u << LI) + 1u) : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
     static __device__ __forceinline__ std::uint32_t addr(std::uint32_t i) {
@@ -146,6 +151,11 @@ struct FftLds {
             const std::uint32_t x = i & ((1u << LT) - 1u), rr = i >> LT;
             return rr * ((1u << LT) + (1u << LT >> 4) + 1u) + x + (x >> 4);
         }
+    }
+    // addr(it | ir) for disjoint thread and register parts.
+    static __device__ __forceinline__ std::uint32_t split(std::uint32_t it, std::uint32_t ir) {
+        if constexpr (kLinear) return addr(it) + addr(ir);
+        else return addr(it | ir);
     }
 };
 
@@ -205,7 +215,8 @@ struct FftPass {
             std::uint32_t jl = x0 & ((1u << lo_rel) - 1u);
             if (COL) jl = (jl << a.l2) | (c0 + (i0 & ((1u << LI) - 1u)));
             const std::uint32_t f = jl << (m - h);
-            return cmul(a.twa[f >> 12], a.twb[f & 4095u]);
+            const __amdgpu_buffer_rsrc_t ta = make_rsrc(a.twa, 4096u * 8u), tb = make_rsrc(a.twb, 4096u * 8u);
+            return cmul(buffer_load<float2>(ta, (f >> 12) * 8u), buffer_load<float2>(tb, (f & 4095u) * 8u));
         }
     }
 
@@ -254,10 +265,10 @@ struct FftPass {
     static __device__ __forceinline__ void exchange(float2 (&v)[kE], float2* lds, std::uint32_t t) {
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kE; ++r) lds[L::addr(phase_index<FROM>(t, r))] = v[r];
+        for (int r = 0; r < kE; ++r) lds[L::split(phase_index<FROM>(t, 0), phase_index<FROM>(0, r))] = v[r];
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = lds[L::addr(phase_index<TO>(t, r))];
+        for (int r = 0; r < kE; ++r) v[r] = lds[L::split(phase_index<TO>(t, 0), phase_index<TO>(0, r))];
     }
 
     struct Tile {
@@ -296,16 +307,37 @@ struct FftPass {
         }
     }
 
+    // Bytes of the tile's span: a one-pass tile's existing rows (the range
+    // check zero-fills loads and drops stores past them), else its transform.
+    static __device__ __forceinline__ std::uint32_t span_bytes(const FftArgs& a, const Tile& tl, std::uint32_t m) {
+        if constexpr (SINGLE) return min(1u << LI, a.rows - tl.row0) << (LT + 3);
+        else return 8u << m;
+    }
+
+    // Element offsets split into a per-thread part and a wave-uniform
+    // per-register part: natural_offset is a sum over disjoint index bit
+    // fields (row bit reversal included, as k0 is a multiple of 2^LI), and
+    // the tile origin enters only the thread part. A partial one-pass tile
+    // keeps the whole offset in the lane offset, which the range check sees.
+    static constexpr bool kLaneOnly = SINGLE && LI > 0;
+    static __device__ __forceinline__ float2 load_at(__amdgpu_buffer_rsrc_t src, std::uint32_t lane_bytes,
+                                                     std::uint32_t reg_bytes) {
+        if (kLaneOnly || reg_bytes < 4096u) return buffer_load<float2>(src, lane_bytes + reg_bytes);
+        return buffer_load<float2>(src, lane_bytes, reg_bytes);
+    }
+    static __device__ __forceinline__ void store_at(float2 x, __amdgpu_buffer_rsrc_t dst, std::uint32_t lane_bytes,
+                                                    std::uint32_t reg_bytes) {
+        if (kLaneOnly || reg_bytes < 4096u) buffer_store<float2>(x, dst, lane_bytes + reg_bytes);
+        else buffer_store<float2>(x, dst, lane_bytes, reg_bytes);
+    }
+
     static __device__ __forceinline__ void load(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
                                                 float2 (&v)[kE]) {
         constexpr int w0 = tile_window<0>();
-        const float2* __restrict__ src = a.in + span_base(a, tl, m);
+        const __amdgpu_buffer_rsrc_t src = make_rsrc(a.in + span_base(a, tl, m), span_bytes(a, tl, m));
+        const std::uint32_t tb = natural_offset(a, tl, phase_index<w0>(t, 0)) * 8u;
 #pragma unroll
-        for (int r = 0; r < kE; ++r) {
-            const std::uint32_t i = phase_index<w0>(t, r);
-            const bool ok = !SINGLE || tl.row0 + (i >> LT) < a.rows;
-            v[r] = ok ? src[natural_offset(a, tl, i)] : make_float2(0.f, 0.f);
-        }
+        for (int r = 0; r < kE; ++r) v[r] = load_at(src, tb, natural_offset(a, Tile{}, phase_index<w0>(0, r)) * 8u);
     }
 
     static __device__ __forceinline__ void bases_of(float2 (&bs)[4], const FftArgs& a, std::uint32_t t,
@@ -332,35 +364,44 @@ struct FftPass {
             digit<3>(v, bs[3]);
         }
         constexpr int wl = tile_window<kPhases - 1>();
-        float2* __restrict__ dst = a.out + span_base(a, tl, m);
+        const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.out + span_base(a, tl, m), span_bytes(a, tl, m));
         if constexpr (COL) {  // intermediate: same positions
+            const std::uint32_t tb = natural_offset(a, tl, phase_index<wl>(t, 0)) * 8u;
 #pragma unroll
-            for (int r = 0; r < kE; ++r) dst[natural_offset(a, tl, phase_index<wl>(t, r))] = v[r];
+            for (int r = 0; r < kE; ++r)
+                store_at(v[r], dst, tb, natural_offset(a, Tile{}, phase_index<wl>(0, r)) * 8u);
             return;
         }
         // Final pass: bit-reversed positions -> natural order through LDS.
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kE; ++r) lds[L::addr(phase_index<wl>(t, r))] = v[r];
+        for (int r = 0; r < kE; ++r) lds[L::split(phase_index<wl>(t, 0), phase_index<wl>(0, r))] = v[r];
         lds_barrier();
+        std::uint32_t it, ot;
+        staged(a, tl, t, it, ot);
 #pragma unroll
         for (int r = 0; r < kE; ++r) {
-            const std::uint32_t g = t + T * r;
-            std::uint32_t i, off;
-            bool ok = true;
-            if constexpr (SINGLE) {  // rows are transforms: in-row bit reversal, lanes along the row
-                const std::uint32_t xp = g & ((1u << LT) - 1u), rr = g >> LT;
-                i = brev(xp, LT) | (rr << LT);
-                ok = tl.row0 + rr < a.rows;
-                off = (rr << LT) + xp;
-            } else {  // grid transpose: tile rows are bitrev(k0 + rr) of one transform
-                const std::uint32_t rr = g & ((1u << LI) - 1u), cp = g >> LI;
-                const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
-                i = brev(cp, LT) | (rr << LT);
-                off = (cp << a.l1) + k0 + rr;
-            }
-            const float2 x = lds[L::addr(i)];
-            if (ok) dst[off] = make_float2(x.x * a.scale, x.y * a.scale);
+            std::uint32_t ir, orr;
+            staged(a, Tile{}, T * std::uint32_t(r), ir, orr);
+            const float2 x = lds[L::split(it, ir)];
+            store_at(make_float2(x.x * a.scale, x.y * a.scale), dst, ot * 8u, orr * 8u);
+        }
+    }
+
+    // Final-store enumeration of element g (physical contiguity order): its
+    // tile index i and its offset in the span. Both are sums over disjoint
+    // bit fields of g (so g = t + T r splits into thread and register parts).
+    static __device__ __forceinline__ void staged(const FftArgs& a, const Tile& tl, std::uint32_t g, std::uint32_t& i,
+                                                  std::uint32_t& off) {
+        if constexpr (SINGLE) {  // rows are transforms: in-row bit reversal, lanes along the row
+            const std::uint32_t xp = g & ((1u << LT) - 1u), rr = g >> LT;
+            i = brev(xp, LT) | (rr << LT);
+            off = (rr << LT) + xp;
+        } else {  // grid transpose: tile rows are bitrev(k0 + rr) of one transform
+            const std::uint32_t rr = g & ((1u << LI) - 1u), cp = g >> LI;
+            const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
+            i = brev(cp, LT) | (rr << LT);
+            off = (cp << a.l1) + k0 + rr;
         }
     }
 

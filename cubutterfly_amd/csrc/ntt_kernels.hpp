@@ -20,6 +20,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "buffer.hpp"
 #include "ntt_engine.hpp"
 
 #include <cstddef>
@@ -216,53 +217,6 @@ __device__ __forceinline__ void gs_scale_butterfly(W& x, W& y, const DeviceDomai
     const W span = LAZY ? d.q2 : d.q;
     x = shoup(u + v, d.ninv.w, d.ninv.wp, d.nq);
     y = shoup(u - v + span, d.last.w, d.last.wp, d.nq);
-}
-
-// ---- buffer access ----------------------------------------------------------
-
-constexpr int kBufferWord3 = 0x00020000;  // raw 32-bit buffer, gfx9 family
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, std::uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
-                                             kBufferWord3);
-}
-
-// byte_off: per-lane offset; scalar_off: a wave-uniform offset carried in
-// the instruction's scalar operand (outside the range check: callers use it
-// only where every access lies inside the resource's range).
-template <class W>
-__device__ __forceinline__ W buffer_load(__amdgpu_buffer_rsrc_t r, std::uint32_t byte_off, std::uint32_t scalar_off = 0) {
-    if constexpr (sizeof(W) == 4) {
-        return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0);
-    } else {
-        const auto v =
-            __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0);
-        return (std::uint64_t(v[1]) << 32) | v[0];
-    }
-}
-
-// AUX: the instruction's cache-policy bits.
-template <class W, int AUX = 0>
-__device__ __forceinline__ void buffer_store(W x, __amdgpu_buffer_rsrc_t r, std::uint32_t byte_off,
-                                             std::uint32_t scalar_off = 0) {
-    if constexpr (sizeof(W) == 4) {
-        __builtin_amdgcn_raw_buffer_store_b32(x, r, static_cast<int>(byte_off), static_cast<int>(scalar_off), AUX);
-    } else {
-        using V2 = __attribute__((ext_vector_type(2))) std::uint32_t;
-        V2 v;
-        v[0] = static_cast<std::uint32_t>(x);
-        v[1] = static_cast<std::uint32_t>(x >> 32);
-        __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(byte_off), static_cast<int>(scalar_off), AUX);
-    }
-}
-
-// Wave-uniform copies (readfirstlane returns int: go through uint32 so the
-// low half of a 64-bit value is not sign-extended).
-__device__ __forceinline__ std::uint32_t uniform(std::uint32_t x) {
-    return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
-}
-__device__ __forceinline__ std::uint64_t uniform(std::uint64_t x) {
-    return (std::uint64_t(uniform(std::uint32_t(x >> 32))) << 32) | std::uint64_t(uniform(std::uint32_t(x)));
 }
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
