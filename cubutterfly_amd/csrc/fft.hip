@@ -1,13 +1,14 @@
 // Complex FFT (COMPLEX_FP32, natural order in and out) for gfx950.
 //
-// Decimation in frequency over 4-bit digits, top digit first. A workgroup
-// holds a tile of 2^LB complex values = 2^LT transform points x 2^LI lines,
-// 16 per thread. For each digit: an in-register radix-2^r DIF codelet with
-// compile-time twiddles (r = 4, the last digit r = 1..4), then every element
-// is multiplied by w_{2^h}^(j_low * c): j_low = the element's index bits below
-// the digit, c = its digit output, h = the digit's top bit + 1 (the four-step
-// twiddle of that level). LDS exchanges regroup the data between digits. The
-// result lands in bit-reversed position (digit reversal with each digit
+// Decimation in frequency over digits of DB bits (5 on one-pass 2^13- and
+// 2^14-point tiles, 4 elsewhere), top digit first. A workgroup holds a tile of 2^LB complex
+// values = 2^LT transform points x 2^LI lines, 2^DB per thread. For each
+// digit: an in-register radix-2^r DIF codelet with compile-time twiddles
+// (r = DB, the last digit r = 1..DB), then every element is multiplied by
+// w_{2^h}^(j_low * c): j_low = the element's index bits below the digit, c =
+// its digit output, h = the digit's top bit + 1 (the four-step twiddle of
+// that level). LDS exchanges regroup the data between digits. The result
+// lands in bit-reversed position (digit reversal with each digit
 // bit-reversed), so the final pass stores through an LDS-staged
 // bit-reversal; two-pass lengths also transpose the 2^l1 x 2^l2 grid there.
 //
@@ -33,9 +34,6 @@
 namespace cbw {
 namespace {
 
-constexpr int kLE = 4;
-constexpr int kE = 16;
-
 struct FftArgs {
     const float2* in;
     float2* out;
@@ -56,82 +54,71 @@ __device__ __forceinline__ std::uint32_t brev(std::uint32_t x, std::uint32_t bit
     return bits ? __brev(x) >> (32 - bits) : 0u;
 }
 
+// Hides a value from the optimiser (no code): keeps computations that use it
+// where they are written.
+__device__ __forceinline__ void opaque(float2& x) { asm volatile("" : "+v"(x.x), "+v"(x.y)); }
+
 constexpr std::uint32_t brev_const(std::uint32_t x, int bits) {
     std::uint32_t r = 0;
     for (int i = 0; i < bits; ++i) r |= ((x >> i) & 1u) << (bits - 1 - i);
     return r;
 }
 
-template <int S>
+// Tile index of (thread t, register r) when the DB register bits sit at
+// tile bits [S, S + DB).
+template <int S, int DB>
 __device__ __forceinline__ std::uint32_t phase_index(std::uint32_t t, std::uint32_t r) {
-    return (t & ((1u << S) - 1u)) | (r << S) | ((t >> S) << (S + kLE));
+    return (t & ((1u << S) - 1u)) | (r << S) | ((t >> S) << (S + DB));
 }
 
-// cos / sin of 2 pi j / 16 for j = 0..15 (exact decimal expansions).
-constexpr double kCos16[16] = {1.0, 0.92387953251128676, 0.70710678118654752, 0.38268343236508977,
-                               0.0, -0.38268343236508977, -0.70710678118654752, -0.92387953251128676,
-                               -1.0, -0.92387953251128676, -0.70710678118654752, -0.38268343236508977,
-                               0.0, 0.38268343236508977, 0.70710678118654752, 0.92387953251128676};
+// cos(2 pi j / 32) for j = 0..31 (decimal expansions of the exact values).
+constexpr double kCos32[32] = {
+    1.0, 9.80785280403230449126e-1, 9.23879532511286756128e-1, 8.31469612302545237079e-1,
+    7.07106781186547524401e-1, 5.55570233019602224743e-1, 3.82683432365089771728e-1, 1.95090322016128267848e-1,
+    0.0, -1.95090322016128267848e-1, -3.82683432365089771728e-1, -5.55570233019602224743e-1,
+    -7.07106781186547524401e-1, -8.31469612302545237079e-1, -9.23879532511286756128e-1, -9.80785280403230449126e-1,
+    -1.0, -9.80785280403230449126e-1, -9.23879532511286756128e-1, -8.31469612302545237079e-1,
+    -7.07106781186547524401e-1, -5.55570233019602224743e-1, -3.82683432365089771728e-1, -1.95090322016128267848e-1,
+    0.0, 1.95090322016128267848e-1, 3.82683432365089771728e-1, 5.55570233019602224743e-1,
+    7.07106781186547524401e-1, 8.31469612302545237079e-1, 9.23879532511286756128e-1, 9.80785280403230449126e-1};
 
 // x * w_len^j with w = exp(-+2 pi i / len) (forward / inverse), constants folded.
 template <int LEN, int J, bool INV>
 __device__ __forceinline__ float2 twiddle_const(float2 x) {
-    constexpr int e = (J * (16 / LEN)) & 15;  // angle index in sixteenths of a turn
+    constexpr int e = (J * (32 / LEN)) & 31;  // angle index in 32nds of a turn
     if constexpr (e == 0) {
         return x;
-    } else if constexpr (e == 4) {  // -i (forward) / +i (inverse)
+    } else if constexpr (e == 8) {  // -i (forward) / +i (inverse)
         return INV ? make_float2(-x.y, x.x) : make_float2(x.y, -x.x);
-    } else if constexpr (e == 8) {
+    } else if constexpr (e == 16) {
         return make_float2(-x.x, -x.y);
-    } else if constexpr (e == 12) {
+    } else if constexpr (e == 24) {
         return INV ? make_float2(x.y, -x.x) : make_float2(-x.y, x.x);
     } else {
-        constexpr float c = float(kCos16[e]);
-        constexpr float s = float(INV ? kCos16[(e + 12) & 15] : -kCos16[(e + 12) & 15]);  // +-sin
+        constexpr float c = float(kCos32[e]);
+        constexpr float s = float(INV ? kCos32[(e + 24) & 31] : -kCos32[(e + 24) & 31]);  // +-sin
         return make_float2(x.x * c - x.y * s, x.x * s + x.y * c);
     }
 }
 
-// Radix-2^DS DIF on register bits [0, DS) of each 2^DS group (bit-reversed out).
-template <int DS, bool INV>
-__device__ __forceinline__ void codelet(float2 (&v)[kE]) {
-#pragma unroll
-    for (int b = DS - 1; b >= 0; --b) {
-        const int half = 1 << b;
-#pragma unroll
-        for (int r = 0; r < kE; ++r) {
-            if (r & half) continue;
-            const float2 u = v[r], w = v[r + half];
-            v[r] = make_float2(u.x + w.x, u.y + w.y);
-            const float2 d = make_float2(u.x - w.x, u.y - w.y);
-            // twiddle w_{2 half}^(r mod half)
-            const int j = r & (half - 1);
-            float2 t = d;
-            switch (half) {
-                case 1: break;
-                case 2:
-                    if (j == 1) t = twiddle_const<4, 1, INV>(d);
-                    break;
-                case 4:
-                    if (j == 1) t = twiddle_const<8, 1, INV>(d);
-                    else if (j == 2) t = twiddle_const<8, 2, INV>(d);
-                    else if (j == 3) t = twiddle_const<8, 3, INV>(d);
-                    break;
-                default:
-                    switch (j) {
-                        case 1: t = twiddle_const<16, 1, INV>(d); break;
-                        case 2: t = twiddle_const<16, 2, INV>(d); break;
-                        case 3: t = twiddle_const<16, 3, INV>(d); break;
-                        case 4: t = twiddle_const<16, 4, INV>(d); break;
-                        case 5: t = twiddle_const<16, 5, INV>(d); break;
-                        case 6: t = twiddle_const<16, 6, INV>(d); break;
-                        case 7: t = twiddle_const<16, 7, INV>(d); break;
-                        default: break;
-                    }
-            }
-            v[r + half] = t;
-        }
+// One radix-2 DIF stage (pairs R, R + 2^B inside each group), unrolled over
+// the registers at compile time.
+template <int E, int B, int R, bool INV>
+__device__ __forceinline__ void codelet_stage(float2 (&v)[E]) {
+    constexpr int half = 1 << B;
+    if constexpr (!(R & half)) {
+        const float2 u = v[R], w = v[R + half];
+        v[R] = make_float2(u.x + w.x, u.y + w.y);
+        v[R + half] = twiddle_const<2 * half, (R & (half - 1)), INV>(make_float2(u.x - w.x, u.y - w.y));
     }
+    if constexpr (R + 1 < E) codelet_stage<E, B, R + 1, INV>(v);
+}
+
+// Radix-2^DS DIF on register bits [0, DS) of each 2^DS group (bit-reversed out).
+template <int E, int DS, bool INV>
+__device__ __forceinline__ void codelet(float2 (&v)[E]) {
+    codelet_stage<E, DS - 1, 0, INV>(v);
+    if constexpr (DS > 1) codelet<E, DS - 1, INV>(v);
 }
 
 // Padded LDS image (8-byte complex words), as in the NTT tiles.
@@ -159,31 +146,44 @@ struct FftLds {
     }
 };
 
+// One-pass tiles of 2^13 and 2^14 points (LDS-bound to one or two per CU)
+// use 5-bit digits, 32 values per thread, and prefetch the next tile into
+// registers (2 waves per SIMD leave room for both tiles). Other tiles use
+// 4-bit digits and 16 values per thread. Two-pass tiles at m = 24 measured
+// slower with 5-bit digits and prefetching (their 32-byte column segments,
+// not the VALU, bound them), so they keep the 4-bit layout.
+constexpr int digit_bits_for(int lb, bool single) { return single && lb >= 13 ? 5 : 4; }
+
 // One FFT pass over LT transform bits. COL: high bits, tile of 2^LI columns;
 // ROW: low bits, tile of 2^LI rows (the final pass, storing in natural order);
 // SINGLE: a one-pass transform, 2^LI whole rows per tile.
 template <int LT, int LI, bool COL, bool SINGLE, bool INV>
 struct FftPass {
     static constexpr int LB = LT + LI;
-    static constexpr std::uint32_t T = 1u << (LB - kLE);
-    static constexpr int kPhases = (LT + kLE - 1) / kLE;
-    // Prefetching the next tile into registers fits the 128-VGPR budget for
-    // up to two digits; deeper passes run one tile per workgroup (a finished
-    // workgroup's stores then overlap the next one's loads).
-    static constexpr bool kPrefetch = kPhases <= 2;
+    static constexpr int DB = digit_bits_for(LB, SINGLE);
+    static constexpr int kE = 1 << DB;
+    static constexpr std::uint32_t T = 1u << (LB - DB);
+    static constexpr int kPhases = (LT + DB - 1) / DB;
+    // Prefetching needs registers for two tiles: with 16 values per thread
+    // that fits the 128-register budget for passes of at most two digits.
+    static constexpr bool kPrefetch = DB == 5 || kPhases <= 2;
     using L = FftLds<COL, LT, LI>;
 
     template <int P>
     static constexpr int window() {  // transform-relative register window start
-        return LT - kLE * (P + 1) > 0 ? LT - kLE * (P + 1) : 0;
+        return LT - DB * (P + 1) > 0 ? LT - DB * (P + 1) : 0;
     }
     template <int P>
     static constexpr int digit_bits() {
-        return LT - kLE * P < kLE ? LT - kLE * P : kLE;
+        return LT - DB * P < DB ? LT - DB * P : DB;
     }
     template <int P>
     static constexpr int tile_window() {
         return (COL ? LI : 0) + window<P>();
+    }
+    template <int S>
+    static __device__ __forceinline__ std::uint32_t index(std::uint32_t t, std::uint32_t r) {
+        return phase_index<S, DB>(t, r);
     }
 
     // Whether digit P is followed by a level twiddle (not for the last digit
@@ -208,7 +208,7 @@ struct FftPass {
             const std::uint32_t lo_rel = std::uint32_t(ws);
             const std::uint32_t lo = COL ? a.l2 + lo_rel : lo_rel;
             const std::uint32_t h = lo + ds;
-            const std::uint32_t i0 = phase_index<tile_window<P>()>(t, 0);
+            const std::uint32_t i0 = index<tile_window<P>()>(t, 0);
             // Index bits below the digit: for columns, the low transform bits
             // of the column index and the column; for rows, the low bits.
             const std::uint32_t x0 = COL ? (i0 >> LI) : (i0 & ((1u << LT) - 1u));
@@ -224,17 +224,29 @@ struct FftPass {
     template <int P>
     static __device__ __forceinline__ void digit(float2 (&v)[kE], float2 base) {
         constexpr int ds = digit_bits<P>();
-        codelet<ds, INV>(v);
+        codelet<kE, ds, INV>(v);
         if constexpr (twiddled<P>()) {
-            // base^c for c = 1 .. 2^ds - 1, streamed: only base^1,2,3,4,8 stay
-            // live; every other power is one or two products of those (product
-            // depth <= 4), applied as soon as it is formed.
-            const float2 p1 = base;
-            const float2 p2 = ds > 1 ? cmul(p1, p1) : p1;
-            const float2 p3 = ds > 1 ? cmul(p2, p1) : p1;
-            const float2 p4 = ds > 2 ? cmul(p2, p2) : p1;
-            const float2 p8 = ds > 3 ? cmul(p4, p4) : p1;
-            apply_powers<0, ds>(v, p1, p2, p3, p4, p8);
+            // base^c for c = 1 .. 2^ds - 1, streamed: only base^1,2,3,4,8,16
+            // stay live; every other power is at most three products of those,
+            // applied as soon as it is formed.
+            float2 p1 = base;
+            float2 p2 = ds > 1 ? cmul(p1, p1) : p1;
+            float2 p3 = ds > 1 ? cmul(p2, p1) : p1;
+            float2 p4 = ds > 2 ? cmul(p2, p2) : p1;
+            float2 p8 = ds > 3 ? cmul(p4, p4) : p1;
+            float2 p16 = ds > 4 ? cmul(p8, p8) : p1;
+            // Row passes compute their bases once per thread; in the tile loop
+            // the optimiser would otherwise also hoist all 2^ds - 1 products
+            // out of it and hold them in registers across it.
+            if constexpr (kPrefetch) {
+                opaque(p1);
+                opaque(p2);
+                opaque(p3);
+                opaque(p4);
+                opaque(p8);
+                opaque(p16);
+            }
+            apply_powers<0, ds>(v, p1, p2, p3, p4, p8, p16);
         }
     }
 
@@ -242,12 +254,12 @@ struct FftPass {
     // R above the digit (only in a short last digit) are earlier digits.
     template <int R, int DS>
     static __device__ __forceinline__ void apply_powers(float2 (&v)[kE], float2 p1, float2 p2, float2 p3, float2 p4,
-                                                        float2 p8) {
+                                                        float2 p8, float2 p16) {
         constexpr int c = int(brev_const(std::uint32_t(R) & ((1u << DS) - 1u), DS));
         if constexpr (c != 0) {
             constexpr int lo = c & 7;
             float2 w;
-            if constexpr (lo == 0) w = p8;
+            if constexpr (lo == 0) w = (c & 8) ? p8 : p16;
             else if constexpr (lo == 1) w = p1;
             else if constexpr (lo == 2) w = p2;
             else if constexpr (lo == 3) w = p3;
@@ -255,20 +267,21 @@ struct FftPass {
             else if constexpr (lo == 5) w = cmul(p4, p1);
             else if constexpr (lo == 6) w = cmul(p4, p2);
             else w = cmul(p4, p3);
-            if constexpr (c > 8) w = cmul(p8, w);
+            if constexpr (lo != 0 && (c & 8)) w = cmul(p8, w);
+            if constexpr ((c & 16) && (lo != 0 || (c & 8))) w = cmul(p16, w);
             v[R] = cmul(v[R], w);
         }
-        if constexpr (R + 1 < kE) apply_powers<R + 1, DS>(v, p1, p2, p3, p4, p8);
+        if constexpr (R + 1 < kE) apply_powers<R + 1, DS>(v, p1, p2, p3, p4, p8, p16);
     }
 
     template <int FROM, int TO>
     static __device__ __forceinline__ void exchange(float2 (&v)[kE], float2* lds, std::uint32_t t) {
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kE; ++r) lds[L::split(phase_index<FROM>(t, 0), phase_index<FROM>(0, r))] = v[r];
+        for (int r = 0; r < kE; ++r) lds[L::split(index<FROM>(t, 0), index<FROM>(0, r))] = v[r];
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = lds[L::split(phase_index<TO>(t, 0), phase_index<TO>(0, r))];
+        for (int r = 0; r < kE; ++r) v[r] = lds[L::split(index<TO>(t, 0), index<TO>(0, r))];
     }
 
     struct Tile {
@@ -320,6 +333,9 @@ struct FftPass {
     // the tile origin enters only the thread part. A partial one-pass tile
     // keeps the whole offset in the lane offset, which the range check sees.
     static constexpr bool kLaneOnly = SINGLE && LI > 0;
+    // (Two-pass register offsets depend on l1 / l2 at run time, so the choice
+    // is a wave-uniform branch there; keeping small offsets in the lane offset
+    // measured faster than always using the scalar offset.)
     static __device__ __forceinline__ float2 load_at(__amdgpu_buffer_rsrc_t src, std::uint32_t lane_bytes,
                                                      std::uint32_t reg_bytes) {
         if (kLaneOnly || reg_bytes < 4096u) return buffer_load<float2>(src, lane_bytes + reg_bytes);
@@ -335,21 +351,21 @@ struct FftPass {
                                                 float2 (&v)[kE]) {
         constexpr int w0 = tile_window<0>();
         const __amdgpu_buffer_rsrc_t src = make_rsrc(a.in + span_base(a, tl, m), span_bytes(a, tl, m));
-        const std::uint32_t tb = natural_offset(a, tl, phase_index<w0>(t, 0)) * 8u;
+        const std::uint32_t tb = natural_offset(a, tl, index<w0>(t, 0)) * 8u;
 #pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = load_at(src, tb, natural_offset(a, Tile{}, phase_index<w0>(0, r)) * 8u);
+        for (int r = 0; r < kE; ++r) v[r] = load_at(src, tb, natural_offset(a, Tile{}, index<w0>(0, r)) * 8u);
     }
 
-    static __device__ __forceinline__ void bases_of(float2 (&bs)[4], const FftArgs& a, std::uint32_t t,
+    static __device__ __forceinline__ void bases_of(float2 (&bs)[3], const FftArgs& a, std::uint32_t t,
                                                     std::uint32_t c0, std::uint32_t m) {
         bs[0] = level_base<0>(a, t, c0, m);
         if constexpr (kPhases > 1) bs[1] = level_base<1>(a, t, c0, m);
         if constexpr (kPhases > 2) bs[2] = level_base<2>(a, t, c0, m);
-        if constexpr (kPhases > 3) bs[3] = level_base<3>(a, t, c0, m);
     }
+    static_assert(kPhases <= 4, "at most four digits per pass");
 
     static __device__ __forceinline__ void process(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
-                                                   float2 (&v)[kE], const float2 (&bs)[4], float2* lds) {
+                                                   float2 (&v)[kE], const float2 (&bs)[3], float2* lds) {
         digit<0>(v, bs[0]);
         if constexpr (kPhases > 1) {
             exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
@@ -360,22 +376,23 @@ struct FftPass {
             digit<2>(v, bs[2]);
         }
         if constexpr (kPhases > 3) {
+            // A fourth digit (4-bit digits over 13 or 14 bits) fetches its
+            // base here, keeping the bases held across the tile to three.
             exchange<tile_window<2>(), tile_window<3>()>(v, lds, t);
-            digit<3>(v, bs[3]);
+            digit<3>(v, level_base<3>(a, t, tl.c0, m));
         }
         constexpr int wl = tile_window<kPhases - 1>();
         const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.out + span_base(a, tl, m), span_bytes(a, tl, m));
         if constexpr (COL) {  // intermediate: same positions
-            const std::uint32_t tb = natural_offset(a, tl, phase_index<wl>(t, 0)) * 8u;
+            const std::uint32_t tb = natural_offset(a, tl, index<wl>(t, 0)) * 8u;
 #pragma unroll
-            for (int r = 0; r < kE; ++r)
-                store_at(v[r], dst, tb, natural_offset(a, Tile{}, phase_index<wl>(0, r)) * 8u);
+            for (int r = 0; r < kE; ++r) store_at(v[r], dst, tb, natural_offset(a, Tile{}, index<wl>(0, r)) * 8u);
             return;
         }
         // Final pass: bit-reversed positions -> natural order through LDS.
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kE; ++r) lds[L::split(phase_index<wl>(t, 0), phase_index<wl>(0, r))] = v[r];
+        for (int r = 0; r < kE; ++r) lds[L::split(index<wl>(t, 0), index<wl>(0, r))] = v[r];
         lds_barrier();
         std::uint32_t it, ot;
         staged(a, tl, t, it, ot);
@@ -423,7 +440,7 @@ struct FftPass {
         std::uint32_t pos = xcd ? (b >> 3) : b;
         if (pos >= range_end) return;
         Tile tl = decode(a, range_base + pos, m);
-        float2 bs[4];
+        float2 bs[3];
         if constexpr (!COL) bases_of(bs, a, t, 0, m);  // row passes: the bases depend on the thread only
         float2 v[kE];
         load(a, tl, t, m, v);
@@ -458,8 +475,8 @@ struct FftPass {
 };
 
 template <int LT, int LI, bool COL, bool SINGLE, bool INV>
-__global__ __launch_bounds__(1 << (LT + LI - kLE)) __attribute__((amdgpu_waves_per_eu(4)))
-void fft_pass_kernel(FftArgs a) {
+__global__ __launch_bounds__(1 << (LT + LI - digit_bits_for(LT + LI, SINGLE)))
+__attribute__((amdgpu_waves_per_eu(digit_bits_for(LT + LI, SINGLE) == 5 ? 2 : 4))) void fft_pass_kernel(FftArgs a) {
     FftPass<LT, LI, COL, SINGLE, INV>::run(a);
 }
 
@@ -479,7 +496,7 @@ struct Key {
 template <int LT, int LI, bool COL, bool SINGLE, bool INV>
 void launch(const FftArgs& a, hipStream_t stream) {
     constexpr std::uint32_t bytes = FftLds<COL, LT, LI>::kWords * sizeof(float2);
-    constexpr int threads = 1 << (LT + LI - kLE);
+    constexpr int threads = int(FftPass<LT, LI, COL, SINGLE, INV>::T);
     static const std::uint64_t resident = [] {
         const void* fn = reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, SINGLE, INV>);
         if (bytes > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
@@ -507,16 +524,21 @@ void add() {
     registry()[Key{LT, LI, COL, SINGLE, true}] = &launch<LT, LI, COL, SINGLE, true>;
 }
 
-// Shapes: one pass for m <= 14 (2^12-point tiles, 2^14 for m = 13, 14);
-// two passes l1 = m / 2, l2 = m - l1 with 2^14-point tiles.
+// Shapes: one pass for m <= 14 (2^12-point tiles, 2^13 / 2^14 for m = 13,
+// 14); two passes with 2^14-point tiles over l1 = m / 2 high bits (column
+// tiles) and l2 = m - l1 low bits (row tiles). The even split keeps both the
+// column reads and the transposing row stores in segments of 2^(14 - m/2)
+// elements (32 bytes at m = 24); a column-heavier split would leave the
+// transposing store with single-element segments.
 constexpr int single_li(int m) { return m < 12 ? 12 - m : 0; }
+constexpr int split_l1(int m) { return m / 2; }
+constexpr int col_lines(int l1, int l2) { return 14 - l1 < l2 ? 14 - l1 : l2; }
+constexpr int row_lines(int l1, int l2) { return 14 - l2 < l1 ? 14 - l2 : l1; }
 template <int M>
 void add_two() {
-    constexpr int l1 = M / 2, l2 = M - l1;
-    constexpr int col_li = 14 - l1 < l2 ? 14 - l1 : l2;
-    constexpr int row_li = 14 - l2 < l1 ? 14 - l2 : l1;
-    add<l1, col_li, true, false>();
-    add<l2, row_li, false, false>();
+    constexpr int l1 = split_l1(M), l2 = M - l1;
+    add<l1, col_lines(l1, l2), true, false>();
+    add<l2, row_lines(l1, l2), false, false>();
 }
 
 void register_all() {
@@ -585,11 +607,11 @@ class FftExecutor final : public Executor {
             s.args.rows = unsigned(r.batch);
             s.args.tiles = unsigned(tiles);
             steps_.push_back(s);
-            algorithm = "fft-c64-resident-r16";
+            algorithm = m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16";
         } else {
-            const std::uint32_t l1 = m / 2, l2 = m - l1;
-            const int col_li = std::min<int>(14 - int(l1), int(l2));
-            const int row_li = std::min<int>(14 - int(l2), int(l1));
+            const std::uint32_t l1 = std::uint32_t(split_l1(int(m))), l2 = m - l1;
+            const int col_li = col_lines(int(l1), int(l2));
+            const int row_li = row_lines(int(l1), int(l2));
             const std::uint64_t col_tiles = r.batch << (l2 - col_li);
             const std::uint64_t row_tiles = r.batch << (l1 - row_li);
             require(col_tiles <= 0xffffffffull && row_tiles <= 0xffffffffull, "FFT batch exceeds the grid");
@@ -608,8 +630,9 @@ class FftExecutor final : public Executor {
             workspace_ = static_cast<std::size_t>(r.batch << m) * sizeof(float2);
             algorithm = "fft-c64-two-pass-r16";
         }
-        reason = "decimation in frequency over 4-bit digits: in-register radix-16 codelets, level twiddles from "
-                 "two 4096-entry tables, LDS-staged bit-reversal (and grid transpose) on the final store";
+        reason = "decimation in frequency: in-register radix-16 codelets (radix-32 for one-pass 2^13 and 2^14), "
+                 "level twiddles from two 4096-entry tables, LDS-staged bit-reversal (and grid transpose) on the "
+                 "final store";
         json::Writer w;
         w.begin_object()
             .field("schema_version", 1u)
