@@ -347,10 +347,12 @@ struct FftPass {
         else buffer_store<float2>(x, dst, lane_bytes, reg_bytes);
     }
 
+    // `valid` false: an empty buffer range, so every load returns zero
+    // without touching memory (keeps a prefetch unconditional, see step()).
     static __device__ __forceinline__ void load(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
-                                                float2 (&v)[kE]) {
+                                                float2 (&v)[kE], bool valid = true) {
         constexpr int w0 = tile_window<0>();
-        const __amdgpu_buffer_rsrc_t src = make_rsrc(a.in + span_base(a, tl, m), span_bytes(a, tl, m));
+        const __amdgpu_buffer_rsrc_t src = make_rsrc(a.in + span_base(a, tl, m), valid ? span_bytes(a, tl, m) : 0u);
         const std::uint32_t tb = natural_offset(a, tl, index<w0>(t, 0)) * 8u;
 #pragma unroll
         for (int r = 0; r < kE; ++r) v[r] = load_at(src, tb, natural_offset(a, Tile{}, index<w0>(0, r)) * 8u);
@@ -441,7 +443,14 @@ struct FftPass {
         if (pos >= range_end) return;
         Tile tl = decode(a, range_base + pos, m);
         float2 bs[3];
-        if constexpr (!COL) bases_of(bs, a, t, 0, m);  // row passes: the bases depend on the thread only
+        if constexpr (!COL) {
+            bases_of(bs, a, t, 0, m);  // row passes: the bases depend on the thread only
+            // Finish the bases before the first tile's loads: registers of
+            // their table loads would otherwise still be pending where the
+            // tile loop begins, and the loop's waits (merged over its entry
+            // and its back edge) would wait for the prefetch as well.
+            if constexpr (kPrefetch) __builtin_amdgcn_sched_barrier(0);
+        }
         float2 v[kE];
         load(a, tl, t, m, v);
         if constexpr (!kPrefetch) {  // one tile per workgroup (the grid covers every tile)
@@ -449,28 +458,50 @@ struct FftPass {
             process(a, tl, t, m, v, bs, lds);
             return;
         }
+        // Two register buffers in turn (unrolled by two), so no tile is
+        // copied between registers: a copy would make the wait for its loads
+        // also wait for the prefetch issued after them.
+        float2 w[kE];
         for (;;) {
-            // Per-thread addresses depend on t only; hiding t from the
-            // optimiser here keeps them from being hoisted out of the loop
-            // (and held in registers across it).
-            std::uint32_t tt = t;
-            asm volatile("" : "+v"(tt));
-            const std::uint32_t next = pos + stride;
-            const bool more = next < range_end;
-            if constexpr (COL) bases_of(bs, a, tt, tl.c0, m);
-            Tile tn{};
-            float2 nv[kE];
-            if (more) {
-                tn = decode(a, range_base + next, m);
-                load(a, tn, tt, m, nv);
-            }
-            process(a, tl, tt, m, v, bs, lds);
-            if (!more) break;
-            pos = next;
-            tl = tn;
-#pragma unroll
-            for (int r = 0; r < kE; ++r) v[r] = nv[r];
+            if (!step(a, t, m, pos, stride, range_base, range_end, tl, bs, v, w, lds)) break;
+            if (!step(a, t, m, pos, stride, range_base, range_end, tl, bs, w, v, lds)) break;
         }
+    }
+
+    // One tile of the persistent walk: prefetch the next tile into `next`,
+    // process the current one from `cur`. Returns whether a next tile exists.
+    static __device__ __forceinline__ bool step(const FftArgs& a, std::uint32_t t, std::uint32_t m, std::uint32_t& pos,
+                                                std::uint32_t stride, std::uint32_t range_base,
+                                                std::uint32_t range_end, Tile& tl, float2 (&bs)[3],
+                                                float2 (&cur)[kE], float2 (&next)[kE], float2* lds) {
+        // Per-thread addresses depend on t only; hiding t from the optimiser
+        // here keeps them from being hoisted out of the loop (and held in
+        // registers across it).
+        std::uint32_t tt = t;
+        asm volatile("" : "+v"(tt));
+        const std::uint32_t following = pos + stride;
+        const bool more = following < range_end;
+        if constexpr (COL) bases_of(bs, a, tt, tl.c0, m);
+        // The prefetch is issued even past the last tile (as empty-range
+        // loads): a branch around it would leave the compiler's wait for
+        // `cur` merging a path without the prefetch, and it would then wait
+        // for the prefetch too.
+        const Tile tn = decode(a, range_base + following, m);
+        load(a, tn, tt, m, next, more);
+        // No instruction moves across this point, so every use of `cur` comes
+        // after the prefetch is issued: the wait for `cur` then counts the
+        // prefetch as younger and does not wait for it (or for the previous
+        // tile's stores).
+        __builtin_amdgcn_sched_barrier(0);
+        process(a, tl, tt, m, cur, bs, lds);
+        // Keep `cur`'s registers allocated through the stores: otherwise the
+        // stores take their data from them, and the next prefetch into them
+        // would first wait for those stores.
+#pragma unroll
+        for (int r = 0; r < kE; ++r) opaque(cur[r]);
+        pos = following;
+        tl = tn;
+        return more;
     }
 };
 
