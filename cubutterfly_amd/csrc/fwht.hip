@@ -21,6 +21,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include "buffer.hpp"
 #include "json.hpp"
 #include "planner.hpp"
 
@@ -88,8 +89,25 @@ __device__ __forceinline__ void exchange(float (&v)[kE], float* lds, unsigned t)
 
 // ---- storage adapters ----------------------------------------------------
 
+// 16 bytes at byte offset `off` of a buffer resource.
+__device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+    return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 struct F32Io {
     using T = float;
+    // 16 consecutive floats at byte offset `off` of a tile's buffer.
+    static __device__ __forceinline__ void load16(__amdgpu_buffer_rsrc_t r, unsigned off, float (&v)[kE]) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint4 x = load_b128(r, off + 16u * k);
+            v[4 * k + 0] = __uint_as_float(x.x);
+            v[4 * k + 1] = __uint_as_float(x.y);
+            v[4 * k + 2] = __uint_as_float(x.z);
+            v[4 * k + 3] = __uint_as_float(x.w);
+        }
+    }
     // Full path: 16 consecutive floats = four 16-byte loads.
     static __device__ __forceinline__ void load16(const float* p, float (&v)[kE]) {
         const float4* q = reinterpret_cast<const float4*>(p);
@@ -113,6 +131,18 @@ struct F32Io {
 
 struct F16Io {
     using T = __half;
+    static __device__ __forceinline__ void load16(__amdgpu_buffer_rsrc_t r, unsigned off, float (&v)[kE]) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint4 x = load_b128(r, off + 16u * k);
+            const unsigned w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[8 * k + 2 * j + 0] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[j] & 0xffffu)));
+                v[8 * k + 2 * j + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[j] >> 16)));
+            }
+        }
+    }
     static __device__ __forceinline__ void load16(const __half* p, float (&v)[kE]) {
         const uint4* q = reinterpret_cast<const uint4*>(p);
 #pragma unroll
@@ -146,21 +176,90 @@ struct F16Io {
 
 // A workgroup owns tiles of 2^LB consecutive elements (2^(LB-LOG_N) whole
 // rows) and walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...; the next
-// tile's global loads are issued before the current tile is processed, so
-// HBM reads overlap the register/LDS phases.
+// tile's loads are issued before the current tile is processed, so HBM reads
+// overlap the register/LDS phases.
 // `norm` is 1 or 1/n (normalised inverse), `scale` the FP16 output scale; the
 // two products are applied in this order, as the reference's finalize and
 // narrowing kernel do. Multiplying by 1.0f is exact, so unused factors are 1.
+
+// Element-wise load of a tile that ends past `total` (zeros there).
 template <int LB, class Io>
-__device__ __forceinline__ void load_tile(const typename Io::T* __restrict__ input, std::uint64_t base,
-                                          std::uint64_t total, unsigned t, float (&v)[kE]) {
-    if (base + (1ull << LB) <= total) {
-        Io::load16(input + base + t * kE, v);
-    } else {
+__device__ __forceinline__ void load_partial(const typename Io::T* __restrict__ input, std::uint64_t base,
+                                             std::uint64_t total, unsigned t, float (&v)[kE]) {
+#pragma unroll
+    for (int r = 0; r < kE; ++r) {
+        const std::uint64_t i = base + t * kE + r;
+        v[r] = i < total ? Io::load1(input + i) : 0.0f;
+    }
+}
+
+// A full tile's 16 elements per thread through a buffer over the tile;
+// `valid` false gives an empty buffer, so the loads return zeros without
+// touching memory (keeps the prefetch below unconditional).
+template <int LB, class Io>
+__device__ __forceinline__ void load_full(const typename Io::T* __restrict__ input, std::uint64_t tile, bool valid,
+                                          unsigned t, float (&v)[kE]) {
+    constexpr unsigned kBytes = (1u << LB) * unsigned(sizeof(typename Io::T));
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(input + (tile << LB), valid ? kBytes : 0u);
+    Io::load16(r, t * kE * unsigned(sizeof(typename Io::T)), v);
+}
+
+// Hides a value from the optimiser (no code). Applied to the scaled fp32
+// result before the FP16 narrowing, it keeps the two roundings of the
+// contract (fp32 product, then RNE to fp16): the backend would otherwise fuse
+// product and narrowing into one mixed-precision FMA with a single rounding.
+__device__ __forceinline__ void opaque(float& x) { asm volatile("" : "+v"(x)); }
+
+// The butterflies of one tile and its store (`full`: the tile lies inside
+// `total`).
+template <int LOG_N, int LB, class Io>
+__device__ __forceinline__ void transform_store(float (&v)[kE], float* lds, unsigned t, typename Io::T* output,
+                                                std::uint64_t base, std::uint64_t total, bool full, float norm,
+                                                float scale) {
+    constexpr int kPhases = (LOG_N + kLE - 1) / kLE;
+    constexpr int kLast = kPhases - 1;
+    // Store straight from the last phase when its lanes cover >= 64
+    // consecutive elements; otherwise regroup to 16-per-thread vectors.
+    constexpr bool kDirectStore = kPhases > 1 && window_start<kLast, LB>() >= 6;
+    register_stages<0, LOG_N, LB>(v);
+    if constexpr (kPhases > 1) {
+        exchange<0, 1, LB>(v, lds, t);
+        register_stages<1, LOG_N, LB>(v);
+    }
+    if constexpr (kPhases > 2) {
+        exchange<1, 2, LB>(v, lds, t);
+        register_stages<2, LOG_N, LB>(v);
+    }
+    if constexpr (kPhases > 3) {
+        exchange<2, 3, LB>(v, lds, t);
+        register_stages<3, LOG_N, LB>(v);
+    }
+    // The products land in new registers (not in `v`), so the caller can keep
+    // `v` free of pending store data (see the tile loop).
+    if constexpr (kDirectStore) {
 #pragma unroll
         for (int r = 0; r < kE; ++r) {
-            const std::uint64_t i = base + t * kE + r;
-            v[r] = i < total ? Io::load1(input + i) : 0.0f;
+            const std::uint64_t i = base + phase_index<kLast, LB>(t, r);
+            float y = (v[r] * norm) * scale;
+            opaque(y);
+            if (full || i < total) Io::store1(output + i, y);
+        }
+    } else {
+        if constexpr (kPhases > 1) exchange<kLast, 0, LB>(v, lds, t);
+        float x[kE];
+#pragma unroll
+        for (int r = 0; r < kE; ++r) {
+            x[r] = (v[r] * norm) * scale;
+            opaque(x[r]);
+        }
+        if (full) {
+            Io::store16(output + base + t * kE, x);
+        } else {
+#pragma unroll
+            for (int r = 0; r < kE; ++r) {
+                const std::uint64_t i = base + t * kE + r;
+                if (i < total) Io::store1(output + i, x[r]);
+            }
         }
     }
 }
@@ -170,63 +269,46 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_resident_kernel(const ty
                                                                         typename Io::T* output,
                                                                         std::uint64_t total, float norm,
                                                                         float scale, unsigned tiles) {
-    constexpr int kPhases = (LOG_N + kLE - 1) / kLE;
-    constexpr int kLast = kPhases - 1;
-    // Store straight from the last phase when its lanes cover >= 64
-    // consecutive elements; otherwise regroup to 16-per-thread vectors.
-    constexpr bool kDirectStore = kPhases > 1 && window_start<kLast, LB>() >= 6;
     constexpr unsigned kBlock = 1u << LB;
     __shared__ float lds[kBlock + (kBlock >> kLE)];
     const unsigned t = threadIdx.x;
+    const unsigned grid = gridDim.x;
+    const unsigned full_tiles = static_cast<unsigned>(total >> LB);
     unsigned tile = blockIdx.x;
-    if (tile >= tiles) return;
 
-    float v[kE], next[kE];
-    load_tile<LB, Io>(input, std::uint64_t(tile) * kBlock, total, t, v);
-    for (;;) {
-        const std::uint64_t base = std::uint64_t(tile) * kBlock;
-        const unsigned following = tile + gridDim.x;
-        const bool more = following < tiles;
-        if (more) load_tile<LB, Io>(input, std::uint64_t(following) * kBlock, total, t, next);
-
-        register_stages<0, LOG_N, LB>(v);
-        if constexpr (kPhases > 1) {
-            exchange<0, 1, LB>(v, lds, t);
-            register_stages<1, LOG_N, LB>(v);
-        }
-        if constexpr (kPhases > 2) {
-            exchange<1, 2, LB>(v, lds, t);
-            register_stages<2, LOG_N, LB>(v);
-        }
-        if constexpr (kPhases > 3) {
-            exchange<2, 3, LB>(v, lds, t);
-            register_stages<3, LOG_N, LB>(v);
-        }
+    // Full tiles: two register buffers in turn. Each step issues the next
+    // tile's loads (empty-range loads past the last one, so the issue is
+    // unconditional), then transforms the current tile. A branch around the
+    // prefetch, or a copy between buffers, would make the compiler's wait for
+    // the current tile also wait for the prefetch.
+    auto step = [&](float (&cur)[kE], float (&nxt)[kE]) -> bool {
+        const unsigned following = tile + grid;
+        const bool more = following < full_tiles;
+        load_full<LB, Io>(input, following, more, t, nxt);
+        __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before any use of `cur`
+        transform_store<LOG_N, LB, Io>(cur, lds, t, output, std::uint64_t(tile) << LB, total, true, norm, scale);
+        // Keep `cur`'s registers allocated through the stores, so no store
+        // takes its data from them: the prefetch into them two steps on would
+        // otherwise first wait for those stores.
 #pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = (v[r] * norm) * scale;
-        const bool full = base + kBlock <= total;
-        if constexpr (kDirectStore) {
-#pragma unroll
-            for (int r = 0; r < kE; ++r) {
-                const std::uint64_t i = base + phase_index<kLast, LB>(t, r);
-                if (full || i < total) Io::store1(output + i, v[r]);
-            }
-        } else {
-            if constexpr (kPhases > 1) exchange<kLast, 0, LB>(v, lds, t);
-            if (full) {
-                Io::store16(output + base + t * kE, v);
-            } else {
-#pragma unroll
-                for (int r = 0; r < kE; ++r) {
-                    const std::uint64_t i = base + t * kE + r;
-                    if (i < total) Io::store1(output + i, v[r]);
-                }
-            }
-        }
-        if (!more) break;
+        for (int r = 0; r < kE; ++r) opaque(cur[r]);
         tile = following;
-#pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = next[r];
+        return more;
+    };
+    if (tile < full_tiles) {
+        float a[kE], b[kE];
+        load_full<LB, Io>(input, tile, true, t, a);
+        for (;;) {
+            if (!step(a, b)) break;
+            if (!step(b, a)) break;
+        }
+    }
+    // A last, partial tile goes to the workgroup whose walk reaches it.
+    if (full_tiles < tiles && full_tiles % grid == blockIdx.x) {
+        const std::uint64_t base = std::uint64_t(full_tiles) << LB;
+        float v[kE];
+        load_partial<LB, Io>(input, base, total, t, v);
+        transform_store<LOG_N, LB, Io>(v, lds, t, output, base, total, false, norm, scale);
     }
 }
 
