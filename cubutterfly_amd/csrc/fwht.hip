@@ -329,57 +329,36 @@ void launch_resident(const void* in, void* out, std::uint64_t total, float norm,
                        scale, static_cast<unsigned>(tiles));
 }
 
-// Workgroups of this kernel resident per CU (registers, LDS, waves).
-template <int LOG_N, class Io>
-unsigned resident_per_cu() {
-    constexpr int LB = block_log<LOG_N, Io>();
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void*>(&fwht_resident_kernel<LOG_N, LB, Io>), 1 << (LB - kLE), 0) !=
-            hipSuccess ||
-        n < 1)
-        n = 1;
-    return unsigned(n);
-}
-
-struct Kernel {
-    Launch launch;
-    unsigned (*resident)();
-};
-
 template <class Io, int... L>
-Kernel resident_table_entry(int log_n, std::integer_sequence<int, L...>) {
-    Kernel table[] = {{nullptr, nullptr}, {launch_resident<L + 1, Io>, resident_per_cu<L + 1, Io>}...};
+Launch resident_table_entry(int log_n, std::integer_sequence<int, L...>) {
+    Launch table[] = {nullptr, launch_resident<L + 1, Io>...};
     return table[log_n];
 }
 
 constexpr int kMaxResidentLog = 13;
 
 template <class Io>
-Kernel resident_launcher(int log_n) {
-    if (log_n < 1 || log_n > kMaxResidentLog) return {nullptr, nullptr};
+Launch resident_launcher(int log_n) {
+    if (log_n < 1 || log_n > kMaxResidentLog) return nullptr;
     return resident_table_entry<Io>(log_n, std::make_integer_sequence<int, kMaxResidentLog>{});
 }
 
 class FwhtExecutor final : public Executor {
   public:
-    FwhtExecutor(const Request& r, Kernel kernel) : r_(r), launch_(kernel.launch) {
+    FwhtExecutor(const Request& r, Launch launch) : r_(r), launch_(launch) {
         norm_ = r.normalize ? 1.0f / static_cast<float>(r.n) : 1.0f;
         scale_ = r.fp16_final ? r.output_scale : 1.0f;
         const int lb = r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
         const std::uint64_t total = r.n * r.batch;
         const std::uint64_t tiles = (total + (1ull << lb) - 1) >> lb;
         require(tiles <= 0xffffffffull, "FWHT batch exceeds the tile index range");
-        // Grid: rows of three or more radix-16 phases (more LDS and register
-        // work per tile) run a persistent grid of as many workgroups as can
-        // be resident at once (occupancy of the kernel: registers, LDS,
-        // waves), each prefetching its next tile; shorter rows run one tile
-        // per workgroup, which measured faster for them on gfx950.
+        // Grid: one workgroup per tile (measured at least as fast as a
+        // persistent, occupancy-sized grid for every BASELINE shape once the
+        // kernel's prefetch overlapped), capped at the launch limit; the
+        // kernel walks any tiles beyond the grid with next-tile prefetch.
         const unsigned threads = 1u << (lb - kLE);
         const std::uint64_t lds = ((1u << lb) + ((1u << lb) >> kLE)) * 4ull;
-        const unsigned phases = (r.log_n + kLE - 1) / kLE;
-        const std::uint64_t resident = std::uint64_t(device_cu_count()) * kernel.resident();
-        grid_ = static_cast<unsigned>(phases >= 3 ? std::min<std::uint64_t>(tiles, resident) : tiles);
+        grid_ = static_cast<unsigned>(std::min<std::uint64_t>(tiles, 0x7fffffffull));
         algorithm = r.fp16_final ? "fwht-fp16-fp32-resident-r16" : "fwht-fp32-resident-r16";
         reason = "whole rows resident in one workgroup (" + std::to_string(threads) +
                  " threads x 16 registers, padded LDS exchange)" +
@@ -420,9 +399,9 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
     supported(r.log_n <= kMaxResidentLog,
               "FWHT lengths above 2^" + std::to_string(kMaxResidentLog) + " are not yet lowered for gfx950");
     supported(!r.allow_mma || r.fp16_final, "MFMA Hadamard blocks require FP16 storage");
-    const Kernel kernel = r.fp16_final ? resident_launcher<F16Io>(r.log_n) : resident_launcher<F32Io>(r.log_n);
-    require(kernel.launch != nullptr, "FWHT length has no launcher");
-    return std::make_unique<FwhtExecutor>(r, kernel);
+    const Launch launch = r.fp16_final ? resident_launcher<F16Io>(r.log_n) : resident_launcher<F32Io>(r.log_n);
+    require(launch != nullptr, "FWHT length has no launcher");
+    return std::make_unique<FwhtExecutor>(r, launch);
 }
 
 }  // namespace cbw
