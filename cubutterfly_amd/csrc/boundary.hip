@@ -1,0 +1,117 @@
+// Semantic boundary for strided sides and FWHT / FFT logical orders: gather
+// the input into packed natural order, run the packed transform, scatter the
+// result (the reference's boundary plan, src/c_api.cpp:3085-3130, 5064-5085,
+// with its ordered gather / scatter, src/general_kernels.cu:30-54, 475-535).
+//
+// Element (b, j) of the packed buffer is element b * batch_stride +
+// r(j) * stride of the strided side, r(j) = j, or the log2 n-bit reversal of j
+// for a bit-reversed logical order. Each thread moves consecutive packed
+// elements, so the packed side is coalesced; the strided side is as
+// contiguous as its stride allows.
+#include <hip/hip_runtime.h>
+
+#include "json.hpp"
+#include "planner.hpp"
+
+namespace cbw {
+namespace {
+
+constexpr unsigned kThreads = 256;
+
+template <class T, bool GATHER>
+__global__ __launch_bounds__(kThreads) void boundary_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                                            std::uint64_t count, std::uint32_t log_n,
+                                                            std::uint64_t stride, std::uint64_t batch_stride,
+                                                            bool reversed) {
+    const std::uint64_t mask = (std::uint64_t{1} << log_n) - 1u;
+    for (std::uint64_t linear = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; linear < count;
+         linear += std::uint64_t(gridDim.x) * kThreads) {
+        const std::uint64_t j = linear & mask;
+        const std::uint64_t r = reversed ? (__brevll(j) >> (64u - log_n)) : j;
+        const std::uint64_t physical = (linear >> log_n) * batch_stride + r * stride;
+        if constexpr (GATHER) dst[linear] = src[physical];
+        else dst[physical] = src[linear];
+    }
+}
+
+template <class T>
+void launch_boundary(bool gather, const void* src, void* dst, std::uint64_t count, std::uint32_t log_n,
+                     std::uint64_t stride, std::uint64_t batch_stride, bool reversed, hipStream_t stream) {
+    const std::uint64_t blocks = std::min<std::uint64_t>((count + kThreads - 1) / kThreads, 65536);
+    if (gather)
+        hipLaunchKernelGGL((boundary_kernel<T, true>), dim3(unsigned(blocks)), dim3(kThreads), 0, stream,
+                           static_cast<const T*>(src), static_cast<T*>(dst), count, log_n, stride, batch_stride,
+                           reversed);
+    else
+        hipLaunchKernelGGL((boundary_kernel<T, false>), dim3(unsigned(blocks)), dim3(kThreads), 0, stream,
+                           static_cast<const T*>(src), static_cast<T*>(dst), count, log_n, stride, batch_stride,
+                           reversed);
+    hip_check(hipGetLastError(), "boundary gather / scatter launch");
+}
+
+std::size_t align16(std::size_t bytes) { return (bytes + 15) & ~std::size_t{15}; }
+
+class BoundaryExecutor final : public Executor {
+  public:
+    BoundaryExecutor(const Request& r, std::unique_ptr<Executor> child) : r_(r), child_(std::move(child)) {
+        algorithm = "semantic-boundary[" + child_->algorithm + "]";
+        reason = "strided or reordered sides: gather to packed natural order, packed transform, scatter; child: " +
+                 child_->reason;
+        json::Writer w;
+        w.begin_object()
+            .field("schema_version", 1u)
+            .field("kind", "semantic-boundary")
+            .field("boundary", "gather-natural-child-scatter")
+            .field("input_stride", r.in_stride)
+            .field("input_batch_stride", r.in_batch_stride)
+            .field("input_bit_reversed", r.input_bit_reversed)
+            .field("output_stride", r.out_stride)
+            .field("output_batch_stride", r.out_batch_stride)
+            .field("output_bit_reversed", r.output_bit_reversed)
+            .field("workspace_bytes", std::uint64_t(workspace_bytes()))
+            .key("child")
+            .value_raw(child_->mapping_json)
+            .end_object();
+        mapping_json = w.str();
+    }
+    std::size_t workspace_bytes() const override { return 2 * align16(r_.data_bytes()) + child_->workspace_bytes(); }
+    void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
+        require(ws != nullptr, "a semantic-boundary plan needs its workspace");
+        auto* first = static_cast<unsigned char*>(ws);
+        auto* second = first + align16(r_.data_bytes());
+        auto* child_ws = child_->workspace_bytes() ? second + align16(r_.data_bytes()) : nullptr;
+        const std::uint64_t count = r_.n * r_.batch;
+        move(true, in, first, count, r_.in_stride, r_.in_batch_stride, r_.input_bit_reversed, stream);
+        child_->execute(first, second, child_ws, stream);
+        move(false, second, out, count, r_.out_stride, r_.out_batch_stride, r_.output_bit_reversed, stream);
+    }
+
+  private:
+    void move(bool gather, const void* src, void* dst, std::uint64_t count, std::uint64_t stride,
+              std::uint64_t batch_stride, bool reversed, hipStream_t stream) const {
+        switch (r_.element_bytes) {
+            case 2: launch_boundary<std::uint16_t>(gather, src, dst, count, r_.log_n, stride, batch_stride, reversed, stream); break;
+            case 4: launch_boundary<std::uint32_t>(gather, src, dst, count, r_.log_n, stride, batch_stride, reversed, stream); break;
+            case 8: launch_boundary<std::uint64_t>(gather, src, dst, count, r_.log_n, stride, batch_stride, reversed, stream); break;
+            default: throw NotSupported("boundary element size has no gfx950 kernel");
+        }
+    }
+    Request r_;
+    std::unique_ptr<Executor> child_;
+};
+
+}  // namespace
+
+std::unique_ptr<Executor> make_boundary_executor(const Request& r) {
+    Request child = r;
+    child.boundary = false;
+    child.in_place = false;
+    child.input_bit_reversed = child.output_bit_reversed = false;
+    child.in_stride = child.out_stride = 1;
+    child.in_batch_stride = child.out_batch_stride = r.n;
+    child.policy = CUBUTTERFLY_ALGORITHM_DEFAULT;
+    child.explicit_algorithm.clear();
+    return std::make_unique<BoundaryExecutor>(r, plan_executor(child));
+}
+
+}  // namespace cbw

@@ -365,7 +365,8 @@ cubutterflyStatus_t cubutterflyCreatePlan(cubutterflyHandle_t handle, cubutterfl
                                created->executor->algorithm + ")");
             created->source = CUBUTTERFLY_SELECTION_EXPLICIT;
         }
-        created->input_bytes = created->output_bytes = created->request.data_bytes();
+        created->input_bytes = created->request.span_bytes(true);
+        created->output_bytes = created->request.span_bytes(false);
         created->workspace_bytes = created->executor->workspace_bytes();
         log_event(handle, CUBUTTERFLY_LOG_INFO, "plan-created", created->executor->algorithm);
         *plan = created.release();

@@ -6,6 +6,8 @@
 #include <algorithm>
 #include <cmath>
 #include <limits>
+#include <numeric>
+#include <unordered_set>
 
 namespace cbw {
 namespace {
@@ -49,6 +51,87 @@ bool side_bit_reversed(const cubutterflyDescriptor& d, bool input) {
         reversed = true;
     }
     return reversed;
+}
+
+// Normalised layout of one side: empty strides mean packed, a zero batch
+// stride means the axis span (reference semantic_contract.cpp:104-123).
+struct SideLayout {
+    std::vector<std::size_t> strides;
+    std::size_t batch_stride = 0;
+};
+
+std::size_t checked_mul(std::size_t a, std::size_t b) {
+    require(b == 0 || a <= std::numeric_limits<std::size_t>::max() / b, "layout size overflows size_t");
+    return a * b;
+}
+std::size_t checked_add(std::size_t a, std::size_t b) {
+    require(a <= std::numeric_limits<std::size_t>::max() - b, "layout size overflows size_t");
+    return a + b;
+}
+
+// Whether the addresses sum_k c_k s_k (0 <= c_k < n_k) of a layout repeat.
+// Sorted by stride, a layout whose every stride clears the span of the
+// smaller ones is one-to-one. Otherwise a pair (s_a, n_a), (s_b, n_b) with
+// n_a - 1 >= s_b / g and n_b - 1 >= s_a / g (g = gcd) has the collision
+// (s_b / g) s_a = (s_a / g) s_b. Small layouts are enumerated; larger ones
+// with no such pair are accepted (as the reference's normaliser does,
+// semantic_contract.cpp:55-103).
+bool layout_overlaps(std::vector<std::pair<std::size_t, std::size_t>> dims) {
+    std::sort(dims.begin(), dims.end());
+    std::size_t covered = 1;
+    bool nested = true;
+    for (const auto& [stride, extent] : dims) {
+        if (stride < covered) nested = false;
+        covered = checked_add(covered, checked_mul(extent - 1, stride));
+    }
+    if (nested) return false;
+    for (std::size_t a = 0; a < dims.size(); ++a)
+        for (std::size_t b = a + 1; b < dims.size(); ++b) {
+            const std::size_t g = std::gcd(dims[a].first, dims[b].first);
+            if (dims[a].second - 1 >= dims[b].first / g && dims[b].second - 1 >= dims[a].first / g) return true;
+        }
+    std::size_t points = 1;
+    for (const auto& dim : dims) {
+        if (dim.second > 65536 / points) return false;
+        points *= dim.second;
+    }
+    std::unordered_set<std::size_t> seen;
+    for (std::size_t index = 0; index < points; ++index) {
+        std::size_t rest = index, address = 0;
+        for (const auto& [stride, extent] : dims) {
+            address += (rest % extent) * stride;
+            rest /= extent;
+        }
+        if (!seen.insert(address).second) return true;
+    }
+    return false;
+}
+
+SideLayout side_layout(const cubutterflyDescriptor& d, bool input) {
+    SideLayout l;
+    l.strides = input ? d.input_strides : d.output_strides;
+    l.batch_stride = input ? d.input_batch_stride : d.output_batch_stride;
+    if (l.strides.empty()) {
+        l.strides.resize(d.rank);
+        std::size_t stride = 1;
+        for (std::size_t axis = d.rank; axis-- > 0;) {
+            l.strides[axis] = stride;
+            stride = checked_mul(stride, d.extents[axis]);
+        }
+    }
+    require(l.strides.size() == d.rank, "one stride per axis is required");
+    std::size_t span = 1;
+    std::vector<std::pair<std::size_t, std::size_t>> dims;
+    for (std::size_t axis = 0; axis < d.rank; ++axis) {
+        require(l.strides[axis] > 0, "axis strides must be positive");
+        span = checked_add(span, checked_mul(d.extents[axis] - 1, l.strides[axis]));
+        if (d.extents[axis] > 1) dims.emplace_back(l.strides[axis], d.extents[axis]);
+    }
+    if (l.batch_stride == 0) l.batch_stride = span;
+    checked_add(span, checked_mul(d.batch - 1, l.batch_stride));
+    if (d.batch > 1) dims.emplace_back(l.batch_stride, d.batch);
+    require(!layout_overlaps(dims), "descriptor layout overlaps");
+    return l;
 }
 
 }  // namespace
@@ -119,6 +202,8 @@ void validate_descriptor(const cubutterflyDescriptor& d) {
             if (orders[axis] == CUBUTTERFLY_ORDER_BIT_REVERSED)
                 require(is_pow2(d.extents[axis]), "bit-reversed order requires a power-of-two extent");
     }
+    (void)side_layout(d, true);
+    (void)side_layout(d, false);
     // Epilogue contract (reference src/butterfly.cu:569-576): a non-unit output
     // scale or final-storage rounding needs FP16 FWHT with FP32 compute.
     if (d.output_scale != 1.0 || d.output_rounding == CUBUTTERFLY_ROUNDING_FINAL_STORAGE)
@@ -146,13 +231,12 @@ Request lower_request(const cubutterflyDescriptor& d) {
               "APPT static layouts are not executable");
     const std::size_t n = d.extents[0];
     supported(is_pow2(n) && n >= 2, "only power-of-two lengths >= 2 are executable");
-    for (bool input : {true, false}) {
-        const auto& strides = input ? d.input_strides : d.output_strides;
-        const auto batch_stride = input ? d.input_batch_stride : d.output_batch_stride;
-        supported((strides.empty() || strides[0] == 1) && (batch_stride == 0 || batch_stride == n || d.batch == 1),
-                  "only packed layouts are executable");
-    }
     Request r;
+    const SideLayout in = side_layout(d, true), out = side_layout(d, false);
+    r.in_stride = in.strides[0];
+    r.out_stride = out.strides[0];
+    r.in_batch_stride = in.batch_stride;
+    r.out_batch_stride = out.batch_stride;
     r.n = n;
     r.log_n = log2_u64(n);
     r.batch = d.batch;
@@ -164,11 +248,19 @@ Request lower_request(const cubutterflyDescriptor& d) {
     r.input_bit_reversed = side_bit_reversed(d, true);
     r.output_bit_reversed = side_bit_reversed(d, false);
     r.element_bytes = storage_bytes(d.storage);
+    // Strided sides, and FWHT / FFT logical orders, go through the semantic
+    // boundary: gather to packed natural order, the packed transform,
+    // scatter (reference src/c_api.cpp:2969-2993, 5064-5085). NTT orders on
+    // packed sides are native to the NTT kernels.
+    const auto packed = [&](std::size_t stride, std::size_t batch_stride) {
+        return stride == 1 && (d.batch == 1 || batch_stride == n);
+    };
+    const bool strided = !packed(r.in_stride, r.in_batch_stride) || !packed(r.out_stride, r.out_batch_stride);
+    r.boundary = strided || (d.op != CUBUTTERFLY_OPERATOR_NTT && (r.input_bit_reversed || r.output_bit_reversed));
     switch (d.op) {
         case CUBUTTERFLY_OPERATOR_FWHT:
             r.op = Op::Fwht;
             r.normalize = r.inverse && d.normalize_inverse;
-            supported(!r.input_bit_reversed && !r.output_bit_reversed, "FWHT logical reordering is not executable");
             if (d.storage == CUBUTTERFLY_DATA_FP16) {
                 supported(d.compute == CUBUTTERFLY_COMPUTE_FP32 &&
                               d.output_rounding == CUBUTTERFLY_ROUNDING_FINAL_STORAGE,
@@ -189,7 +281,6 @@ Request lower_request(const cubutterflyDescriptor& d) {
                           (d.compute == CUBUTTERFLY_COMPUTE_NATIVE || d.compute == CUBUTTERFLY_COMPUTE_FP32),
                       "FFT executes COMPLEX_FP32 storage with FP32 compute");
             supported(d.fft_output_scale == 1.0, "FFT output scale is not executable");
-            supported(!r.input_bit_reversed && !r.output_bit_reversed, "FFT logical reordering is not executable");
             break;
         case CUBUTTERFLY_OPERATOR_NTT: {
             r.op = Op::Ntt;

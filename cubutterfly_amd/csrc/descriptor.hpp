@@ -68,7 +68,17 @@ struct Request {
     cubutterflyAlgorithmPolicy_t policy = CUBUTTERFLY_ALGORITHM_DEFAULT;
     std::string explicit_algorithm;
     std::size_t element_bytes = 0;
+    // Normalised element and batch strides of each side (packed: 1 and n).
+    std::uint64_t in_stride = 1, out_stride = 1, in_batch_stride = 0, out_batch_stride = 0;
+    // The sides are strided, or carry FWHT / FFT logical orders: the plan
+    // gathers, runs the packed natural-order transform and scatters.
+    bool boundary = false;
     std::size_t data_bytes() const { return static_cast<std::size_t>(n * batch) * element_bytes; }
+    // Bytes a side spans: (n - 1) stride + (batch - 1) batch stride + 1 elements.
+    std::size_t span_bytes(bool input) const {
+        const std::uint64_t s = input ? in_stride : out_stride, bs = input ? in_batch_stride : out_batch_stride;
+        return static_cast<std::size_t>((n - 1) * s + (batch - 1) * bs + 1) * element_bytes;
+    }
 };
 
 // Full semantic validation (std::invalid_argument), then the executable

@@ -12,8 +12,11 @@ namespace cbw {
 std::unique_ptr<Executor> make_fwht_executor(const Request& r);
 std::unique_ptr<Executor> make_fft_executor(const Request& r);
 std::unique_ptr<Executor> make_ntt_executor(const Request& r);
+// Gather / packed child / scatter, for strided sides and FWHT / FFT orders.
+std::unique_ptr<Executor> make_boundary_executor(const Request& r);
 
 inline std::unique_ptr<Executor> plan_executor(const Request& r) {
+    if (r.boundary) return make_boundary_executor(r);
     switch (r.op) {
         case Op::Fwht: return make_fwht_executor(r);
         case Op::Fft: return make_fft_executor(r);
