@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Headline benchmark of the MI355X butterfly path (one GPU).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c2|c3a|c3b|c4|c5a|c5b|copy]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c1p|c2|c3a|c3b|c4|c5a|c5b|copy]
                 [--no-cpu] [--verify] [--eager]
 
 A step is one call of the hot path over one batch of the named BASELINE
@@ -107,6 +107,49 @@ class FwhtFp32(Workload):
             elapsed += time.perf_counter() - t0
             reps += 1
         return elapsed, reps * self.batch, f"{reps} full C1 batches (4096 x 4096) through reference_fwht"
+
+
+class FwhtFp32Pitched(FwhtFp32):
+    """C1's transform on pitched rows (row stride n + 64 on both sides): the
+    semantic-boundary plan (gather, packed transform, scatter)."""
+    name = "c1p"
+    description = ("FWHT fp32 unnormalized forward, batch 4096 x n=4096, rows pitched at n + 64 on both sides "
+                   "(semantic boundary), integer inputs in [-8,8]")
+    PAD = 64
+
+    def setup(self, torch, lib, stream):
+        import cubutterfly_amd as cb
+        from cubutterfly_amd import workloads
+        n = 1 << self.log_n
+        pitch = n + self.PAD
+        t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
+                         extents=[n], batch=self.batch, input_strides=[1], input_batch_stride=pitch,
+                         output_strides=[1], output_batch_stride=pitch)
+        plan = cb.Plan(lib, t, stream=stream)
+        ws = plan.workspace_size()
+        self.workspace = torch.empty(ws, dtype=torch.uint8, device="cuda")
+        plan.set_workspace(self.workspace, ws)
+        self.plans = [plan]
+        self.host = workloads.fwht_integer_input(self.log_n, self.batch, seed=1)
+        padded = np.zeros((self.batch, pitch), dtype=np.float32)
+        padded[:, :n] = self.host
+        flat = padded.reshape(-1)[: (self.batch - 1) * pitch + n]
+        sets = self._rotation(torch, self.bytes_per_call)
+        src = _np_to_torch(torch, np.ascontiguousarray(flat)).to("cuda")
+        self.inputs = [src.clone() for _ in range(sets)]
+        self.outputs = [torch.zeros_like(src) for _ in range(sets)]
+
+    def verify(self, torch):
+        import oracle
+        n, pitch = 1 << self.log_n, (1 << self.log_n) + self.PAD
+        flat = self.outputs[0].cpu().numpy()
+        got = np.zeros((self.batch, pitch), dtype=np.float32).reshape(-1)
+        got[: flat.size] = flat
+        got = got.reshape(self.batch, pitch)[:, :n]
+        return bool(np.array_equal(got, oracle.fwht_f32(self.host, threads=oracle.default_threads())))
+
+    def kernel_name(self):
+        return "fwht_resident_kernel (inside " + self.plans[0].algorithm_name() + ")"
 
 
 class NttNegacyclic(Workload):
@@ -367,7 +410,7 @@ class DeviceCopy(Workload):
         return 1.0, 0, "no CPU baseline for the calibration copy"
 
 
-WORKLOADS = {"c1": FwhtFp32, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1), "c3b": lambda: FftC64(14, 1024),
+WORKLOADS = {"c1": FwhtFp32, "c1p": FwhtFp32Pitched, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1), "c3b": lambda: FftC64(14, 1024),
              "c4": RnsNegacyclic, "c5a": lambda: FwhtFp16(16384, 4096), "c5b": lambda: FwhtFp16(524288, 128),
              "copy": DeviceCopy}
 DEFAULT_WORKLOAD = "c2"

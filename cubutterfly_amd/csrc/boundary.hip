@@ -34,9 +34,42 @@ __global__ __launch_bounds__(kThreads) void boundary_kernel(const T* __restrict_
     }
 }
 
+// Unit stride in natural order (pitched rows): 16-byte chunks of a row,
+// V = 16 / sizeof(element) elements each, both sides 16-byte aligned.
+template <bool GATHER>
+__global__ __launch_bounds__(kThreads) void pitched_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                           std::uint64_t chunks, std::uint32_t row_log,
+                                                           std::uint64_t pitch) {
+    const std::uint64_t mask = (std::uint64_t{1} << row_log) - 1u;
+    for (std::uint64_t linear = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; linear < chunks;
+         linear += std::uint64_t(gridDim.x) * kThreads) {
+        const std::uint64_t physical = (linear >> row_log) * pitch + (linear & mask);
+        if constexpr (GATHER) dst[linear] = src[physical];
+        else dst[physical] = src[linear];
+    }
+}
+
 template <class T>
 void launch_boundary(bool gather, const void* src, void* dst, std::uint64_t count, std::uint32_t log_n,
                      std::uint64_t stride, std::uint64_t batch_stride, bool reversed, hipStream_t stream) {
+    constexpr std::uint32_t kPerChunk = 16 / sizeof(T);
+    if (!reversed && stride == 1 && (std::uint64_t{1} << log_n) % kPerChunk == 0 && batch_stride % kPerChunk == 0 &&
+        reinterpret_cast<std::uintptr_t>(src) % 16 == 0 && reinterpret_cast<std::uintptr_t>(dst) % 16 == 0) {
+        const std::uint64_t chunks = count / kPerChunk;
+        std::uint32_t row_log = log_n;
+        for (std::uint32_t k = kPerChunk; k > 1; k >>= 1) --row_log;
+        const std::uint64_t blocks = std::min<std::uint64_t>((chunks + kThreads - 1) / kThreads, 65536);
+        if (gather)
+            hipLaunchKernelGGL((pitched_kernel<true>), dim3(unsigned(blocks)), dim3(kThreads), 0, stream,
+                               static_cast<const uint4*>(src), static_cast<uint4*>(dst), chunks, row_log,
+                               batch_stride / kPerChunk);
+        else
+            hipLaunchKernelGGL((pitched_kernel<false>), dim3(unsigned(blocks)), dim3(kThreads), 0, stream,
+                               static_cast<const uint4*>(src), static_cast<uint4*>(dst), chunks, row_log,
+                               batch_stride / kPerChunk);
+        hip_check(hipGetLastError(), "boundary gather / scatter launch");
+        return;
+    }
     const std::uint64_t blocks = std::min<std::uint64_t>((count + kThreads - 1) / kThreads, 65536);
     if (gather)
         hipLaunchKernelGGL((boundary_kernel<T, true>), dim3(unsigned(blocks)), dim3(kThreads), 0, stream,

@@ -34,7 +34,10 @@ def positions(n, batch, stride, batch_stride, reversed_):
 
 
 def batch_stride_of(n, stride, batch_stride):
-    return batch_stride or (n - 1) * stride + 1  # zero means the axis span
+    """Zero means the axis span; a negative value -p means pitched rows, the
+    span plus p padding elements."""
+    span_ = (n - 1) * stride + 1
+    return span_ - batch_stride if batch_stride < 0 else batch_stride or span_
 
 
 def span(n, batch, stride, batch_stride):
@@ -78,6 +81,7 @@ def case(n, batch, dtype, seed, in_layout, out_layout, sentinel):
 def transform(op, n, batch, in_layout, out_layout, **kw):
     (s_in, bs_in, rev_in), (s_out, bs_out, rev_out) = in_layout, out_layout
     order = lambda rev: [cb.LogicalOrder.BIT_REVERSED if rev else cb.LogicalOrder.NATURAL]
+    bs_in, bs_out = (b if b >= 0 else batch_stride_of(n, s, b) for s, b in ((s_in, bs_in), (s_out, bs_out)))
     return cb.Transform(op=op, extents=[n], batch=batch, input_strides=[s_in], input_batch_stride=bs_in,
                         output_strides=[s_out], output_batch_stride=bs_out, input_orders=order(rev_in),
                         output_orders=order(rev_out), **kw)
@@ -88,6 +92,8 @@ LAYOUTS = [
     ((1, 0, True), (2, 0, False)),       # bit-reversed packed input, strided output with gaps
     ((3, 0, False), (1, 0, True)),       # strided input, bit-reversed packed output
     ((1, 0, False), (1, 0, True)),       # packed, logical order only
+    ((1, -8, False), (1, -4, False)),    # pitched rows on both sides
+    ((1, -8, False), (1, -3, False)),    # pitched input, odd output pitch
 ]
 
 
