@@ -10,6 +10,7 @@ there is no CPU fallback. Device pointers may be ints, ctypes pointers or any
 object with data_ptr() (torch tensors); streams are hipStream_t handles.
 """
 import ctypes as ct
+import json
 import operator
 import os
 from dataclasses import dataclass, field
@@ -422,6 +423,13 @@ class Plan:
 
     def execute_steady(self, input, output):
         self.library._call("ExecuteSteady", self._context, self.native_handle, pointer(input), pointer(output))
+
+    def physical_extents(self):
+        """Executed extent of every axis, outermost first."""
+        rank = len(json.loads(self.descriptor_json())["shape"])
+        extents = (ct.c_size_t * rank)()
+        self.library._call("PlanGetPhysicalExtents", self.native_handle, extents, rank)
+        return list(extents)
 
     def selection_source(self):
         value = ct.c_int()

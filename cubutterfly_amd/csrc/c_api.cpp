@@ -7,6 +7,7 @@
 #include "json.hpp"
 #include "planner.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -356,7 +357,7 @@ cubutterflyStatus_t cubutterflyCreatePlan(cubutterflyHandle_t handle, cubutterfl
         created->request = cbw::lower_request(*descriptor);
         if (created->request.policy == CUBUTTERFLY_ALGORITHM_MEASURE)
             log_event(handle, CUBUTTERFLY_LOG_INFO, "measure-static",
-                      "MEASURE uses the static gfx950 model for the rank-1 butterfly path");
+                      "MEASURE uses the static gfx950 model for the butterfly path");
         created->executor = cbw::plan_executor(created->request);
         if (created->request.policy == CUBUTTERFLY_ALGORITHM_EXPLICIT) {
             cbw::supported(created->executor->algorithm == created->request.explicit_algorithm,
@@ -403,8 +404,10 @@ cubutterflyStatus_t cubutterflyPlanGetOutputSize(cubutterflyPlan_t plan, size_t*
 cubutterflyStatus_t cubutterflyPlanGetPhysicalExtents(cubutterflyPlan_t plan, size_t* extents, uint32_t capacity) {
     return protect([&] {
         require(plan && extents, "plan and extents must be non-null");
-        require(capacity >= 1, "extent capacity is too small");
-        extents[0] = plan->request.n;
+        const auto& r = plan->request;
+        require(capacity >= r.rank, "extent capacity is too small");
+        if (r.rank == 1) extents[0] = r.n;
+        else std::copy(r.extents.begin(), r.extents.end(), extents);
     });
 }
 cubutterflyStatus_t cubutterflyPlanGetSelectionSource(cubutterflyPlan_t plan, cubutterflySelectionSource_t* source) {

@@ -1,0 +1,347 @@
+// Rank-2 and higher transforms composed from batched rank-1 plans (the
+// reference's rank-two lowering, src/c_api.cpp:5231-5327, and its generic
+// axis schedule, src/c_api.cpp:623-672, 5163-5219).
+//
+// Axes are transformed innermost first. Before each axis plan a batched
+// tiled transpose moves that axis to the innermost (contiguous) position, so
+// every axis plan is an ordinary packed batched rank-1 plan; after the last
+// axis further transposes restore the original axis order. A batched
+// transpose of G blocks of R x C elements covers every such move: the axes
+// before the moved one form the blocks, the moved axis the rows, the axes
+// after it the columns.
+//
+// FWHT needs none of this: the Sylvester Hadamard matrix of n0 * n1 points
+// is the Kronecker product H(n0) (x) H(n1), and the innermost-first axis
+// order applies the stages from the lowest index bit to the highest, which is
+// the rank-1 stage order. A rank-N FWHT whose point count a single rank-1
+// plan covers therefore runs as that one plan, bit-identically (the inverse
+// with normalisation keeps the per-axis composition, whose per-axis 1/n
+// scaling rounds differently in the subnormal range).
+//
+// Strided sides and bit-reversed logical orders are handled as in the
+// rank-1 semantic boundary: an N-dimensional gather into packed natural
+// order first, an N-dimensional scatter last. A packed natural side is read
+// or written directly by the first or last step.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <numeric>
+
+#include "json.hpp"
+#include "planner.hpp"
+
+namespace cbw {
+namespace {
+
+constexpr unsigned kThreads = 256;
+constexpr unsigned kTile = 64;  // transpose tile edge (elements)
+
+inline std::size_t align16(std::size_t bytes) { return (bytes + 15) & ~std::size_t{15}; }
+
+// dst[g][c][r] = src[g][r][c] for G blocks of 2^log_rows x 2^log_cols
+// elements. Each workgroup moves 64 x 64 tiles through LDS: reads run along
+// the source rows and writes along the destination rows, 64 consecutive
+// elements per wave. The row pitch of 65 elements keeps the column-wise LDS
+// reads on distinct banks.
+template <class T>
+__global__ __launch_bounds__(kThreads) void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                                             std::uint64_t tiles, std::uint32_t log_rows,
+                                                             std::uint32_t log_cols) {
+    __shared__ T tile[kTile][kTile + 1];
+    const std::uint32_t tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
+    const std::uint64_t rows = std::uint64_t{1} << log_rows, cols = std::uint64_t{1} << log_cols;
+    const std::uint32_t lr = log_rows > 6 ? log_rows - 6 : 0, lc = log_cols > 6 ? log_cols - 6 : 0;
+    for (std::uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const std::uint64_t c0 = (t & ((std::uint64_t{1} << lc) - 1)) * kTile;
+        const std::uint64_t r0 = ((t >> lc) & ((std::uint64_t{1} << lr) - 1)) * kTile;
+        const std::uint64_t block = (t >> (lc + lr)) << (log_rows + log_cols);
+        const T* s = src + block;
+        T* d = dst + block;
+        {
+            const std::uint64_t c = c0 + tx;
+#pragma unroll
+            for (unsigned k = 0; k < kTile; k += kThreads / kTile) {
+                const std::uint64_t r = r0 + ty + k;
+                if (r < rows && c < cols) tile[ty + k][tx] = s[(r << log_cols) + c];
+            }
+        }
+        __syncthreads();
+        {
+            const std::uint64_t r = r0 + tx;
+#pragma unroll
+            for (unsigned k = 0; k < kTile; k += kThreads / kTile) {
+                const std::uint64_t c = c0 + ty + k;
+                if (r < rows && c < cols) d[(c << log_rows) + r] = tile[tx][ty + k];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// One side of an N-dimensional layout: element (b, i_0 .. i_{rank-1}) of the
+// packed natural buffer is element b * batch_stride + sum_a r_a(i_a) *
+// stride[a] of the side, r_a the log_extent[a]-bit reversal where bit a of
+// `reversed` is set, else the identity.
+struct NdSide {
+    std::uint32_t rank = 0;
+    std::uint32_t reversed = 0;
+    std::uint32_t log_extent[kMaxRank] = {};
+    std::uint64_t stride[kMaxRank] = {};
+    std::uint64_t batch_stride = 0;
+};
+
+template <class T, bool GATHER>
+__global__ __launch_bounds__(kThreads) void nd_boundary_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                                               std::uint64_t count, NdSide side) {
+    for (std::uint64_t linear = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; linear < count;
+         linear += std::uint64_t(gridDim.x) * kThreads) {
+        std::uint64_t rest = linear, physical = 0;
+        for (int a = int(side.rank) - 1; a >= 0; --a) {
+            const std::uint32_t l = side.log_extent[a];
+            std::uint64_t i = rest & ((std::uint64_t{1} << l) - 1);
+            rest >>= l;
+            if ((side.reversed >> a) & 1u) i = __brevll(i) >> (64u - l);
+            physical += i * side.stride[a];
+        }
+        physical += rest * side.batch_stride;
+        if constexpr (GATHER) dst[linear] = src[physical];
+        else dst[physical] = src[linear];
+    }
+}
+
+template <class T>
+void launch_transpose(const void* src, void* dst, std::uint64_t groups, std::uint32_t log_rows,
+                      std::uint32_t log_cols, hipStream_t stream) {
+    const std::uint32_t lr = log_rows > 6 ? log_rows - 6 : 0, lc = log_cols > 6 ? log_cols - 6 : 0;
+    const std::uint64_t tiles = groups << (lr + lc);
+    const std::uint64_t blocks = std::min<std::uint64_t>(tiles, std::uint64_t{1} << 20);
+    hipLaunchKernelGGL((transpose_kernel<T>), dim3(unsigned(blocks)), dim3(kThreads), 0, stream,
+                       static_cast<const T*>(src), static_cast<T*>(dst), tiles, log_rows, log_cols);
+    hip_check(hipGetLastError(), "composite transpose launch");
+}
+
+template <class T>
+void launch_nd_boundary(bool gather, const void* src, void* dst, std::uint64_t count, const NdSide& side,
+                        hipStream_t stream) {
+    const std::uint64_t blocks = std::min<std::uint64_t>((count + kThreads - 1) / kThreads, 65536);
+    if (gather)
+        hipLaunchKernelGGL((nd_boundary_kernel<T, true>), dim3(unsigned(blocks)), dim3(kThreads), 0, stream,
+                           static_cast<const T*>(src), static_cast<T*>(dst), count, side);
+    else
+        hipLaunchKernelGGL((nd_boundary_kernel<T, false>), dim3(unsigned(blocks)), dim3(kThreads), 0, stream,
+                           static_cast<const T*>(src), static_cast<T*>(dst), count, side);
+    hip_check(hipGetLastError(), "composite gather / scatter launch");
+}
+
+// One step of the schedule: an axis plan, or a batched transpose moving one
+// axis innermost.
+struct Step {
+    bool transpose = false;
+    std::size_t child = 0;                // axis plan index (transpose == false)
+    std::uint32_t axis = 0;               // logical axis it transforms
+    std::uint64_t groups = 0;             // transpose: blocks, log2 rows / cols
+    std::uint32_t log_rows = 0, log_cols = 0;
+};
+
+class CompositeExecutor final : public Executor {
+  public:
+    CompositeExecutor(const Request& r, bool flatten) : r_(r) {
+        const std::uint32_t rank = r.rank;
+        std::vector<std::uint32_t> logs(rank);
+        for (std::uint32_t a = 0; a < rank; ++a) logs[a] = log2_u64(r.extents[a]);
+        direct_in_ = packed_natural(true);
+        direct_out_ = packed_natural(false);
+        in_side_ = side(true, logs);
+        out_side_ = side(false, logs);
+        std::vector<std::string> names;
+        if (flatten) {
+            children_.push_back(plan_executor(axis_request(r.n, r.batch)));
+            steps_.push_back(Step{false, 0, 0, 0, 0, 0});
+        } else {
+            // Innermost axis first; each axis is first moved innermost.
+            std::vector<std::uint32_t> order(rank);
+            std::iota(order.begin(), order.end(), 0u);
+            const auto move_innermost = [&](std::uint32_t axis) {
+                const auto pos = std::size_t(std::find(order.begin(), order.end(), axis) - order.begin());
+                if (pos + 1 == rank) return;
+                Step s;
+                s.transpose = true;
+                s.groups = r.batch;
+                for (std::size_t i = 0; i < pos; ++i) s.groups <<= logs[order[i]];
+                s.log_rows = logs[axis];
+                for (std::size_t i = pos + 1; i < rank; ++i) s.log_cols += logs[order[i]];
+                steps_.push_back(s);
+                order.erase(order.begin() + std::ptrdiff_t(pos));
+                order.push_back(axis);
+            };
+            for (std::uint32_t k = 0; k < rank; ++k) {
+                const std::uint32_t axis = rank - 1 - k;
+                move_innermost(axis);
+                const std::uint64_t e = r.extents[axis];
+                children_.push_back(plan_executor(axis_request(e, r.batch * (r.n / e))));
+                Step s;
+                s.child = children_.size() - 1;
+                s.axis = axis;
+                steps_.push_back(s);
+            }
+            for (std::uint32_t axis = 0; axis < rank; ++axis) move_innermost(axis);
+        }
+        for (const auto& c : children_) {
+            names.push_back(c->algorithm);
+            child_ws_ = std::max(child_ws_, c->workspace_bytes());
+        }
+        std::string joined;
+        for (std::size_t i = 0; i < names.size(); ++i) joined += (i ? "," : "") + names[i];
+        algorithm = std::string(flatten ? (rank == 2 ? "rank2-kronecker" : "rankN-kronecker")
+                                        : (rank == 2 ? "rank2-transpose" : "rankN-composite")) +
+                    "[" + joined + "]" + (direct_in_ ? "+direct-input" : "") + (direct_out_ ? "+direct-output" : "");
+        reason = flatten ? "FWHT of the flattened point count: H(n0 n1) = H(n0) (x) H(n1), same stage order"
+                         : "one batched rank-1 plan per axis, innermost first, tiled transposes between";
+        json::Writer w;
+        w.begin_object()
+            .field("schema_version", 1u)
+            .field("kind", "composition")
+            .field("rank", rank)
+            .field("lowering", flatten ? "kronecker" : "transpose");
+        w.begin_array("extents");
+        for (auto e : r.extents) w.value(e);
+        w.end_array();
+        w.begin_array("schedule");
+        for (const auto& s : steps_) {
+            w.begin_object();
+            if (s.transpose) {
+                w.field("step", "transpose").field("blocks", s.groups).field("rows", std::uint64_t{1} << s.log_rows)
+                    .field("cols", std::uint64_t{1} << s.log_cols);
+            } else {
+                w.field("step", "axis").field("axis", s.axis).key("child").value_raw(children_[s.child]->mapping_json);
+            }
+            w.end_object();
+        }
+        w.end_array();
+        w.field("direct_input_boundary", direct_in_)
+            .field("direct_output_boundary", direct_out_)
+            .field("workspace_bytes", std::uint64_t(workspace_bytes()))
+            .end_object();
+        mapping_json = w.str();
+    }
+
+    std::size_t workspace_bytes() const override {
+        // Two ping-pong buffers of the packed data, then the largest child's.
+        const bool one_buffer = steps_.size() == 1 && (direct_in_ || direct_out_);
+        const std::size_t buffers = steps_.size() == 1 && direct_in_ && direct_out_ ? 0 : one_buffer ? 1 : 2;
+        return buffers * align16(r_.data_bytes()) + align16(child_ws_);
+    }
+
+    void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
+        const std::size_t bytes = align16(r_.data_bytes());
+        const std::size_t ws_bytes = workspace_bytes();
+        require(ws_bytes == 0 || ws != nullptr, "a composite plan needs its workspace");
+        auto* base = static_cast<unsigned char*>(ws);
+        unsigned char* buffer[2] = {base, base + bytes};
+        const std::size_t buffers = (ws_bytes - align16(child_ws_)) / (bytes ? bytes : 1);
+        void* child_ws = child_ws_ ? base + buffers * bytes : nullptr;
+        const std::uint64_t count = r_.n * r_.batch;
+
+        // Ping-pong: the next destination is the buffer the current data is
+        // not in (the caller's input counts as neither).
+        int next = 0;
+        const void* cur = in;
+        if (!direct_in_) {
+            move(true, in, buffer[0], count, in_side_, stream);
+            cur = buffer[0];
+            next = 1;
+        }
+        for (std::size_t i = 0; i < steps_.size(); ++i) {
+            const bool last = i + 1 == steps_.size();
+            void* dst = last && direct_out_ ? out : buffer[next];
+            const auto& s = steps_[i];
+            if (s.transpose) transpose(cur, dst, s, stream);
+            else children_[s.child]->execute(cur, dst, child_ws, stream);
+            cur = dst;
+            next = dst == buffer[0] ? 1 : 0;
+        }
+        if (!direct_out_) move(false, cur, out, count, out_side_, stream);
+    }
+
+  private:
+    Request axis_request(std::uint64_t n, std::uint64_t batch) const {
+        Request c = r_;
+        c.rank = 1;
+        c.extents.clear();
+        c.in_strides.clear();
+        c.out_strides.clear();
+        c.in_reversed.clear();
+        c.out_reversed.clear();
+        c.n = n;
+        c.log_n = log2_u64(n);
+        c.batch = batch;
+        c.boundary = false;
+        c.in_place = false;
+        c.input_bit_reversed = c.output_bit_reversed = false;
+        c.in_stride = c.out_stride = 1;
+        c.in_batch_stride = c.out_batch_stride = n;
+        c.policy = CUBUTTERFLY_ALGORITHM_DEFAULT;
+        c.explicit_algorithm.clear();
+        return c;
+    }
+
+    bool packed_natural(bool input) const {
+        const auto& strides = input ? r_.in_strides : r_.out_strides;
+        const auto& reversed = input ? r_.in_reversed : r_.out_reversed;
+        std::uint64_t expect = 1;
+        for (std::size_t a = r_.rank; a-- > 0;) {
+            if (strides[a] != expect || reversed[a]) return false;
+            expect *= r_.extents[a];
+        }
+        return r_.batch == 1 || (input ? r_.in_batch_stride : r_.out_batch_stride) == r_.n;
+    }
+
+    NdSide side(bool input, const std::vector<std::uint32_t>& logs) const {
+        NdSide s;
+        s.rank = r_.rank;
+        const auto& strides = input ? r_.in_strides : r_.out_strides;
+        const auto& reversed = input ? r_.in_reversed : r_.out_reversed;
+        for (std::uint32_t a = 0; a < r_.rank; ++a) {
+            s.log_extent[a] = logs[a];
+            s.stride[a] = strides[a];
+            if (reversed[a]) s.reversed |= 1u << a;
+        }
+        s.batch_stride = input ? r_.in_batch_stride : r_.out_batch_stride;
+        return s;
+    }
+
+    void transpose(const void* src, void* dst, const Step& s, hipStream_t stream) const {
+        switch (r_.element_bytes) {
+            case 4: launch_transpose<std::uint32_t>(src, dst, s.groups, s.log_rows, s.log_cols, stream); break;
+            case 8: launch_transpose<std::uint64_t>(src, dst, s.groups, s.log_rows, s.log_cols, stream); break;
+            default: throw NotSupported("transpose element size has no gfx950 kernel");
+        }
+    }
+
+    void move(bool gather, const void* src, void* dst, std::uint64_t count, const NdSide& side,
+              hipStream_t stream) const {
+        switch (r_.element_bytes) {
+            case 4: launch_nd_boundary<std::uint32_t>(gather, src, dst, count, side, stream); break;
+            case 8: launch_nd_boundary<std::uint64_t>(gather, src, dst, count, side, stream); break;
+            default: throw NotSupported("boundary element size has no gfx950 kernel");
+        }
+    }
+
+    Request r_;
+    bool direct_in_ = false, direct_out_ = false;
+    NdSide in_side_, out_side_;
+    std::vector<std::unique_ptr<Executor>> children_;
+    std::vector<Step> steps_;
+    std::size_t child_ws_ = 0;
+};
+
+}  // namespace
+
+std::unique_ptr<Executor> make_composite_executor(const Request& r) {
+    require(r.rank >= 2 && r.rank <= kMaxRank && r.extents.size() == r.rank, "composite plans need rank 2 to 8");
+    // A flattened FWHT is one rank-1 plan; it exists up to the resident length.
+    const bool flatten = r.op == Op::Fwht && !(r.inverse && r.normalize) && r.log_n <= 13;
+    return std::make_unique<CompositeExecutor>(r, flatten);
+}
+
+}  // namespace cbw

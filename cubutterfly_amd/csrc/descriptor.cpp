@@ -222,19 +222,39 @@ void validate_descriptor(const cubutterflyDescriptor& d) {
 
 Request lower_request(const cubutterflyDescriptor& d) {
     validate_descriptor(d);
-    supported(d.rank == 1, "only rank-1 transforms are executable");
+    supported(d.rank <= kMaxRank, "ranks above eight are not executable");
     supported(d.length_mode == CUBUTTERFLY_LENGTH_STANDARD, "zero-extended embedding is not executable");
     supported(d.execution_mode != CUBUTTERFLY_EXECUTION_XD, "XD execution requires a multidimensional descriptor");
     supported(d.fft_type == CUBUTTERFLY_FFT_C2C, "only C2C FFTs are executable");
     supported(d.input_ntt_layout != CUBUTTERFLY_NTT_LAYOUT_APPT_STATIC &&
                   d.output_ntt_layout != CUBUTTERFLY_NTT_LAYOUT_APPT_STATIC,
               "APPT static layouts are not executable");
-    const std::size_t n = d.extents[0];
-    supported(is_pow2(n) && n >= 2, "only power-of-two lengths >= 2 are executable");
+    std::size_t n = 1;
+    for (auto e : d.extents) {
+        supported(is_pow2(e) && e >= 2, "only power-of-two lengths >= 2 are executable");
+        n = checked_mul(n, e);
+    }
+    (void)checked_mul(checked_mul(n, d.batch), storage_bytes(d.storage));
     Request r;
     const SideLayout in = side_layout(d, true), out = side_layout(d, false);
-    r.in_stride = in.strides[0];
-    r.out_stride = out.strides[0];
+    r.rank = d.rank;
+    if (d.rank == 1) {
+        r.in_stride = in.strides[0];
+        r.out_stride = out.strides[0];
+    } else {
+        // Rank two and above: per-axis layout for the composite plan, which
+        // brings each axis innermost in turn (reference src/c_api.cpp:4578-4600).
+        r.extents.assign(d.extents.begin(), d.extents.end());
+        r.in_strides.assign(in.strides.begin(), in.strides.end());
+        r.out_strides.assign(out.strides.begin(), out.strides.end());
+        for (bool input : {true, false}) {
+            const auto& orders = input ? d.input_orders : d.output_orders;
+            auto& reversed = input ? r.in_reversed : r.out_reversed;
+            reversed.assign(d.rank, 0);
+            for (std::size_t axis = 0; axis < orders.size(); ++axis)
+                reversed[axis] = orders[axis] == CUBUTTERFLY_ORDER_BIT_REVERSED;
+        }
+    }
     r.in_batch_stride = in.batch_stride;
     r.out_batch_stride = out.batch_stride;
     r.n = n;
@@ -245,8 +265,8 @@ Request lower_request(const cubutterflyDescriptor& d) {
     r.storage = d.storage;
     r.policy = d.algorithm_policy;
     r.explicit_algorithm = d.explicit_algorithm;
-    r.input_bit_reversed = side_bit_reversed(d, true);
-    r.output_bit_reversed = side_bit_reversed(d, false);
+    r.input_bit_reversed = d.rank == 1 && side_bit_reversed(d, true);
+    r.output_bit_reversed = d.rank == 1 && side_bit_reversed(d, false);
     r.element_bytes = storage_bytes(d.storage);
     // Strided sides, and FWHT / FFT logical orders, go through the semantic
     // boundary: gather to packed natural order, the packed transform,
@@ -256,7 +276,8 @@ Request lower_request(const cubutterflyDescriptor& d) {
         return stride == 1 && (d.batch == 1 || batch_stride == n);
     };
     const bool strided = !packed(r.in_stride, r.in_batch_stride) || !packed(r.out_stride, r.out_batch_stride);
-    r.boundary = strided || (d.op != CUBUTTERFLY_OPERATOR_NTT && (r.input_bit_reversed || r.output_bit_reversed));
+    r.boundary = d.rank == 1 &&
+                 (strided || (d.op != CUBUTTERFLY_OPERATOR_NTT && (r.input_bit_reversed || r.output_bit_reversed)));
     switch (d.op) {
         case CUBUTTERFLY_OPERATOR_FWHT:
             r.op = Op::Fwht;
@@ -265,6 +286,7 @@ Request lower_request(const cubutterflyDescriptor& d) {
                 supported(d.compute == CUBUTTERFLY_COMPUTE_FP32 &&
                               d.output_rounding == CUBUTTERFLY_ROUNDING_FINAL_STORAGE,
                           "FP16 FWHT requires FP32 compute with final-storage rounding");
+                supported(d.rank == 1, "FP16 FWHT is executable at rank one");
                 r.fp16_final = true;
                 r.output_scale = static_cast<float>(d.output_scale);
                 r.allow_mma = d.arithmetic_policy == CUBUTTERFLY_ARITHMETIC_ALLOW_FP16_MMA;
@@ -288,6 +310,7 @@ Request lower_request(const cubutterflyDescriptor& d) {
             r.modulus = d.modulus;
             r.word_bits = d.word_bits;
             r.negacyclic = d.ring == CUBUTTERFLY_NTT_RING_NEGACYCLIC;
+            supported(d.rank == 1 || !r.negacyclic, "the negacyclic ring is executable at rank one");
             r.psi = d.psi;
             supported(d.word_bits == 64 || d.modulus < (std::uint64_t{1} << 31),
                       "32-bit NTT words require modulus < 2^31");

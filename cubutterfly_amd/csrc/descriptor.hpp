@@ -48,7 +48,12 @@ namespace cbw {
 
 enum class Op { Fwht, Fft, Ntt };
 
-// A validated, packed, rank-1 power-of-two request.
+// Highest executable rank (reference kGeneralMaxRank).
+constexpr std::uint32_t kMaxRank = 8;
+
+// A validated power-of-two request. Rank 1 is described by n, the strides
+// and the orders below; rank 2 and above additionally by the per-axis
+// vectors (outermost axis first), with n the points per transform.
 struct Request {
     Op op = Op::Fwht;
     cubutterflyDataType_t storage = CUBUTTERFLY_DATA_FP32;
@@ -73,11 +78,24 @@ struct Request {
     // The sides are strided, or carry FWHT / FFT logical orders: the plan
     // gathers, runs the packed natural-order transform and scatters.
     bool boundary = false;
+    // Rank >= 2: per-axis extents, element strides and bit-reversed orders of
+    // each side (outermost axis first). Empty for rank 1.
+    std::uint32_t rank = 1;
+    std::vector<std::uint64_t> extents, in_strides, out_strides;
+    std::vector<std::uint8_t> in_reversed, out_reversed;
     std::size_t data_bytes() const { return static_cast<std::size_t>(n * batch) * element_bytes; }
-    // Bytes a side spans: (n - 1) stride + (batch - 1) batch stride + 1 elements.
+    // Bytes a side spans: the sum over axes of (extent - 1) stride, plus
+    // (batch - 1) batch stride, plus one element.
     std::size_t span_bytes(bool input) const {
-        const std::uint64_t s = input ? in_stride : out_stride, bs = input ? in_batch_stride : out_batch_stride;
-        return static_cast<std::size_t>((n - 1) * s + (batch - 1) * bs + 1) * element_bytes;
+        const std::uint64_t bs = input ? in_batch_stride : out_batch_stride;
+        std::uint64_t last = (batch - 1) * bs;
+        if (rank == 1) {
+            last += (n - 1) * (input ? in_stride : out_stride);
+        } else {
+            const auto& strides = input ? in_strides : out_strides;
+            for (std::size_t axis = 0; axis < extents.size(); ++axis) last += (extents[axis] - 1) * strides[axis];
+        }
+        return static_cast<std::size_t>(last + 1) * element_bytes;
     }
 };
 

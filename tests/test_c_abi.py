@@ -86,7 +86,8 @@ def test_invalid_descriptors_are_rejected(lib):
 
 
 def test_unsupported_lowerings_report_not_supported(lib):
-    two_d = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, extents=[8, 8])
+    two_d = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
+                         output_rounding=cb.OutputRounding.FINAL_STORAGE, extents=[8, 8])
     assert status_of(cb.Plan, lib, two_d) == cb.Status.NOT_SUPPORTED
     zeta = cb.Transform(op=cb.Operator.SUBSET_ZETA, storage=cb.DataType.UINT32, extents=[8])
     assert status_of(cb.Plan, lib, zeta) == cb.Status.NOT_SUPPORTED
