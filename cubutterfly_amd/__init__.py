@@ -372,10 +372,12 @@ class Plan:
     """Plan with its own handle (context) and a caller-bound workspace.
 
     execute() is asynchronous on the plan's stream; input, output and
-    workspace must stay alive until the work completes.
+    workspace must stay alive until the work completes. `cache_path` names
+    the selection cache: DEFAULT plans replay its records, MEASURE plans
+    append the candidate they measured fastest.
     """
 
-    def __init__(self, library, transform, options=None, stream=None):
+    def __init__(self, library, transform, options=None, stream=None, cache_path=None):
         self.library = library
         self._context, self._handle = ct.c_void_p(), ct.c_void_p()
         self._workspace = None
@@ -383,6 +385,8 @@ class Plan:
             library._call("Create", ct.byref(self._context))
             if stream is not None:
                 library._call("SetStream", self._context, pointer(stream))
+            if cache_path is not None:
+                library._call("SetCachePath", self._context, os.fsencode(cache_path))
             if isinstance(transform, Descriptor):
                 if options is not None:
                     raise ValueError("selection options must be set when constructing the Descriptor")

@@ -135,7 +135,7 @@ class BoundaryExecutor final : public Executor {
 
 }  // namespace
 
-std::unique_ptr<Executor> make_boundary_executor(const Request& r) {
+std::unique_ptr<Executor> make_boundary_executor(const Request& r, Selection* sel) {
     Request child = r;
     child.boundary = false;
     child.in_place = false;
@@ -144,7 +144,8 @@ std::unique_ptr<Executor> make_boundary_executor(const Request& r) {
     child.in_batch_stride = child.out_batch_stride = r.n;
     child.policy = CUBUTTERFLY_ALGORITHM_DEFAULT;
     child.explicit_algorithm.clear();
-    return std::make_unique<BoundaryExecutor>(r, plan_executor(child));
+    child.variant.clear();
+    return std::make_unique<BoundaryExecutor>(r, plan_executor(child, sel));
 }
 
 }  // namespace cbw

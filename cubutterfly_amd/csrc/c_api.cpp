@@ -355,16 +355,29 @@ cubutterflyStatus_t cubutterflyCreatePlan(cubutterflyHandle_t handle, cubutterfl
         auto created = std::make_unique<cubutterflyPlan>();
         created->descriptor = *descriptor;
         created->request = cbw::lower_request(*descriptor);
-        if (created->request.policy == CUBUTTERFLY_ALGORITHM_MEASURE)
-            log_event(handle, CUBUTTERFLY_LOG_INFO, "measure-static",
-                      "MEASURE uses the static gfx950 model for the butterfly path");
-        created->executor = cbw::plan_executor(created->request);
+        // Selection (reference src/c_api.cpp:4329-4420): EXPLICIT builds the
+        // named lowering, DEFAULT replays the selection cache where it holds a
+        // record, MEASURE times every candidate of each rank-1 plan and records
+        // the fastest.
+        cbw::Selection selection;
+        selection.policy = created->request.policy;
+        selection.cache_path = handle->cache_path;
+        selection.stream = handle->stream;
+        created->executor = cbw::plan_executor(created->request, &selection);
         if (created->request.policy == CUBUTTERFLY_ALGORITHM_EXPLICIT) {
             cbw::supported(created->executor->algorithm == created->request.explicit_algorithm,
                            "explicit algorithm '" + created->request.explicit_algorithm +
                                "' is not a lowering of this descriptor (available: " +
                                created->executor->algorithm + ")");
             created->source = CUBUTTERFLY_SELECTION_EXPLICIT;
+        } else {
+            created->source = selection.source;
+        }
+        if (!selection.notes.empty()) {
+            created->executor->reason += "; " + selection.notes;
+            log_event(handle, CUBUTTERFLY_LOG_INFO,
+                      created->request.policy == CUBUTTERFLY_ALGORITHM_MEASURE ? "measure-complete" : "cache-replay",
+                      selection.notes + "; algorithm=" + created->executor->algorithm);
         }
         created->input_bytes = created->request.span_bytes(true);
         created->output_bytes = created->request.span_bytes(false);

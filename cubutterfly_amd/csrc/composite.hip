@@ -145,7 +145,7 @@ struct Step {
 
 class CompositeExecutor final : public Executor {
   public:
-    CompositeExecutor(const Request& r, bool flatten) : r_(r) {
+    CompositeExecutor(const Request& r, bool flatten, Selection* sel) : r_(r) {
         const std::uint32_t rank = r.rank;
         std::vector<std::uint32_t> logs(rank);
         for (std::uint32_t a = 0; a < rank; ++a) logs[a] = log2_u64(r.extents[a]);
@@ -155,7 +155,7 @@ class CompositeExecutor final : public Executor {
         out_side_ = side(false, logs);
         std::vector<std::string> names;
         if (flatten) {
-            children_.push_back(plan_executor(axis_request(r.n, r.batch)));
+            children_.push_back(plan_executor(axis_request(r.n, r.batch), sel));
             steps_.push_back(Step{false, 0, 0, 0, 0, 0});
         } else {
             // Innermost axis first; each axis is first moved innermost.
@@ -178,7 +178,7 @@ class CompositeExecutor final : public Executor {
                 const std::uint32_t axis = rank - 1 - k;
                 move_innermost(axis);
                 const std::uint64_t e = r.extents[axis];
-                children_.push_back(plan_executor(axis_request(e, r.batch * (r.n / e))));
+                children_.push_back(plan_executor(axis_request(e, r.batch * (r.n / e)), sel));
                 Step s;
                 s.child = children_.size() - 1;
                 s.axis = axis;
@@ -282,6 +282,7 @@ class CompositeExecutor final : public Executor {
         c.in_batch_stride = c.out_batch_stride = n;
         c.policy = CUBUTTERFLY_ALGORITHM_DEFAULT;
         c.explicit_algorithm.clear();
+        c.variant.clear();
         return c;
     }
 
@@ -337,11 +338,11 @@ class CompositeExecutor final : public Executor {
 
 }  // namespace
 
-std::unique_ptr<Executor> make_composite_executor(const Request& r) {
+std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel) {
     require(r.rank >= 2 && r.rank <= kMaxRank && r.extents.size() == r.rank, "composite plans need rank 2 to 8");
     // A flattened FWHT is one rank-1 plan; it exists up to the resident length.
     const bool flatten = r.op == Op::Fwht && !(r.inverse && r.normalize) && r.log_n <= 13;
-    return std::make_unique<CompositeExecutor>(r, flatten);
+    return std::make_unique<CompositeExecutor>(r, flatten, sel);
 }
 
 }  // namespace cbw

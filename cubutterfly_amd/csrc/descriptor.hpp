@@ -72,6 +72,9 @@ struct Request {
     bool input_bit_reversed = false, output_bit_reversed = false;
     cubutterflyAlgorithmPolicy_t policy = CUBUTTERFLY_ALGORITHM_DEFAULT;
     std::string explicit_algorithm;
+    // Rank-1 lowering to build, by algorithm name (empty: the static model's
+    // choice). Set by the selection (explicit, cached or measured).
+    std::string variant;
     std::size_t element_bytes = 0;
     // Normalised element and batch strides of each side (packed: 1 and n).
     std::uint64_t in_stride = 1, out_stride = 1, in_batch_stride = 0, out_batch_stride = 0;

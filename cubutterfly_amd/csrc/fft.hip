@@ -23,6 +23,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -599,17 +600,49 @@ void register_all() {
     add_two<24>();
 }
 
-Launch find(const Key& k) {
+Launch lookup(const Key& k) {
     static std::once_flag once;
     std::call_once(once, register_all);
     auto it = registry().find(k);
-    if (it == registry().end()) throw NotSupported("FFT pass shape has no gfx950 kernel");
-    return it->second;
+    return it == registry().end() ? nullptr : it->second;
+}
+
+Launch find(const Key& k) {
+    const Launch fn = lookup(k);
+    if (fn == nullptr) throw NotSupported("FFT pass shape has no gfx950 kernel");
+    return fn;
+}
+
+// A two-pass split l1 + l2 = m whose column and row kernels both exist.
+bool split_available(int m, int l1, bool inverse) {
+    const int l2 = m - l1;
+    return l1 >= 1 && l2 >= 1 && l1 <= 14 && l2 <= 14 &&
+           lookup(Key{l1, col_lines(l1, l2), true, false, inverse}) != nullptr &&
+           lookup(Key{l2, row_lines(l1, l2), false, false, inverse}) != nullptr;
+}
+
+constexpr const char* kTwoPassName = "fft-c64-two-pass-r16";
+
+std::string two_pass_name(int m, int l1) {
+    if (l1 == split_l1(m)) return kTwoPassName;
+    return std::string(kTwoPassName) + "-" + std::to_string(l1) + "x" + std::to_string(m - l1);
+}
+
+// Column bits of a two-pass variant name, or -1 when the name is not one.
+int parse_split(int m, const std::string& name) {
+    if (name == kTwoPassName) return split_l1(m);
+    const std::string prefix = std::string(kTwoPassName) + "-";
+    if (name.compare(0, prefix.size(), prefix) != 0) return -1;
+    unsigned a = 0, b = 0;
+    char tail = 0;
+    if (std::sscanf(name.c_str() + prefix.size(), "%ux%u%c", &a, &b, &tail) != 2) return -1;
+    return int(a + b) == m && two_pass_name(m, int(a)) == name ? int(a) : -1;
 }
 
 class FftExecutor final : public Executor {
   public:
-    explicit FftExecutor(const Request& r) : r_(r) {
+    // split: column bits of a two-pass lowering (0: one pass).
+    FftExecutor(const Request& r, int split) : r_(r) {
         const std::uint32_t m = r.log_n;
         supported(m >= 1 && m <= 24, "complex FFT lengths above 2^24 are not yet lowered for gfx950");
         // Level twiddles: w^(4096 k) and w^k, w = exp(-+2 pi i / n), from double.
@@ -629,7 +662,7 @@ class FftExecutor final : public Executor {
         base.twa = twa_.as<float2>();
         base.twb = twb_.as<float2>();
         base.scale = scale;
-        if (m <= 14) {
+        if (split == 0) {
             const int li = single_li(int(m));
             const std::uint64_t tiles = (r.batch + (1ull << li) - 1) >> li;
             Step s{find(Key{int(m), li, false, true, r.inverse}), base, false, false};
@@ -640,7 +673,7 @@ class FftExecutor final : public Executor {
             steps_.push_back(s);
             algorithm = m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16";
         } else {
-            const std::uint32_t l1 = std::uint32_t(split_l1(int(m))), l2 = m - l1;
+            const std::uint32_t l1 = std::uint32_t(split), l2 = m - l1;
             const int col_li = col_lines(int(l1), int(l2));
             const int row_li = row_lines(int(l1), int(l2));
             const std::uint64_t col_tiles = r.batch << (l2 - col_li);
@@ -659,7 +692,7 @@ class FftExecutor final : public Executor {
             b.args.tiles = unsigned(row_tiles);
             steps_ = {a, b};
             workspace_ = static_cast<std::size_t>(r.batch << m) * sizeof(float2);
-            algorithm = "fft-c64-two-pass-r16";
+            algorithm = two_pass_name(int(m), int(l1));
         }
         reason = "decimation in frequency: in-register radix-16 codelets (radix-32 for one-pass 2^13 and 2^14), "
                  "level twiddles from two 4096-entry tables, LDS-staged bit-reversal (and grid transpose) on the "
@@ -673,6 +706,7 @@ class FftExecutor final : public Executor {
             .field("batch", r.batch)
             .field("direction", r.inverse ? "inverse" : "forward")
             .field("passes", unsigned(steps_.size()))
+            .field("column_bits", unsigned(split))
             .field("workspace_bytes", std::uint64_t(workspace_))
             .end_object();
         mapping_json = w.str();
@@ -703,6 +737,29 @@ class FftExecutor final : public Executor {
 
 }  // namespace
 
-std::unique_ptr<Executor> make_fft_executor(const Request& r) { return std::make_unique<FftExecutor>(r); }
+std::unique_ptr<Executor> make_fft_executor(const Request& r) {
+    const int m = int(r.log_n);
+    supported(m >= 1 && m <= 24, "complex FFT lengths above 2^24 are not yet lowered for gfx950");
+    if (m <= 14) {
+        supported(r.variant.empty() || r.variant == (m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16"),
+                  "'" + r.variant + "' is not a lowering of this FFT");
+        return std::make_unique<FftExecutor>(r, 0);
+    }
+    const int split = r.variant.empty() ? split_l1(m) : parse_split(m, r.variant);
+    supported(split > 0 && split_available(m, split, r.inverse),
+              "'" + r.variant + "' is not a lowering of this FFT");
+    return std::make_unique<FftExecutor>(r, split);
+}
+
+// One-pass lengths have one lowering; two-pass lengths add the neighbouring
+// column / row splits whose kernels exist.
+std::vector<std::string> fft_candidates(const Request& r) {
+    const int m = int(r.log_n);
+    if (m <= 14) return {m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16"};
+    std::vector<std::string> names{two_pass_name(m, split_l1(m))};
+    for (int l1 : {split_l1(m) - 1, split_l1(m) + 1, split_l1(m) - 2, split_l1(m) + 2})
+        if (split_available(m, l1, r.inverse)) names.push_back(two_pass_name(m, l1));
+    return names;
+}
 
 }  // namespace cbw

@@ -401,7 +401,16 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
     supported(!r.allow_mma || r.fp16_final, "MFMA Hadamard blocks require FP16 storage");
     const Launch launch = r.fp16_final ? resident_launcher<F16Io>(r.log_n) : resident_launcher<F32Io>(r.log_n);
     require(launch != nullptr, "FWHT length has no launcher");
-    return std::make_unique<FwhtExecutor>(r, launch);
+    auto e = std::make_unique<FwhtExecutor>(r, launch);
+    supported(r.variant.empty() || r.variant == e->algorithm,
+              "'" + r.variant + "' is not a lowering of this FWHT (available: " + e->algorithm + ")");
+    return e;
+}
+
+std::vector<std::string> fwht_candidates(const Request& r) {
+    Request v = r;
+    v.variant.clear();
+    return {make_fwht_executor(v)->algorithm};
 }
 
 }  // namespace cbw

@@ -122,7 +122,7 @@ struct EngineImplT {
         const unsigned bits = sizeof(W) * 8;
         std::uint64_t max_q = 0;
         for (const auto& d : c.domains) max_q = std::max(max_q, d.modulus);
-        lazy = max_q < (std::uint64_t{1} << (bits - 2));
+        lazy = !c.force_strict && max_q < (std::uint64_t{1} << (bits - 2));
         const std::uint64_t polys = c.polynomials.empty() ? c.batch : c.polynomials.size();
         require(polys >= 1 && polys <= 0xffffffffull, "NTT batch must be in [1, 2^32)");
         const bool offsets = !c.polynomials.empty();
@@ -293,7 +293,7 @@ NttEngine::NttEngine(const NttEngineConfig& c) : impl_(new Impl) {
         impl_->u64 = std::make_unique<EngineImplT<std::uint64_t>>(c);
     const bool two = passes() == 2;
     algorithm_ = std::string("ntt-u") + std::to_string(c.word_bits) + (c.negacyclic ? "-negacyclic" : "-cyclic") +
-                 (two ? "-two-pass-r16" : "-resident-r16");
+                 (two ? "-two-pass-r16" : "-resident-r16") + (c.force_strict ? "-strict" : "");
     json::Writer w;
     w.begin_object()
         .field("schema_version", 1u)
@@ -335,6 +335,12 @@ void NttEngine::execute(const void* in, void* out, void* ws, hipStream_t stream)
 
 namespace {
 
+// Name of the static model's lowering: resident up to 2^12, then two passes.
+std::string default_name(const Request& r) {
+    return "ntt-u" + std::to_string(r.word_bits) + (r.negacyclic ? "-negacyclic" : "-cyclic") +
+           (r.log_n <= 12 ? "-resident-r16" : "-two-pass-r16");
+}
+
 class NttExecutor final : public Executor {
   public:
     explicit NttExecutor(const Request& r) {
@@ -362,6 +368,10 @@ class NttExecutor final : public Executor {
             }
         }
         c.domains.push_back({r.modulus, root});
+        c.force_strict = !r.variant.empty() && r.variant == default_name(r) + "-strict";
+        supported(r.variant.empty() || c.force_strict || r.variant == default_name(r),
+                  "'" + r.variant + "' is not a lowering of this NTT (available: " + default_name(r) + ", " +
+                      default_name(r) + "-strict)");
         engine_ = std::make_unique<NttEngine>(c);
         algorithm = engine_->algorithm();
         mapping_json = engine_->mapping_json();
@@ -382,5 +392,13 @@ class NttExecutor final : public Executor {
 }  // namespace
 
 std::unique_ptr<Executor> make_ntt_executor(const Request& r) { return std::make_unique<NttExecutor>(r); }
+
+// Lazy reduction (values in [0, 2q) / [0, 4q) between stages) where the
+// modulus leaves two spare bits, and the fully reduced butterflies.
+std::vector<std::string> ntt_candidates(const Request& r) {
+    std::vector<std::string> names{default_name(r)};
+    if (r.modulus < (std::uint64_t{1} << (r.word_bits - 2))) names.push_back(default_name(r) + "-strict");
+    return names;
+}
 
 }  // namespace cbw

@@ -43,6 +43,7 @@ struct NttEngineConfig {
     bool input_bit_reversed = false;
     bool output_bit_reversed = false;
     bool reduce_input = true;  // reduce arbitrary words mod q on load
+    bool force_strict = false; // fully reduced butterflies even where lazy ones fit
     std::vector<NttDomain> domains;
     std::vector<NttPolynomial> polynomials;  // empty: `batch` dense rows of domain 0
     std::uint64_t batch = 0;

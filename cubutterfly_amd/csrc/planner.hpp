@@ -9,24 +9,46 @@
 
 namespace cbw {
 
+// Rank-1 kernel families. Each factory builds `r.variant` (one of its
+// candidates' names) or, when that is empty, the static model's choice, and
+// throws NotSupported for a name that is not a lowering of the request.
 std::unique_ptr<Executor> make_fwht_executor(const Request& r);
 std::unique_ptr<Executor> make_fft_executor(const Request& r);
 std::unique_ptr<Executor> make_ntt_executor(const Request& r);
+// Candidate lowerings of a rank-1 request, the static model's choice first.
+std::vector<std::string> fwht_candidates(const Request& r);
+std::vector<std::string> fft_candidates(const Request& r);
+std::vector<std::string> ntt_candidates(const Request& r);
+
+// Plan-time selection state (reference src/c_api.cpp:1756-1901): the policy,
+// the user selection cache and the stream MEASURE times on; `source` and
+// `notes` accumulate over every rank-1 plan the request lowers to.
+struct Selection {
+    cubutterflyAlgorithmPolicy_t policy = CUBUTTERFLY_ALGORITHM_DEFAULT;
+    std::string cache_path;
+    hipStream_t stream = nullptr;
+    cubutterflySelectionSource_t source = CUBUTTERFLY_SELECTION_STATIC_MODEL;
+    std::string notes;
+};
+void combine_source(Selection& sel, cubutterflySelectionSource_t next);
+std::string selection_key(const Request& r);
+std::string lookup_cache(const std::string& path, const std::string& key);
+void store_cache(const std::string& path, const std::string& key, const std::string& algorithm);
+std::unique_ptr<Executor> build_leaf(const Request& r);
+// A packed rank-1 plan: explicit variant, cached record (DEFAULT), measured
+// candidates (MEASURE) or the static model.
+std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel);
+
 // Gather / packed child / scatter, for strided sides and FWHT / FFT orders.
-std::unique_ptr<Executor> make_boundary_executor(const Request& r);
+std::unique_ptr<Executor> make_boundary_executor(const Request& r, Selection* sel);
 // Rank >= 2: one batched rank-1 plan per axis, innermost first, with tiled
 // transposes bringing each axis innermost and the original order back.
-std::unique_ptr<Executor> make_composite_executor(const Request& r);
+std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel);
 
-inline std::unique_ptr<Executor> plan_executor(const Request& r) {
-    if (r.rank > 1) return make_composite_executor(r);
-    if (r.boundary) return make_boundary_executor(r);
-    switch (r.op) {
-        case Op::Fwht: return make_fwht_executor(r);
-        case Op::Fft: return make_fft_executor(r);
-        case Op::Ntt: return make_ntt_executor(r);
-    }
-    throw NotSupported("operator has no MI355X lowering");
+inline std::unique_ptr<Executor> plan_executor(const Request& r, Selection* sel = nullptr) {
+    if (r.rank > 1) return make_composite_executor(r, sel);
+    if (r.boundary) return make_boundary_executor(r, sel);
+    return select_leaf(r, sel);
 }
 
 }  // namespace cbw

@@ -1,0 +1,254 @@
+// Plan-time selection of rank-1 lowerings: the static gfx950 model, replay
+// from the user selection cache, or on-device measurement of every candidate
+// (reference src/c_api.cpp:722-764 for the cache, 1420-1885 for the searches).
+//
+// The cache is a text file of `key<TAB>algorithm` records, appended under an
+// exclusive flock and read under a shared one; the last record for a key
+// wins and an unterminated final line (a writer that died mid-record) is
+// ignored. Keys name the device (architecture, CU count), this library's
+// selection version and every field of the rank-1 request that changes the
+// kernels run, so a record is replayed only for the same work on the same
+// kind of device.
+#include "planner.hpp"
+
+#include <fcntl.h>
+#include <sys/file.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <fstream>
+#include <limits>
+
+#include "json.hpp"
+
+namespace cbw {
+namespace {
+
+class CacheLock {
+  public:
+    CacheLock(const std::string& path, bool write)
+        : fd_(::open(path.c_str(), write ? (O_RDWR | O_CREAT) : O_RDONLY, 0600)) {
+        if (fd_ < 0) {
+            if (write) throw std::runtime_error("cannot open the selection cache " + path);
+            return;  // no file yet: nothing to replay
+        }
+        if (::flock(fd_, write ? LOCK_EX : LOCK_SH) != 0) {
+            ::close(fd_);
+            fd_ = -1;
+            throw std::runtime_error("cannot lock the selection cache " + path);
+        }
+    }
+    ~CacheLock() {
+        if (fd_ >= 0) {
+            ::flock(fd_, LOCK_UN);
+            ::close(fd_);
+        }
+    }
+    CacheLock(const CacheLock&) = delete;
+    CacheLock& operator=(const CacheLock&) = delete;
+
+  private:
+    int fd_;
+};
+
+std::string device_identity() {
+    int device = 0;
+    hipDeviceProp_t prop{};
+    if (hipGetDevice(&device) != hipSuccess || hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        (void)hipGetLastError();
+        return "no-device";
+    }
+    return std::string(prop.gcnArchName) + "|cu" + std::to_string(prop.multiProcessorCount);
+}
+
+// Priority of the reference's combined_source (src/c_api.cpp:1887-1901).
+int rank_of(cubutterflySelectionSource_t s) {
+    switch (s) {
+        case CUBUTTERFLY_SELECTION_UNMEASURED_FALLBACK: return 5;
+        case CUBUTTERFLY_SELECTION_RUNTIME_MEASURED: return 4;
+        case CUBUTTERFLY_SELECTION_USER_CACHE: return 3;
+        case CUBUTTERFLY_SELECTION_EXPLICIT: return 2;
+        case CUBUTTERFLY_SELECTION_MEASURED_TABLE: return 1;
+        default: return 0;
+    }
+}
+
+void note(Selection& sel, const std::string& text) {
+    if (!sel.notes.empty()) sel.notes += "; ";
+    sel.notes += text;
+}
+
+struct DeviceScratch {
+    void* ptr = nullptr;
+    explicit DeviceScratch(std::size_t bytes) {
+        if (bytes && hipMalloc(&ptr, bytes) != hipSuccess) {
+            ptr = nullptr;
+            (void)hipGetLastError();
+            throw std::bad_alloc();
+        }
+    }
+    ~DeviceScratch() {
+        if (ptr) (void)hipFree(ptr);
+    }
+    DeviceScratch(const DeviceScratch&) = delete;
+    DeviceScratch& operator=(const DeviceScratch&) = delete;
+};
+
+struct Event {
+    hipEvent_t e = nullptr;
+    Event() { hip_check(hipEventCreate(&e), "MEASURE event"); }
+    ~Event() {
+        if (e) (void)hipEventDestroy(e);
+    }
+    Event(const Event&) = delete;
+    Event& operator=(const Event&) = delete;
+};
+
+// Mean milliseconds of one execution: 3 untimed runs, then 20 between two
+// events on the selection stream (the reference's host-event-loop protocol,
+// warmup 3 / repeat 20).
+double time_executor(Executor& e, const void* in, void* out, void* ws, hipStream_t stream) {
+    constexpr int kWarmup = 3, kRepeat = 20;
+    for (int i = 0; i < kWarmup; ++i) e.execute(in, out, ws, stream);
+    Event start, stop;
+    hip_check(hipEventRecord(start.e, stream), "MEASURE event record");
+    for (int i = 0; i < kRepeat; ++i) e.execute(in, out, ws, stream);
+    hip_check(hipEventRecord(stop.e, stream), "MEASURE event record");
+    hip_check(hipEventSynchronize(stop.e), "MEASURE synchronize");
+    float ms = 0.0f;
+    hip_check(hipEventElapsedTime(&ms, start.e, stop.e), "MEASURE elapsed time");
+    return double(ms) / kRepeat;
+}
+
+}  // namespace
+
+void combine_source(Selection& sel, cubutterflySelectionSource_t next) {
+    if (rank_of(next) > rank_of(sel.source)) sel.source = next;
+}
+
+std::string lookup_cache(const std::string& path, const std::string& key) {
+    if (path.empty()) return {};
+    CacheLock lock(path, false);
+    std::ifstream input(path);
+    std::string line, match;
+    while (std::getline(input, line)) {
+        if (input.eof()) break;  // unterminated final record
+        const auto tab = line.find('\t');
+        if (tab == key.size() && line.compare(0, tab, key) == 0) match = line.substr(tab + 1);
+    }
+    return match;
+}
+
+void store_cache(const std::string& path, const std::string& key, const std::string& algorithm) {
+    if (path.empty()) return;
+    require(key.find('\n') == std::string::npos && algorithm.find_first_of("\t\n") == std::string::npos,
+            "selection cache records are single lines");
+    CacheLock lock(path, true);
+    std::ofstream output(path, std::ios::app);
+    if (!output) throw std::runtime_error("cannot open the selection cache " + path + " for writing");
+    output << key << '\t' << algorithm << '\n';
+    output.flush();
+    if (!output) throw std::runtime_error("cannot persist the selection cache record");
+}
+
+std::string selection_key(const Request& r) {
+    json::Writer w;
+    w.begin_object()
+        .field("op", int(r.op))
+        .field("storage", int(r.storage))
+        .field("log_n", r.log_n)
+        .field("batch", r.batch)
+        .field("inverse", r.inverse)
+        .field("normalize", r.normalize)
+        .field("in_place", r.in_place)
+        .field("fp16_final", r.fp16_final)
+        .field("allow_mma", r.allow_mma)
+        .field("output_scale", double(r.output_scale))
+        .field("modulus", r.modulus)
+        .field("word_bits", r.word_bits)
+        .field("negacyclic", r.negacyclic)
+        .field("psi", r.psi)
+        .field("input_bit_reversed", r.input_bit_reversed)
+        .field("output_bit_reversed", r.output_bit_reversed)
+        .end_object();
+    return "cubutterfly-gfx950-selection-v1|" + device_identity() + "|" + w.str();
+}
+
+std::unique_ptr<Executor> build_leaf(const Request& r) {
+    switch (r.op) {
+        case Op::Fwht: return make_fwht_executor(r);
+        case Op::Fft: return make_fft_executor(r);
+        case Op::Ntt: return make_ntt_executor(r);
+    }
+    throw NotSupported("operator has no MI355X lowering");
+}
+
+std::vector<std::string> leaf_candidates(const Request& r) {
+    switch (r.op) {
+        case Op::Fwht: return fwht_candidates(r);
+        case Op::Fft: return fft_candidates(r);
+        case Op::Ntt: return ntt_candidates(r);
+    }
+    return {};
+}
+
+std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
+    if (sel == nullptr || sel->policy == CUBUTTERFLY_ALGORITHM_EXPLICIT) {
+        if (r.policy != CUBUTTERFLY_ALGORITHM_EXPLICIT) return build_leaf(r);
+        Request v = r;
+        v.variant = r.explicit_algorithm;
+        return build_leaf(v);
+    }
+    const std::string key = selection_key(r);
+    if (sel->policy == CUBUTTERFLY_ALGORITHM_DEFAULT) {
+        const std::string cached = lookup_cache(sel->cache_path, key);
+        if (!cached.empty()) {
+            Request v = r;
+            v.variant = cached;
+            try {
+                auto e = build_leaf(v);
+                combine_source(*sel, CUBUTTERFLY_SELECTION_USER_CACHE);
+                note(*sel, "replayed '" + cached + "' from the selection cache");
+                return e;
+            } catch (const NotSupported&) {
+                note(*sel, "ignored cache record '" + cached + "' (not a lowering of this request)");
+            }
+        }
+        return build_leaf(r);
+    }
+    // MEASURE: every candidate on the device, on shared scratch buffers.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    hip_check(hipStreamIsCapturing(sel->stream, &capture), "MEASURE capture query");
+    supported(capture == hipStreamCaptureStatusNone, "MEASURE cannot time candidates during stream capture");
+    std::vector<std::unique_ptr<Executor>> built;
+    std::size_t ws_bytes = 0;
+    for (const auto& name : leaf_candidates(r)) {
+        Request v = r;
+        v.variant = name;
+        built.push_back(build_leaf(v));
+        ws_bytes = std::max(ws_bytes, built.back()->workspace_bytes());
+    }
+    require(!built.empty(), "no candidate lowering to measure");
+    const std::size_t bytes = r.data_bytes();
+    DeviceScratch in(bytes), out(bytes), ws(ws_bytes);
+    hip_check(hipMemsetAsync(in.ptr, 0, bytes, sel->stream), "MEASURE input fill");
+    std::size_t best = 0;
+    double best_ms = std::numeric_limits<double>::infinity();
+    std::string results;
+    for (std::size_t i = 0; i < built.size(); ++i) {
+        const double ms = time_executor(*built[i], in.ptr, r.in_place ? in.ptr : out.ptr, ws.ptr, sel->stream);
+        char text[64];
+        std::snprintf(text, sizeof text, "=%.4f ms", ms);
+        results += (i ? ", " : "") + built[i]->algorithm + text;
+        if (ms < best_ms) {
+            best_ms = ms;
+            best = i;
+        }
+    }
+    store_cache(sel->cache_path, key, built[best]->algorithm);
+    combine_source(*sel, CUBUTTERFLY_SELECTION_RUNTIME_MEASURED);
+    note(*sel, "measured " + results);
+    return std::move(built[best]);
+}
+
+}  // namespace cbw
