@@ -111,10 +111,10 @@ class FwhtFp32(Workload):
 
 class FwhtFp32Pitched(FwhtFp32):
     """C1's transform on pitched rows (row stride n + 64 on both sides): the
-    semantic-boundary plan (gather, packed transform, scatter)."""
+    FWHT kernel reads and writes the pitched rows directly."""
     name = "c1p"
     description = ("FWHT fp32 unnormalized forward, batch 4096 x n=4096, rows pitched at n + 64 on both sides "
-                   "(semantic boundary), integer inputs in [-8,8]")
+                   "(pitched-row FWHT kernel), integer inputs in [-8,8]")
     PAD = 64
 
     def setup(self, torch, lib, stream):
@@ -127,8 +127,9 @@ class FwhtFp32Pitched(FwhtFp32):
                          output_strides=[1], output_batch_stride=pitch)
         plan = cb.Plan(lib, t, stream=stream)
         ws = plan.workspace_size()
-        self.workspace = torch.empty(ws, dtype=torch.uint8, device="cuda")
-        plan.set_workspace(self.workspace, ws)
+        if ws:
+            self.workspace = torch.empty(ws, dtype=torch.uint8, device="cuda")
+            plan.set_workspace(self.workspace, ws)
         self.plans = [plan]
         self.host = workloads.fwht_integer_input(self.log_n, self.batch, seed=1)
         padded = np.zeros((self.batch, pitch), dtype=np.float32)
@@ -149,7 +150,8 @@ class FwhtFp32Pitched(FwhtFp32):
         return bool(np.array_equal(got, oracle.fwht_f32(self.host, threads=oracle.default_threads())))
 
     def kernel_name(self):
-        return "fwht_resident_kernel (inside " + self.plans[0].algorithm_name() + ")"
+        name = self.plans[0].algorithm_name()
+        return ("fwht_pitched_kernel" if name.endswith("-pitched") else "fwht_resident_kernel (inside " + name + ")")
 
 
 class NttNegacyclic(Workload):

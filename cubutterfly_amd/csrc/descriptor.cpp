@@ -276,7 +276,21 @@ Request lower_request(const cubutterflyDescriptor& d) {
         return stride == 1 && (d.batch == 1 || batch_stride == n);
     };
     const bool strided = !packed(r.in_stride, r.in_batch_stride) || !packed(r.out_stride, r.out_batch_stride);
-    r.boundary = d.rank == 1 &&
+    // FWHT rows with a pitch: unit element stride, natural order, n >= 16 and
+    // 16-byte pitches (a thread's 16-element vectors stay in one row and stay
+    // aligned), a tile's row span below 2^31 bytes (32-bit lane offsets), and
+    // no in-place pitch change (a tile's output would overlap rows that other
+    // workgroups have yet to read).
+    const auto pitch_ok = [&](std::uint64_t pitch) {
+        const std::uint64_t rows_per_tile = n >= 4096 ? 1 : 4096 / n;
+        return (pitch * r.element_bytes) % 16 == 0 &&
+               ((rows_per_tile - 1) * pitch + n) * r.element_bytes < (std::uint64_t{1} << 31);
+    };
+    r.pitched = d.rank == 1 && strided && d.op == CUBUTTERFLY_OPERATOR_FWHT && r.in_stride == 1 &&
+                r.out_stride == 1 && !r.input_bit_reversed && !r.output_bit_reversed && n >= 16 &&
+                pitch_ok(r.in_batch_stride) && pitch_ok(r.out_batch_stride) &&
+                (!r.in_place || r.in_batch_stride == r.out_batch_stride);
+    r.boundary = d.rank == 1 && !r.pitched &&
                  (strided || (d.op != CUBUTTERFLY_OPERATOR_NTT && (r.input_bit_reversed || r.output_bit_reversed)));
     switch (d.op) {
         case CUBUTTERFLY_OPERATOR_FWHT:

@@ -210,11 +210,50 @@ __device__ __forceinline__ void load_full(const typename Io::T* __restrict__ inp
 // product and narrowing into one mixed-precision FMA with a single rounding.
 __device__ __forceinline__ void opaque(float& x) { asm volatile("" : "+v"(x)); }
 
-// The butterflies of one tile and its store (`full`: the tile lies inside
-// `total`).
-template <int LOG_N, int LB, class Io>
-__device__ __forceinline__ void transform_store(float (&v)[kE], float* lds, unsigned t, typename Io::T* output,
-                                                std::uint64_t base, std::uint64_t total, bool full, float norm,
+// Where transform_store puts tile element i: packed rows (element base + i,
+// `full`: the tile lies inside `total`) ...
+template <class Io>
+struct PackedOut {
+    typename Io::T* output;
+    std::uint64_t base, total;
+    bool full;
+    __device__ __forceinline__ void one(unsigned i, float y) const {
+        const std::uint64_t k = base + i;
+        if (full || k < total) Io::store1(output + k, y);
+    }
+    __device__ __forceinline__ void sixteen(unsigned t, const float (&x)[kE]) const {
+        if (full) {
+            Io::store16(output + base + t * kE, x);
+            return;
+        }
+#pragma unroll
+        for (int r = 0; r < kE; ++r) {
+            const std::uint64_t k = base + t * kE + r;
+            if (k < total) Io::store1(output + k, x[r]);
+        }
+    }
+};
+
+// ... or pitched rows: element (row, column) of the tile at row * pitch +
+// column from the tile's first row, rows past `rows` absent.
+template <int LOG_N, class Io>
+struct PitchedOut {
+    typename Io::T* output;
+    std::uint64_t pitch;
+    unsigned rows;
+    __device__ __forceinline__ void one(unsigned i, float y) const {
+        const unsigned row = i >> LOG_N;
+        if (row < rows) Io::store1(output + row * pitch + (i & ((1u << LOG_N) - 1u)), y);
+    }
+    __device__ __forceinline__ void sixteen(unsigned t, const float (&x)[kE]) const {
+        const unsigned i = t * kE, row = i >> LOG_N;
+        if (row < rows) Io::store16(output + row * pitch + (i & ((1u << LOG_N) - 1u)), x);
+    }
+};
+
+// The butterflies of one tile and its store through `out`.
+template <int LOG_N, int LB, class Io, class Out>
+__device__ __forceinline__ void transform_store(float (&v)[kE], float* lds, unsigned t, const Out& out, float norm,
                                                 float scale) {
     constexpr int kPhases = (LOG_N + kLE - 1) / kLE;
     constexpr int kLast = kPhases - 1;
@@ -239,10 +278,9 @@ __device__ __forceinline__ void transform_store(float (&v)[kE], float* lds, unsi
     if constexpr (kDirectStore) {
 #pragma unroll
         for (int r = 0; r < kE; ++r) {
-            const std::uint64_t i = base + phase_index<kLast, LB>(t, r);
             float y = (v[r] * norm) * scale;
             opaque(y);
-            if (full || i < total) Io::store1(output + i, y);
+            out.one(phase_index<kLast, LB>(t, r), y);
         }
     } else {
         if constexpr (kPhases > 1) exchange<kLast, 0, LB>(v, lds, t);
@@ -252,15 +290,7 @@ __device__ __forceinline__ void transform_store(float (&v)[kE], float* lds, unsi
             x[r] = (v[r] * norm) * scale;
             opaque(x[r]);
         }
-        if (full) {
-            Io::store16(output + base + t * kE, x);
-        } else {
-#pragma unroll
-            for (int r = 0; r < kE; ++r) {
-                const std::uint64_t i = base + t * kE + r;
-                if (i < total) Io::store1(output + i, x[r]);
-            }
-        }
+        out.sixteen(t, x);
     }
 }
 
@@ -286,7 +316,8 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_resident_kernel(const ty
         const bool more = following < full_tiles;
         load_full<LB, Io>(input, following, more, t, nxt);
         __builtin_amdgcn_sched_barrier(0);  // the prefetch is issued before any use of `cur`
-        transform_store<LOG_N, LB, Io>(cur, lds, t, output, std::uint64_t(tile) << LB, total, true, norm, scale);
+        transform_store<LOG_N, LB, Io>(cur, lds, t, PackedOut<Io>{output, std::uint64_t(tile) << LB, total, true},
+                                       norm, scale);
         // Keep `cur`'s registers allocated through the stores, so no store
         // takes its data from them: the prefetch into them two steps on would
         // otherwise first wait for those stores.
@@ -308,7 +339,70 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_resident_kernel(const ty
         const std::uint64_t base = std::uint64_t(full_tiles) << LB;
         float v[kE];
         load_partial<LB, Io>(input, base, total, t, v);
-        transform_store<LOG_N, LB, Io>(v, lds, t, output, base, total, false, norm, scale);
+        transform_store<LOG_N, LB, Io>(v, lds, t, PackedOut<Io>{output, base, total, false}, norm, scale);
+    }
+}
+
+// Pitched rows: row k of the input at input + k * in_pitch, of the output at
+// output + k * out_pitch (elements; both 16-byte multiples, n >= 16, so a
+// thread's 16 consecutive elements stay in one row and load as 16-byte
+// vectors). Tiles are 2^(LB - LOG_N) rows, walked as in the packed kernel;
+// each tile's loads go through a buffer ending after its last row, so the
+// last, partial tile reads zeros for its missing rows and skips their stores.
+template <int LOG_N, int LB, class Io>
+__global__ __launch_bounds__(1 << (LB - kLE)) void fwht_pitched_kernel(const typename Io::T* __restrict__ input,
+                                                                       typename Io::T* output, std::uint64_t rows,
+                                                                       std::uint64_t in_pitch,
+                                                                       std::uint64_t out_pitch, float norm,
+                                                                       float scale, unsigned tiles) {
+    static_assert(LOG_N >= kLE, "a thread's 16 elements lie in one row");
+    using T = typename Io::T;
+    constexpr unsigned kBlock = 1u << LB;
+    constexpr unsigned kRows = 1u << (LB - LOG_N);
+    constexpr unsigned kMask = (1u << LOG_N) - 1u;
+    __shared__ float lds[kBlock + (kBlock >> kLE)];
+    const unsigned t = threadIdx.x;
+    const unsigned grid = gridDim.x;
+    const unsigned full_tiles = static_cast<unsigned>(rows / kRows);
+    const auto span = [&](std::uint64_t n_rows) {
+        return static_cast<std::uint32_t>(((n_rows - 1) * in_pitch + (kMask + 1)) * sizeof(T));
+    };
+    const std::uint32_t in_off =
+        static_cast<std::uint32_t>((((t * kE) >> LOG_N) * in_pitch + ((t * kE) & kMask)) * sizeof(T));
+    const std::uint32_t full_span = span(kRows);
+    const auto load = [&](unsigned tile, std::uint32_t bytes, float (&v)[kE]) {
+        Io::load16(make_rsrc(input + std::uint64_t(tile) * kRows * in_pitch, bytes), in_off, v);
+    };
+    unsigned tile = blockIdx.x;
+    auto step = [&](float (&cur)[kE], float (&nxt)[kE]) -> bool {
+        const unsigned following = tile + grid;
+        const bool more = following < full_tiles;
+        load(following, more ? full_span : 0u, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        transform_store<LOG_N, LB, Io>(
+            cur, lds, t, PitchedOut<LOG_N, Io>{output + std::uint64_t(tile) * kRows * out_pitch, out_pitch, kRows},
+            norm, scale);
+#pragma unroll
+        for (int r = 0; r < kE; ++r) opaque(cur[r]);
+        tile = following;
+        return more;
+    };
+    if (tile < full_tiles) {
+        float a[kE], b[kE];
+        load(tile, full_span, a);
+        for (;;) {
+            if (!step(a, b)) break;
+            if (!step(b, a)) break;
+        }
+    }
+    if (full_tiles < tiles && full_tiles % grid == blockIdx.x) {
+        const unsigned present = static_cast<unsigned>(rows - std::uint64_t(full_tiles) * kRows);
+        float v[kE];
+        load(full_tiles, span(present), v);
+        transform_store<LOG_N, LB, Io>(
+            v, lds, t,
+            PitchedOut<LOG_N, Io>{output + std::uint64_t(full_tiles) * kRows * out_pitch, out_pitch, present}, norm,
+            scale);
     }
 }
 
@@ -329,6 +423,26 @@ void launch_resident(const void* in, void* out, std::uint64_t total, float norm,
                        scale, static_cast<unsigned>(tiles));
 }
 
+using PitchedLaunch = void (*)(const void*, void*, std::uint64_t, std::uint64_t, std::uint64_t, float, float,
+                               unsigned, hipStream_t);
+
+template <int LOG_N, class Io>
+void launch_pitched(const void* in, void* out, std::uint64_t rows, std::uint64_t in_pitch, std::uint64_t out_pitch,
+                    float norm, float scale, unsigned grid, hipStream_t stream) {
+    constexpr int LB = block_log<LOG_N, Io>();
+    constexpr std::uint64_t kRows = std::uint64_t{1} << (LB - LOG_N);
+    const std::uint64_t tiles = (rows + kRows - 1) / kRows;
+    hipLaunchKernelGGL((fwht_pitched_kernel<LOG_N, LB, Io>), dim3(grid), dim3(1u << (LB - kLE)), 0, stream,
+                       static_cast<const typename Io::T*>(in), static_cast<typename Io::T*>(out), rows, in_pitch,
+                       out_pitch, norm, scale, static_cast<unsigned>(tiles));
+}
+
+template <class Io, int... L>
+PitchedLaunch pitched_table_entry(int log_n, std::integer_sequence<int, L...>) {
+    PitchedLaunch table[] = {launch_pitched<L + kLE, Io>...};
+    return table[log_n - kLE];
+}
+
 template <class Io, int... L>
 Launch resident_table_entry(int log_n, std::integer_sequence<int, L...>) {
     Launch table[] = {nullptr, launch_resident<L + 1, Io>...};
@@ -343,14 +457,23 @@ Launch resident_launcher(int log_n) {
     return resident_table_entry<Io>(log_n, std::make_integer_sequence<int, kMaxResidentLog>{});
 }
 
+template <class Io>
+PitchedLaunch pitched_launcher(int log_n) {
+    if (log_n < kLE || log_n > kMaxResidentLog) return nullptr;
+    return pitched_table_entry<Io>(log_n, std::make_integer_sequence<int, kMaxResidentLog - kLE + 1>{});
+}
+
 class FwhtExecutor final : public Executor {
   public:
-    FwhtExecutor(const Request& r, Launch launch) : r_(r), launch_(launch) {
+    FwhtExecutor(const Request& r, Launch launch, PitchedLaunch pitched)
+        : r_(r), launch_(launch), pitched_(pitched) {
         norm_ = r.normalize ? 1.0f / static_cast<float>(r.n) : 1.0f;
         scale_ = r.fp16_final ? r.output_scale : 1.0f;
         const int lb = r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
         const std::uint64_t total = r.n * r.batch;
-        const std::uint64_t tiles = (total + (1ull << lb) - 1) >> lb;
+        const std::uint64_t rows_per_tile = std::uint64_t{1} << (lb - int(r.log_n));
+        const std::uint64_t tiles =
+            pitched_ ? (r.batch + rows_per_tile - 1) / rows_per_tile : (total + (1ull << lb) - 1) >> lb;
         require(tiles <= 0xffffffffull, "FWHT batch exceeds the tile index range");
         // Grid: one workgroup per tile (measured at least as fast as a
         // persistent, occupancy-sized grid for every BASELINE shape once the
@@ -359,7 +482,8 @@ class FwhtExecutor final : public Executor {
         const unsigned threads = 1u << (lb - kLE);
         const std::uint64_t lds = ((1u << lb) + ((1u << lb) >> kLE)) * 4ull;
         grid_ = static_cast<unsigned>(std::min<std::uint64_t>(tiles, 0x7fffffffull));
-        algorithm = r.fp16_final ? "fwht-fp16-fp32-resident-r16" : "fwht-fp32-resident-r16";
+        algorithm = std::string(r.fp16_final ? "fwht-fp16-fp32-resident-r16" : "fwht-fp32-resident-r16") +
+                    (pitched_ ? "-pitched" : "");
         reason = "whole rows resident in one workgroup (" + std::to_string(threads) +
                  " threads x 16 registers, padded LDS exchange)" +
                  std::string(grid_ < tiles ? ", persistent grid with next-tile prefetch" : "") +
@@ -378,17 +502,23 @@ class FwhtExecutor final : public Executor {
             .field("registers_per_thread", unsigned(kE))
             .field("phases", unsigned((r.log_n + kLE - 1) / kLE))
             .field("lds_bytes", lds)
+            .field("input_pitch", pitched_ ? r.in_batch_stride : r.n)
+            .field("output_pitch", pitched_ ? r.out_batch_stride : r.n)
             .end_object();
         mapping_json = w.str();
     }
     void execute(const void* in, void* out, void*, hipStream_t stream) override {
-        launch_(in, out, r_.n * r_.batch, norm_, scale_, grid_, stream);
+        if (pitched_)
+            pitched_(in, out, r_.batch, r_.in_batch_stride, r_.out_batch_stride, norm_, scale_, grid_, stream);
+        else
+            launch_(in, out, r_.n * r_.batch, norm_, scale_, grid_, stream);
         hip_check(hipGetLastError(), "FWHT launch");
     }
 
   private:
     Request r_;
     Launch launch_;
+    PitchedLaunch pitched_;
     float norm_ = 1.0f, scale_ = 1.0f;
     unsigned grid_ = 1;
 };
@@ -401,7 +531,12 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
     supported(!r.allow_mma || r.fp16_final, "MFMA Hadamard blocks require FP16 storage");
     const Launch launch = r.fp16_final ? resident_launcher<F16Io>(r.log_n) : resident_launcher<F32Io>(r.log_n);
     require(launch != nullptr, "FWHT length has no launcher");
-    auto e = std::make_unique<FwhtExecutor>(r, launch);
+    PitchedLaunch pitched = nullptr;
+    if (r.pitched) {
+        pitched = r.fp16_final ? pitched_launcher<F16Io>(r.log_n) : pitched_launcher<F32Io>(r.log_n);
+        require(pitched != nullptr, "pitched FWHT rows need n >= 16");
+    }
+    auto e = std::make_unique<FwhtExecutor>(r, launch, pitched);
     supported(r.variant.empty() || r.variant == e->algorithm,
               "'" + r.variant + "' is not a lowering of this FWHT (available: " + e->algorithm + ")");
     return e;
