@@ -276,7 +276,8 @@ Request lower_request(const cubutterflyDescriptor& d) {
         return stride == 1 && (d.batch == 1 || batch_stride == n);
     };
     const bool strided = !packed(r.in_stride, r.in_batch_stride) || !packed(r.out_stride, r.out_batch_stride);
-    // FWHT rows with a pitch: unit element stride, natural order, n >= 16 and
+    // Rows with a pitch load and store in the transform kernels themselves.
+    // FWHT: unit element stride, natural order, n >= 16 and
     // 16-byte pitches (a thread's 16-element vectors stay in one row and stay
     // aligned), a tile's row span below 2^31 bytes (32-bit lane offsets), and
     // no in-place pitch change (a tile's output would overlap rows that other
@@ -286,10 +287,18 @@ Request lower_request(const cubutterflyDescriptor& d) {
         return (pitch * r.element_bytes) % 16 == 0 &&
                ((rows_per_tile - 1) * pitch + n) * r.element_bytes < (std::uint64_t{1} << 31);
     };
-    r.pitched = d.rank == 1 && strided && d.op == CUBUTTERFLY_OPERATOR_FWHT && r.in_stride == 1 &&
-                r.out_stride == 1 && !r.input_bit_reversed && !r.output_bit_reversed && n >= 16 &&
-                pitch_ok(r.in_batch_stride) && pitch_ok(r.out_batch_stride) &&
-                (!r.in_place || r.in_batch_stride == r.out_batch_stride);
+    // NTT and FFT rows with a pitch, n >= 2^12: one transform per tile, each
+    // at its own offset (NTT: the RNS engine's per-polynomial offsets; FFT:
+    // a per-side transform pitch).
+    const bool rows_pitched = d.rank == 1 && strided && r.in_stride == 1 && r.out_stride == 1 &&
+                              (!r.in_place || r.in_batch_stride == r.out_batch_stride);
+    if (d.op == CUBUTTERFLY_OPERATOR_FWHT)
+        r.pitched = rows_pitched && !r.input_bit_reversed && !r.output_bit_reversed && n >= 16 &&
+                    pitch_ok(r.in_batch_stride) && pitch_ok(r.out_batch_stride);
+    else if (d.op == CUBUTTERFLY_OPERATOR_NTT)
+        r.pitched = rows_pitched && n >= 4096;
+    else if (d.op == CUBUTTERFLY_OPERATOR_FFT)  // one transform per tile from 2^12 points
+        r.pitched = rows_pitched && !r.input_bit_reversed && !r.output_bit_reversed && n >= 4096;
     r.boundary = d.rank == 1 && !r.pitched &&
                  (strided || (d.op != CUBUTTERFLY_OPERATOR_NTT && (r.input_bit_reversed || r.output_bit_reversed)));
     switch (d.op) {

@@ -81,8 +81,9 @@ struct Request {
     // The sides are strided, or carry FWHT / FFT logical orders: the plan
     // gathers, runs the packed natural-order transform and scatters.
     bool boundary = false;
-    // FWHT rows with a pitch (unit element stride, natural order) that the
-    // FWHT kernels load and store directly, in place of a boundary plan.
+    // Rows with a pitch (unit element stride; in/out_batch_stride apart)
+    // that the transform kernels load and store directly, in place of a
+    // boundary plan.
     bool pitched = false;
     // Rank >= 2: per-axis extents, element strides and bit-reversed orders of
     // each side (outermost axis first). Empty for rank 1.

@@ -43,6 +43,9 @@ struct FftArgs {
     std::uint32_t l1, l2;  // high / low index bits (l1 = 0: one pass)
     std::uint32_t rows, tiles;
     float scale;  // 1/n for the normalised inverse on the final store, else 1
+    // Elements between consecutive transforms of the input / output buffer:
+    // n when packed, a caller's row pitch otherwise (one transform per tile).
+    std::uint64_t in_pitch, out_pitch;
 };
 
 __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
@@ -288,7 +291,7 @@ struct FftPass {
     struct Tile {
         std::uint32_t row0;  // ROW: first global row (= transform for one pass)
         std::uint32_t c0;    // COL: first column
-        std::uint64_t base;  // COL: element offset of the tile's transform
+        std::uint64_t base;  // COL: the tile's transform
     };
 
     static __device__ __forceinline__ Tile decode(const FftArgs& a, std::uint32_t tile, std::uint32_t m) {
@@ -296,19 +299,20 @@ struct FftPass {
         if constexpr (COL) {
             const std::uint32_t shift = a.l2 - LI;
             tl.c0 = (tile & ((1u << shift) - 1u)) << LI;
-            tl.base = std::uint64_t(tile >> shift) << m;
+            tl.base = tile >> shift;
         } else {
             tl.row0 = tile << LI;
         }
         return tl;
     }
 
-    // Uniform base of the tile's span and the 32-bit element offset of tile
-    // element i on the natural (load) side.
-    static __device__ __forceinline__ std::uint64_t span_base(const FftArgs& a, const Tile& tl, std::uint32_t m) {
-        if constexpr (COL) return tl.base;
-        else if constexpr (SINGLE) return std::uint64_t(tl.row0) << LT;
-        else return std::uint64_t((tl.row0 >> LI) >> (a.l1 - LI)) << m;  // the transform of the tile's rows
+    // Uniform base of the tile's span in a buffer whose transforms lie
+    // `pitch` elements apart, and the 32-bit element offset of tile element i
+    // on the natural (load) side.
+    static __device__ __forceinline__ std::uint64_t span_base(const FftArgs& a, const Tile& tl, std::uint64_t pitch) {
+        if constexpr (COL) return tl.base * pitch;
+        else if constexpr (SINGLE) return std::uint64_t(tl.row0) * pitch;
+        else return std::uint64_t((tl.row0 >> LI) >> (a.l1 - LI)) * pitch;  // the transform of the tile's rows
     }
     static __device__ __forceinline__ std::uint32_t natural_offset(const FftArgs& a, const Tile& tl, std::uint32_t i) {
         if constexpr (COL) {
@@ -353,7 +357,8 @@ struct FftPass {
     static __device__ __forceinline__ void load(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
                                                 float2 (&v)[kE], bool valid = true) {
         constexpr int w0 = tile_window<0>();
-        const __amdgpu_buffer_rsrc_t src = make_rsrc(a.in + span_base(a, tl, m), valid ? span_bytes(a, tl, m) : 0u);
+        const __amdgpu_buffer_rsrc_t src =
+            make_rsrc(a.in + span_base(a, tl, a.in_pitch), valid ? span_bytes(a, tl, m) : 0u);
         const std::uint32_t tb = natural_offset(a, tl, index<w0>(t, 0)) * 8u;
 #pragma unroll
         for (int r = 0; r < kE; ++r) v[r] = load_at(src, tb, natural_offset(a, Tile{}, index<w0>(0, r)) * 8u);
@@ -385,7 +390,7 @@ struct FftPass {
             digit<3>(v, level_base<3>(a, t, tl.c0, m));
         }
         constexpr int wl = tile_window<kPhases - 1>();
-        const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.out + span_base(a, tl, m), span_bytes(a, tl, m));
+        const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.out + span_base(a, tl, a.out_pitch), span_bytes(a, tl, m));
         if constexpr (COL) {  // intermediate: same positions
             const std::uint32_t tb = natural_offset(a, tl, index<wl>(t, 0)) * 8u;
 #pragma unroll
@@ -662,6 +667,8 @@ class FftExecutor final : public Executor {
         base.twa = twa_.as<float2>();
         base.twb = twb_.as<float2>();
         base.scale = scale;
+        const std::uint64_t in_pitch = r.pitched ? r.in_batch_stride : r.n;
+        const std::uint64_t out_pitch = r.pitched ? r.out_batch_stride : r.n;
         if (split == 0) {
             const int li = single_li(int(m));
             const std::uint64_t tiles = (r.batch + (1ull << li) - 1) >> li;
@@ -670,6 +677,8 @@ class FftExecutor final : public Executor {
             s.args.l2 = m;
             s.args.rows = unsigned(r.batch);
             s.args.tiles = unsigned(tiles);
+            s.args.in_pitch = in_pitch;
+            s.args.out_pitch = out_pitch;
             steps_.push_back(s);
             algorithm = m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16";
         } else {
@@ -685,15 +694,20 @@ class FftExecutor final : public Executor {
             a.args.rows = unsigned(r.batch << l1);
             a.args.tiles = unsigned(col_tiles);
             a.args.scale = 1.0f;
+            a.args.in_pitch = in_pitch;
+            a.args.out_pitch = r.n;  // the workspace is packed
             Step b{find(Key{int(l2), row_li, false, false, r.inverse}), base, true, false};
             b.args.l1 = l1;
             b.args.l2 = l2;
             b.args.rows = unsigned(r.batch << l1);
             b.args.tiles = unsigned(row_tiles);
+            b.args.in_pitch = r.n;
+            b.args.out_pitch = out_pitch;
             steps_ = {a, b};
             workspace_ = static_cast<std::size_t>(r.batch << m) * sizeof(float2);
             algorithm = two_pass_name(int(m), int(l1));
         }
+        if (r.pitched) algorithm += "-pitched";
         reason = "decimation in frequency: in-register radix-16 codelets (radix-32 for one-pass 2^13 and 2^14), "
                  "level twiddles from two 4096-entry tables, LDS-staged bit-reversal (and grid transpose) on the "
                  "final store";
@@ -740,12 +754,22 @@ class FftExecutor final : public Executor {
 std::unique_ptr<Executor> make_fft_executor(const Request& r) {
     const int m = int(r.log_n);
     supported(m >= 1 && m <= 24, "complex FFT lengths above 2^24 are not yet lowered for gfx950");
+    require(!r.pitched || single_li(m) == 0, "pitched FFT rows need n >= 2^12 (one transform per tile)");
+    // Pitched plans carry the suffix on every candidate name.
+    std::string variant = r.variant;
+    const std::string suffix = r.pitched ? "-pitched" : "";
+    if (!variant.empty() && r.pitched) {
+        supported(variant.size() > suffix.size() &&
+                      variant.compare(variant.size() - suffix.size(), suffix.size(), suffix) == 0,
+                  "'" + r.variant + "' is not a lowering of this FFT");
+        variant.resize(variant.size() - suffix.size());
+    }
     if (m <= 14) {
-        supported(r.variant.empty() || r.variant == (m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16"),
+        supported(variant.empty() || variant == (m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16"),
                   "'" + r.variant + "' is not a lowering of this FFT");
         return std::make_unique<FftExecutor>(r, 0);
     }
-    const int split = r.variant.empty() ? split_l1(m) : parse_split(m, r.variant);
+    const int split = variant.empty() ? split_l1(m) : parse_split(m, variant);
     supported(split > 0 && split_available(m, split, r.inverse),
               "'" + r.variant + "' is not a lowering of this FFT");
     return std::make_unique<FftExecutor>(r, split);
@@ -755,10 +779,11 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r) {
 // column / row splits whose kernels exist.
 std::vector<std::string> fft_candidates(const Request& r) {
     const int m = int(r.log_n);
-    if (m <= 14) return {m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16"};
-    std::vector<std::string> names{two_pass_name(m, split_l1(m))};
+    const std::string suffix = r.pitched ? "-pitched" : "";
+    if (m <= 14) return {std::string(m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16") + suffix};
+    std::vector<std::string> names{two_pass_name(m, split_l1(m)) + suffix};
     for (int l1 : {split_l1(m) - 1, split_l1(m) + 1, split_l1(m) - 2, split_l1(m) + 2})
-        if (split_available(m, l1, r.inverse)) names.push_back(two_pass_name(m, l1));
+        if (split_available(m, l1, r.inverse)) names.push_back(two_pass_name(m, l1) + suffix);
     return names;
 }
 

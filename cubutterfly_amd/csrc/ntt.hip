@@ -368,12 +368,19 @@ class NttExecutor final : public Executor {
             }
         }
         c.domains.push_back({r.modulus, root});
-        c.force_strict = !r.variant.empty() && r.variant == default_name(r) + "-strict";
-        supported(r.variant.empty() || c.force_strict || r.variant == default_name(r),
-                  "'" + r.variant + "' is not a lowering of this NTT (available: " + default_name(r) + ", " +
-                      default_name(r) + "-strict)");
+        if (r.pitched) {  // rows a pitch apart: one polynomial per tile at its own offset
+            require(r.batch <= 0xffffffffull, "NTT batch must be below 2^32");
+            c.polynomials.reserve(r.batch);
+            for (std::uint64_t b = 0; b < r.batch; ++b)
+                c.polynomials.push_back({0u, b * r.in_batch_stride, b * r.out_batch_stride});
+        }
+        const std::string suffix = r.pitched ? "-pitched" : "";
+        c.force_strict = !r.variant.empty() && r.variant == default_name(r) + "-strict" + suffix;
+        supported(r.variant.empty() || c.force_strict || r.variant == default_name(r) + suffix,
+                  "'" + r.variant + "' is not a lowering of this NTT (available: " + default_name(r) + suffix +
+                      ", " + default_name(r) + "-strict" + suffix + ")");
         engine_ = std::make_unique<NttEngine>(c);
-        algorithm = engine_->algorithm();
+        algorithm = engine_->algorithm() + (r.pitched ? "-pitched" : "");
         mapping_json = engine_->mapping_json();
         reason = engine_->passes() == 1
                      ? "whole polynomials resident in one workgroup (radix-16 register windows, LDS exchange)"
@@ -396,8 +403,9 @@ std::unique_ptr<Executor> make_ntt_executor(const Request& r) { return std::make
 // Lazy reduction (values in [0, 2q) / [0, 4q) between stages) where the
 // modulus leaves two spare bits, and the fully reduced butterflies.
 std::vector<std::string> ntt_candidates(const Request& r) {
-    std::vector<std::string> names{default_name(r)};
-    if (r.modulus < (std::uint64_t{1} << (r.word_bits - 2))) names.push_back(default_name(r) + "-strict");
+    const std::string suffix = r.pitched ? "-pitched" : "";
+    std::vector<std::string> names{default_name(r) + suffix};
+    if (r.modulus < (std::uint64_t{1} << (r.word_bits - 2))) names.push_back(default_name(r) + "-strict" + suffix);
     return names;
 }
 
