@@ -644,23 +644,71 @@ int parse_split(int m, const std::string& name) {
     return int(a + b) == m && two_pass_name(m, int(a)) == name ? int(a) : -1;
 }
 
+// Three-pass lowering a + b + c = m (top, middle, low index bits): a column
+// pass over the top a bits (2^(b + c) columns), the column pass of the
+// batched 2^(b + c)-point transforms over the middle b bits (its level
+// twiddles are those of the full transform: a DIF digit's twiddle depends
+// only on the bits below it), and the row pass of a (a + b) x c split. Every
+// pass moves segments of 2^min(14 - bits, ...) elements (512 bytes at
+// 8 + 8 + 8), where the two-pass 12 + 12 split moves 32-byte segments.
+bool split3_available(int m, int a, int b, bool inverse) {
+    const int c = m - a - b;
+    return a >= 1 && b >= 1 && c >= 1 && a <= 14 && b <= 14 && c <= 14 &&
+           lookup(Key{a, col_lines(a, b + c), true, false, inverse}) != nullptr &&
+           lookup(Key{b, col_lines(b, c), true, false, inverse}) != nullptr &&
+           lookup(Key{c, row_lines(a + b, c), false, false, inverse}) != nullptr;
+}
+
+std::string three_pass_name(int m, int a, int b) {
+    return "fft-c64-three-pass-r16-" + std::to_string(a) + "x" + std::to_string(b) + "x" + std::to_string(m - a - b);
+}
+
+// Top and middle bits of a three-pass name, or false.
+bool parse_split3(int m, const std::string& name, int& a, int& b) {
+    const std::string prefix = "fft-c64-three-pass-r16-";
+    if (name.compare(0, prefix.size(), prefix) != 0) return false;
+    unsigned x = 0, y = 0, z = 0;
+    char tail = 0;
+    if (std::sscanf(name.c_str() + prefix.size(), "%ux%ux%u%c", &x, &y, &z, &tail) != 3) return false;
+    a = int(x);
+    b = int(y);
+    return int(x + y + z) == m && three_pass_name(m, a, b) == name;
+}
+
+// The static model's three-pass choice: from 2^23 points, where the
+// two-pass split's segments drop to 32 or 64 bytes (measured on MI355X:
+// 2^24 x 1 in 171 us against 199 us, 2^23 x 2 in 164 us against 188 us),
+// a = m / 3 top bits and half the rest in the middle.
+bool default_three_pass(int m, bool inverse, int& a, int& b) {
+    if (m < 23) return false;
+    a = m / 3;
+    b = (m - a) / 2;
+    return split3_available(m, a, b, inverse);
+}
+
+// Level-twiddle tables of a 2^log_len-point transform: A[k] = w^(4096 k),
+// B[k] = w^k, w = exp(-+2 pi i / 2^log_len), from double.
+void upload_twiddles(DeviceBuffer& a, DeviceBuffer& b, int log_len, bool inverse) {
+    std::vector<float2> ta(4096), tb(4096);
+    const double sign = inverse ? 1.0 : -1.0;
+    const double n = std::ldexp(1.0, log_len);
+    for (int k = 0; k < 4096; ++k) {
+        const double fa = std::fmod(4096.0 * k, n), fb = std::fmod(double(k), n);
+        ta[k] = make_float2(float(std::cos(2 * M_PI * fa / n)), float(sign * std::sin(2 * M_PI * fa / n)));
+        tb[k] = make_float2(float(std::cos(2 * M_PI * fb / n)), float(sign * std::sin(2 * M_PI * fb / n)));
+    }
+    a.upload(ta);
+    b.upload(tb);
+}
+
 class FftExecutor final : public Executor {
   public:
-    // split: column bits of a two-pass lowering (0: one pass).
-    FftExecutor(const Request& r, int split) : r_(r) {
+    // split: column bits of a two-pass lowering (0: one pass); mid > 0: the
+    // middle bits of a three-pass lowering with `split` top bits.
+    FftExecutor(const Request& r, int split, int mid = 0) : r_(r) {
         const std::uint32_t m = r.log_n;
         supported(m >= 1 && m <= 24, "complex FFT lengths above 2^24 are not yet lowered for gfx950");
-        // Level twiddles: w^(4096 k) and w^k, w = exp(-+2 pi i / n), from double.
-        std::vector<float2> ta(4096), tb(4096);
-        const double sign = r.inverse ? 1.0 : -1.0;
-        const double n = std::ldexp(1.0, int(m));
-        for (int k = 0; k < 4096; ++k) {
-            const double fa = std::fmod(4096.0 * k, n), fb = std::fmod(double(k), n);
-            ta[k] = make_float2(float(std::cos(2 * M_PI * fa / n)), float(sign * std::sin(2 * M_PI * fa / n)));
-            tb[k] = make_float2(float(std::cos(2 * M_PI * fb / n)), float(sign * std::sin(2 * M_PI * fb / n)));
-        }
-        twa_.upload(ta);
-        twb_.upload(tb);
+        upload_twiddles(twa_, twb_, int(m), r.inverse);
         const float scale = r.normalize ? 1.0f / float(r.n) : 1.0f;
         require(r.batch <= 0xffffffffull, "FFT batch exceeds 2^32 transforms");
         FftArgs base{};
@@ -669,7 +717,47 @@ class FftExecutor final : public Executor {
         base.scale = scale;
         const std::uint64_t in_pitch = r.pitched ? r.in_batch_stride : r.n;
         const std::uint64_t out_pitch = r.pitched ? r.out_batch_stride : r.n;
-        if (split == 0) {
+        if (mid > 0) {
+            const std::uint32_t ta = std::uint32_t(split), tm = std::uint32_t(mid), tl = m - ta - tm;
+            upload_twiddles(sub_twa_, sub_twb_, int(tm + tl), r.inverse);
+            const int a_li = col_lines(int(ta), int(tm + tl));
+            const int b_li = col_lines(int(tm), int(tl));
+            const int c_li = row_lines(int(ta + tm), int(tl));
+            const std::uint64_t a_tiles = r.batch << (tm + tl - a_li);
+            const std::uint64_t b_tiles = (r.batch << ta) << (tl - b_li);
+            const std::uint64_t c_tiles = r.batch << (ta + tm - c_li);
+            require(a_tiles <= 0xffffffffull && b_tiles <= 0xffffffffull && c_tiles <= 0xffffffffull,
+                    "FFT batch exceeds the grid");
+            Step sa{find(Key{int(ta), a_li, true, false, r.inverse}), base, false, true};
+            sa.args.l1 = ta;
+            sa.args.l2 = tm + tl;
+            sa.args.rows = unsigned(r.batch << ta);
+            sa.args.tiles = unsigned(a_tiles);
+            sa.args.scale = 1.0f;
+            sa.args.in_pitch = in_pitch;
+            sa.args.out_pitch = r.n;
+            // The middle pass sees 2^top batched transforms of 2^(mid + low)
+            // points, in place in the workspace, with their own tables.
+            Step sb{find(Key{int(tm), b_li, true, false, r.inverse}), base, true, true};
+            sb.args.twa = sub_twa_.as<float2>();
+            sb.args.twb = sub_twb_.as<float2>();
+            sb.args.l1 = tm;
+            sb.args.l2 = tl;
+            sb.args.rows = unsigned((r.batch << ta) << tm);
+            sb.args.tiles = unsigned(b_tiles);
+            sb.args.scale = 1.0f;
+            sb.args.in_pitch = sb.args.out_pitch = std::uint64_t{1} << (tm + tl);
+            Step sc{find(Key{int(tl), c_li, false, false, r.inverse}), base, true, false};
+            sc.args.l1 = ta + tm;
+            sc.args.l2 = tl;
+            sc.args.rows = unsigned(r.batch << (ta + tm));
+            sc.args.tiles = unsigned(c_tiles);
+            sc.args.in_pitch = r.n;
+            sc.args.out_pitch = out_pitch;
+            steps_ = {sa, sb, sc};
+            workspace_ = static_cast<std::size_t>(r.batch << m) * sizeof(float2);
+            algorithm = three_pass_name(int(m), split, mid);
+        } else if (split == 0) {
             const int li = single_li(int(m));
             const std::uint64_t tiles = (r.batch + (1ull << li) - 1) >> li;
             Step s{find(Key{int(m), li, false, true, r.inverse}), base, false, false};
@@ -721,6 +809,7 @@ class FftExecutor final : public Executor {
             .field("direction", r.inverse ? "inverse" : "forward")
             .field("passes", unsigned(steps_.size()))
             .field("column_bits", unsigned(split))
+            .field("middle_bits", unsigned(mid))
             .field("workspace_bytes", std::uint64_t(workspace_))
             .end_object();
         mapping_json = w.str();
@@ -744,7 +833,7 @@ class FftExecutor final : public Executor {
         bool reads_ws, writes_ws;
     };
     Request r_;
-    DeviceBuffer twa_, twb_;
+    DeviceBuffer twa_, twb_, sub_twa_, sub_twb_;
     std::vector<Step> steps_;
     std::size_t workspace_ = 0;
 };
@@ -769,6 +858,12 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r) {
                   "'" + r.variant + "' is not a lowering of this FFT");
         return std::make_unique<FftExecutor>(r, 0);
     }
+    int top = 0, mid = 0;
+    if (variant.empty() && default_three_pass(m, r.inverse, top, mid)) return std::make_unique<FftExecutor>(r, top, mid);
+    if (parse_split3(m, variant, top, mid)) {
+        supported(split3_available(m, top, mid, r.inverse), "'" + r.variant + "' is not a lowering of this FFT");
+        return std::make_unique<FftExecutor>(r, top, mid);
+    }
     const int split = variant.empty() ? split_l1(m) : parse_split(m, variant);
     supported(split > 0 && split_available(m, split, r.inverse),
               "'" + r.variant + "' is not a lowering of this FFT");
@@ -781,9 +876,20 @@ std::vector<std::string> fft_candidates(const Request& r) {
     const int m = int(r.log_n);
     const std::string suffix = r.pitched ? "-pitched" : "";
     if (m <= 14) return {std::string(m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16") + suffix};
-    std::vector<std::string> names{two_pass_name(m, split_l1(m)) + suffix};
+    std::vector<std::string> names;
+    int top = 0, mid = 0;
+    const bool three = default_three_pass(m, r.inverse, top, mid);
+    if (three) names.push_back(three_pass_name(m, top, mid) + suffix);
+    names.push_back(two_pass_name(m, split_l1(m)) + suffix);
     for (int l1 : {split_l1(m) - 1, split_l1(m) + 1, split_l1(m) - 2, split_l1(m) + 2})
         if (split_available(m, l1, r.inverse)) names.push_back(two_pass_name(m, l1) + suffix);
+    // Three passes from 2^18: splits within one bit of m / 3 per pass.
+    if (m >= 18)
+        for (int a = m / 3 - 1; a <= m / 3 + 1; ++a)
+            for (int b = m / 3 - 1; b <= m / 3 + 1; ++b)
+                if (std::abs(m - a - b - m / 3) <= 1 && split3_available(m, a, b, r.inverse) &&
+                    !(three && a == top && b == mid))
+                    names.push_back(three_pass_name(m, a, b) + suffix);
     return names;
 }
 
