@@ -125,17 +125,40 @@ __device__ __forceinline__ void codelet(float2 (&v)[E]) {
     if constexpr (DS > 1) codelet<E, DS - 1, INV>(v);
 }
 
-// Padded LDS image (8-byte complex words), as in the NTT tiles.
-template <bool COL, int LT, int LI>
+constexpr int digit_bits_for(int lb, bool single);
+
+// LDS image of a tile (8-byte complex words).
+//
+// One-pass tiles of one whole row of 2^12 .. 2^14 points are unpadded, with
+// the low four word bits XORed with index bits [DB, DB + 4) and [LT - 4, LT)
+// (DB the digit width). A 16-lane group of a 64-bit LDS access covers all
+// banks when its 16 words differ in those four low bits, and every access of
+// these tiles varies across a group in exactly one of the three fields: the
+// lowest four index bits (phase exchanges with the register window above
+// them), the digit's lowest four bits (the exchange into the last digit), or
+// the top four bits (the bit-reversed read of the final store). The other
+// two fields are constant across the group, so the XOR is a bijection on it.
+// A plain 1-in-16 pad left the bit-reversed read with every lane of a group
+// on one bank.
+//
+// Other row tiles pad each row by 1/16 and 1 word; column tiles pad rows and
+// swizzle columns.
+template <bool COL, int LT, int LI, bool SINGLE>
 struct FftLds {
-    // The row layout is a sum of terms over disjoint index bit fields, so
-    // addr(a | b) = addr(a) + addr(b) for disjoint a, b; the column layout's
-    // swizzle is not.
-    static constexpr bool kLinear = !COL;
+    static constexpr int DB = digit_bits_for(LT + LI, SINGLE);
+    static constexpr bool kXor = SINGLE && LI == 0 && LT >= DB + 8;
+    // Row layouts are sums of terms over disjoint index bit fields, so
+    // addr(a | b) = addr(a) + addr(b) for disjoint a, b; the XOR layout is
+    // linear over bits, addr(a | b) = addr(a) ^ addr(b); the column layout's
+    // swizzle is neither.
+    static constexpr bool kLinear = !COL && !kXor;
     static constexpr std::uint32_t kWords =
-        COL ? (1u << LT) * ((1u << LI) + 1u) : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
+        kXor ? (1u << LT)
+             : COL ? (1u << LT) * ((1u << LI) + 1u) : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
     static __device__ __forceinline__ std::uint32_t addr(std::uint32_t i) {
-        if constexpr (COL) {
+        if constexpr (kXor) {
+            return i ^ (((i >> DB) ^ (i >> (LT - 4))) & 15u);
+        } else if constexpr (COL) {
             const std::uint32_t cc = i & ((1u << LI) - 1u), x = i >> LI;
             return x * ((1u << LI) + 1u) + (cc ^ ((x >> 3) & ((1u << LI) - 1u)));
         } else {
@@ -145,7 +168,8 @@ struct FftLds {
     }
     // addr(it | ir) for disjoint thread and register parts.
     static __device__ __forceinline__ std::uint32_t split(std::uint32_t it, std::uint32_t ir) {
-        if constexpr (kLinear) return addr(it) + addr(ir);
+        if constexpr (kXor) return addr(it) ^ addr(ir);
+        else if constexpr (kLinear) return addr(it) + addr(ir);
         else return addr(it | ir);
     }
 };
@@ -171,7 +195,7 @@ struct FftPass {
     // Prefetching needs registers for two tiles: with 16 values per thread
     // that fits the 128-register budget for passes of at most two digits.
     static constexpr bool kPrefetch = DB == 5 || kPhases <= 2;
-    using L = FftLds<COL, LT, LI>;
+    using L = FftLds<COL, LT, LI, SINGLE>;
 
     template <int P>
     static constexpr int window() {  // transform-relative register window start
@@ -532,7 +556,7 @@ struct Key {
 // multiple of 8 when larger. Other passes launch one workgroup per tile.
 template <int LT, int LI, bool COL, bool SINGLE, bool INV>
 void launch(const FftArgs& a, hipStream_t stream) {
-    constexpr std::uint32_t bytes = FftLds<COL, LT, LI>::kWords * sizeof(float2);
+    constexpr std::uint32_t bytes = FftLds<COL, LT, LI, SINGLE>::kWords * sizeof(float2);
     constexpr int threads = int(FftPass<LT, LI, COL, SINGLE, INV>::T);
     static const std::uint64_t resident = [] {
         const void* fn = reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, SINGLE, INV>);
