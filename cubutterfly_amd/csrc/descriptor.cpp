@@ -299,8 +299,12 @@ Request lower_request(const cubutterflyDescriptor& d) {
         r.pitched = rows_pitched && n >= 4096;
     else if (d.op == CUBUTTERFLY_OPERATOR_FFT)  // one transform per tile from 2^12 points
         r.pitched = rows_pitched && !r.input_bit_reversed && !r.output_bit_reversed && n >= 4096;
-    r.boundary = d.rank == 1 && !r.pitched &&
-                 (strided || (d.op != CUBUTTERFLY_OPERATOR_NTT && (r.input_bit_reversed || r.output_bit_reversed)));
+    // Logical orders: native to the NTT kernels, and to one-pass FFTs
+    // (n <= 2^14) on packed sides; FWHT orders and longer FFTs use the boundary.
+    const bool reversed = r.input_bit_reversed || r.output_bit_reversed;
+    const bool native_orders =
+        d.op == CUBUTTERFLY_OPERATOR_NTT || (d.op == CUBUTTERFLY_OPERATOR_FFT && n <= (std::size_t{1} << 14));
+    r.boundary = d.rank == 1 && !r.pitched && (strided || (reversed && !native_orders));
     switch (d.op) {
         case CUBUTTERFLY_OPERATOR_FWHT:
             r.op = Op::Fwht;

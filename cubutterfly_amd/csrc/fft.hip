@@ -185,7 +185,10 @@ constexpr int digit_bits_for(int lb, bool single) { return single && lb >= 13 ? 
 // One FFT pass over LT transform bits. COL: high bits, tile of 2^LI columns;
 // ROW: low bits, tile of 2^LI rows (the final pass, storing in natural order);
 // SINGLE: a one-pass transform, 2^LI whole rows per tile.
-template <int LT, int LI, bool COL, bool SINGLE, bool INV>
+// ORD (one-pass tiles only): bit 0 reads the input in bit-reversed logical
+// order, bit 1 writes the output in bit-reversed order (the DIF result's own
+// order, so the final store skips the reversal).
+template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD = 0>
 struct FftPass {
     static constexpr int LB = LT + LI;
     static constexpr int DB = digit_bits_for(LB, SINGLE);
@@ -341,8 +344,12 @@ struct FftPass {
     static __device__ __forceinline__ std::uint32_t natural_offset(const FftArgs& a, const Tile& tl, std::uint32_t i) {
         if constexpr (COL) {
             return tl.c0 + (i & ((1u << LI) - 1u)) + ((i >> LI) << a.l2);
-        } else if constexpr (SINGLE) {
-            return i;  // rows are consecutive transforms of 2^LT points
+        } else if constexpr (SINGLE) {  // rows are consecutive transforms of 2^LT points
+            if constexpr ((ORD & 1) != 0) {  // element x of a row sits at bitrev(x)
+                const std::uint32_t x = i & ((1u << LT) - 1u);
+                return (i - x) | brev(x, LT);
+            }
+            return i;
         } else {  // rows bitrev(k0 + rr) of one transform, matching the transposing store
             const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
             return (brev(k0 + (i >> LT), a.l1) << a.l2) + (i & ((1u << LT) - 1u));
@@ -444,7 +451,8 @@ struct FftPass {
                                                   std::uint32_t& off) {
         if constexpr (SINGLE) {  // rows are transforms: in-row bit reversal, lanes along the row
             const std::uint32_t xp = g & ((1u << LT) - 1u), rr = g >> LT;
-            i = brev(xp, LT) | (rr << LT);
+            // Bit-reversed output order is the DIF result's own order.
+            i = ((ORD & 2) != 0 ? xp : brev(xp, LT)) | (rr << LT);
             off = (rr << LT) + xp;
         } else {  // grid transpose: tile rows are bitrev(k0 + rr) of one transform
             const std::uint32_t rr = g & ((1u << LI) - 1u), cp = g >> LI;
@@ -535,10 +543,10 @@ struct FftPass {
     }
 };
 
-template <int LT, int LI, bool COL, bool SINGLE, bool INV>
+template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD>
 __global__ __launch_bounds__(1 << (LT + LI - digit_bits_for(LT + LI, SINGLE)))
 __attribute__((amdgpu_waves_per_eu(digit_bits_for(LT + LI, SINGLE) == 5 ? 2 : 4))) void fft_pass_kernel(FftArgs a) {
-    FftPass<LT, LI, COL, SINGLE, INV>::run(a);
+    FftPass<LT, LI, COL, SINGLE, INV, ORD>::run(a);
 }
 
 using Launch = void (*)(const FftArgs&, hipStream_t);
@@ -546,20 +554,21 @@ using Launch = void (*)(const FftArgs&, hipStream_t);
 struct Key {
     int lt, li;
     bool col, single, inv;
+    int ord = 0;
     bool operator<(const Key& o) const {
-        return std::tie(lt, li, col, single, inv) < std::tie(o.lt, o.li, o.col, o.single, o.inv);
+        return std::tie(lt, li, col, single, inv, ord) < std::tie(o.lt, o.li, o.col, o.single, o.inv, o.ord);
     }
 };
 
 // Prefetching passes run a persistent grid: as many workgroups as can be
 // resident (occupancy of this kernel with its LDS), at most one per tile, a
 // multiple of 8 when larger. Other passes launch one workgroup per tile.
-template <int LT, int LI, bool COL, bool SINGLE, bool INV>
+template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD>
 void launch(const FftArgs& a, hipStream_t stream) {
     constexpr std::uint32_t bytes = FftLds<COL, LT, LI, SINGLE>::kWords * sizeof(float2);
-    constexpr int threads = int(FftPass<LT, LI, COL, SINGLE, INV>::T);
+    constexpr int threads = int(FftPass<LT, LI, COL, SINGLE, INV, ORD>::T);
     static const std::uint64_t resident = [] {
-        const void* fn = reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, SINGLE, INV>);
+        const void* fn = reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, SINGLE, INV, ORD>);
         if (bytes > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, bytes) != hipSuccess || per_cu < 1)
@@ -567,11 +576,11 @@ void launch(const FftArgs& a, hipStream_t stream) {
         return std::uint64_t(per_cu) * std::uint64_t(device_cu_count());
     }();
     std::uint64_t grid = a.tiles;
-    if (FftPass<LT, LI, COL, SINGLE, INV>::kPrefetch) {
+    if (FftPass<LT, LI, COL, SINGLE, INV, ORD>::kPrefetch) {
         grid = std::min<std::uint64_t>(grid, resident);
         if (grid > 8) grid &= ~std::uint64_t{7};
     }
-    hipLaunchKernelGGL((fft_pass_kernel<LT, LI, COL, SINGLE, INV>), dim3(unsigned(grid)), dim3(threads), bytes, stream, a);
+    hipLaunchKernelGGL((fft_pass_kernel<LT, LI, COL, SINGLE, INV, ORD>), dim3(unsigned(grid)), dim3(threads), bytes, stream, a);
 }
 
 std::map<Key, Launch>& registry() {
@@ -581,8 +590,16 @@ std::map<Key, Launch>& registry() {
 
 template <int LT, int LI, bool COL, bool SINGLE>
 void add() {
-    registry()[Key{LT, LI, COL, SINGLE, false}] = &launch<LT, LI, COL, SINGLE, false>;
-    registry()[Key{LT, LI, COL, SINGLE, true}] = &launch<LT, LI, COL, SINGLE, true>;
+    registry()[Key{LT, LI, COL, SINGLE, false}] = &launch<LT, LI, COL, SINGLE, false, 0>;
+    registry()[Key{LT, LI, COL, SINGLE, true}] = &launch<LT, LI, COL, SINGLE, true, 0>;
+    if constexpr (SINGLE) {  // bit-reversed logical orders of one-pass tiles
+        registry()[Key{LT, LI, COL, SINGLE, false, 1}] = &launch<LT, LI, COL, SINGLE, false, 1>;
+        registry()[Key{LT, LI, COL, SINGLE, true, 1}] = &launch<LT, LI, COL, SINGLE, true, 1>;
+        registry()[Key{LT, LI, COL, SINGLE, false, 2}] = &launch<LT, LI, COL, SINGLE, false, 2>;
+        registry()[Key{LT, LI, COL, SINGLE, true, 2}] = &launch<LT, LI, COL, SINGLE, true, 2>;
+        registry()[Key{LT, LI, COL, SINGLE, false, 3}] = &launch<LT, LI, COL, SINGLE, false, 3>;
+        registry()[Key{LT, LI, COL, SINGLE, true, 3}] = &launch<LT, LI, COL, SINGLE, true, 3>;
+    }
 }
 
 // Shapes: one pass for m <= 14 (2^12-point tiles, 2^13 / 2^14 for m = 13,
@@ -725,6 +742,11 @@ void upload_twiddles(DeviceBuffer& a, DeviceBuffer& b, int log_len, bool inverse
     b.upload(tb);
 }
 
+// Name suffix of a one-pass plan with bit-reversed logical orders.
+std::string order_suffix(const Request& r) {
+    return std::string(r.input_bit_reversed ? "-bitrev-in" : "") + (r.output_bit_reversed ? "-bitrev-out" : "");
+}
+
 class FftExecutor final : public Executor {
   public:
     // split: column bits of a two-pass lowering (0: one pass); mid > 0: the
@@ -784,7 +806,8 @@ class FftExecutor final : public Executor {
         } else if (split == 0) {
             const int li = single_li(int(m));
             const std::uint64_t tiles = (r.batch + (1ull << li) - 1) >> li;
-            Step s{find(Key{int(m), li, false, true, r.inverse}), base, false, false};
+            const int ord = (r.input_bit_reversed ? 1 : 0) | (r.output_bit_reversed ? 2 : 0);
+            Step s{find(Key{int(m), li, false, true, r.inverse, ord}), base, false, false};
             s.args.l1 = 0;
             s.args.l2 = m;
             s.args.rows = unsigned(r.batch);
@@ -819,6 +842,7 @@ class FftExecutor final : public Executor {
             workspace_ = static_cast<std::size_t>(r.batch << m) * sizeof(float2);
             algorithm = two_pass_name(int(m), int(l1));
         }
+        algorithm += order_suffix(r);
         if (r.pitched) algorithm += "-pitched";
         reason = "decimation in frequency: in-register radix-16 codelets (radix-32 for one-pass 2^13 and 2^14), "
                  "level twiddles from two 4096-entry tables, LDS-staged bit-reversal (and grid transpose) on the "
@@ -868,10 +892,12 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r) {
     const int m = int(r.log_n);
     supported(m >= 1 && m <= 24, "complex FFT lengths above 2^24 are not yet lowered for gfx950");
     require(!r.pitched || single_li(m) == 0, "pitched FFT rows need n >= 2^12 (one transform per tile)");
-    // Pitched plans carry the suffix on every candidate name.
+    require(!(r.input_bit_reversed || r.output_bit_reversed) || m <= 14,
+            "bit-reversed FFT orders are native to one-pass lengths only");
+    // Order and pitch suffixes ride on every candidate name.
     std::string variant = r.variant;
-    const std::string suffix = r.pitched ? "-pitched" : "";
-    if (!variant.empty() && r.pitched) {
+    const std::string suffix = order_suffix(r) + (r.pitched ? "-pitched" : "");
+    if (!variant.empty() && !suffix.empty()) {
         supported(variant.size() > suffix.size() &&
                       variant.compare(variant.size() - suffix.size(), suffix.size(), suffix) == 0,
                   "'" + r.variant + "' is not a lowering of this FFT");
@@ -898,7 +924,7 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r) {
 // column / row splits whose kernels exist.
 std::vector<std::string> fft_candidates(const Request& r) {
     const int m = int(r.log_n);
-    const std::string suffix = r.pitched ? "-pitched" : "";
+    const std::string suffix = order_suffix(r) + (r.pitched ? "-pitched" : "");
     if (m <= 14) return {std::string(m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16") + suffix};
     std::vector<std::string> names;
     int top = 0, mid = 0;

@@ -54,7 +54,7 @@ def run(torch, lib, stream, t, x_flat, out_len, sentinel, in_place=False):
         assert plan.input_size() == x.numel() * x.element_size()
         assert plan.output_size() == y.numel() * y.element_size()
         name = plan.algorithm_name()
-        assert name.startswith("semantic-boundary[") or name.endswith("-pitched"), name
+        assert name.startswith("semantic-boundary[") or name.endswith("-pitched") or "-bitrev-" in name, name
         ws = plan.workspace_size()
         buf = torch.empty(ws, dtype=torch.uint8, device="cuda")
         plan.set_workspace(buf, ws)
@@ -167,9 +167,14 @@ def test_in_place_interleaved(torch_gpu, lib, stream):
 
 
 def test_fft_logical_order_plan(torch_gpu, lib):
+    # One-pass lengths take bit-reversed orders natively; longer ones through
+    # the boundary.
     t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
                      extents=[64], batch=2, output_orders=[cb.LogicalOrder.BIT_REVERSED],
                      input_orders=[cb.LogicalOrder.NATURAL])
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name() == "fft-c64-resident-r16-bitrev-out"
+    t.extents = [1 << 15]
     with cb.Plan(lib, t) as plan:
         assert plan.algorithm_name().startswith("semantic-boundary[fft-c64")
         assert json.loads(plan.mapping_json())["output_bit_reversed"] is True
