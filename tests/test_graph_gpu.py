@@ -1,0 +1,91 @@
+"""Plans captured into a HIP graph (torch.cuda.graph) and replayed several
+times, with eager work between replays, match their eager results on every
+replay: one-, two- and three-pass FFT, one- and two-pass NTT, FWHT (packed and
+pitched), a semantic-boundary plan and a rank-2 composition. Execution
+allocates nothing and records no memset, so capture is legal for every plan
+(reference execution semantics, docs/c_api.md:29-33)."""
+import numpy as np
+import pytest
+
+import cubutterfly_amd as cb
+from gpu_util import to_device, to_host
+
+pytestmark = pytest.mark.gpu
+
+Q30 = 1073479681
+
+
+def fft(n, batch, **kw):
+    return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
+                        extents=[n] if isinstance(n, int) else n, batch=batch, **kw)
+
+
+def ntt(n, batch, **kw):
+    return cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
+                        extents=[n], batch=batch, modulus=Q30, word_bits=32, ring=cb.NttRing.NEGACYCLIC, **kw)
+
+
+def fwht(n, batch, **kw):
+    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
+                        extents=[n], batch=batch, **kw)
+
+
+CASES = {
+    "fft-one-pass": (fft(1 << 12, 16), np.complex64, 1 << 16),
+    "fft-two-pass": (fft(1 << 16, 2), np.complex64, 1 << 17),
+    "fft-three-pass": (fft(1 << 23, 1), np.complex64, 1 << 23),
+    "ntt-one-pass": (ntt(1 << 10, 32), np.uint32, 1 << 15),
+    "ntt-two-pass": (ntt(1 << 16, 4, inverse=True), np.uint32, 1 << 18),
+    "fwht": (fwht(4096, 32), np.float32, 1 << 17),
+    "fwht-pitched": (fwht(1024, 8, input_strides=[1], input_batch_stride=1040, output_strides=[1],
+                          output_batch_stride=1040), np.float32, 7 * 1040 + 1024),
+    "boundary": (fft(256, 6, input_strides=[6], input_batch_stride=1), np.complex64, 6 * 256),
+    "rank2": (fft([64, 128], 2), np.complex64, 2 * 64 * 128),
+}
+
+
+def host_data(dtype, size, seed):
+    rng = np.random.default_rng(seed)
+    if np.dtype(dtype).kind == "c":
+        return (rng.standard_normal(size) + 1j * rng.standard_normal(size)).astype(dtype)
+    if np.dtype(dtype).kind == "u":
+        return rng.integers(0, Q30, size).astype(dtype)
+    return rng.standard_normal(size).astype(dtype)
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_replays_match_eager(torch_gpu, lib, case):
+    t, dtype, span = CASES[case]
+    torch = torch_gpu
+    stream = torch.cuda.Stream()
+    with cb.Plan(lib, t, stream=stream.cuda_stream) as plan:
+        out_span = plan.output_size() // np.dtype(dtype).itemsize
+        assert plan.input_size() == span * np.dtype(dtype).itemsize
+        ws_bytes = plan.workspace_size()
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+        if ws_bytes:
+            plan.set_workspace(ws, ws_bytes)
+        x = to_device(torch, host_data(dtype, span, 1))
+        y = to_device(torch, np.zeros(out_span, dtype))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            plan.execute(x, y)
+        torch.cuda.synchronize()
+        for replay in range(3):
+            data = host_data(dtype, span, 10 + replay)
+            x.copy_(to_device(torch, data))          # eager work between replays
+            y.zero_()
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                graph.replay()
+            torch.cuda.synchronize()
+            got = to_host(torch, y, dtype).copy()
+            # The same plan, eagerly, on the same input.
+            y.zero_()
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                plan.execute(x, y)
+            torch.cuda.synchronize()
+            eager = to_host(torch, y, dtype)
+            bits = {4: np.uint32, 8: np.uint64}[np.dtype(dtype).itemsize] if np.dtype(dtype).kind != "c" else np.uint64
+            np.testing.assert_array_equal(got.view(bits), eager.view(bits), err_msg=f"{case} replay {replay}")
