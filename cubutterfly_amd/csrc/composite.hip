@@ -22,6 +22,12 @@
 // rank-1 semantic boundary: an N-dimensional gather into packed natural
 // order first, an N-dimensional scatter last. A packed natural side is read
 // or written directly by the first or last step.
+//
+// The zero-extended embedding (any rank, reference src/c_api.cpp:5231-5245,
+// 5312-5325) runs the power-of-two transform of each axis's next power of
+// two: the forward input side (logical extents) is gathered with zeros in
+// the padding, the inverse output side keeps the first logical-extent
+// elements of each axis.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -79,13 +85,17 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(const T* __restrict
 }
 
 // One side of an N-dimensional layout: element (b, i_0 .. i_{rank-1}) of the
-// packed natural buffer is element b * batch_stride + sum_a r_a(i_a) *
-// stride[a] of the side, r_a the log_extent[a]-bit reversal where bit a of
-// `reversed` is set, else the identity.
+// packed natural buffer (power-of-two extents 2^log_extent[a]) is element
+// b * batch_stride + sum_a r_a(i_a) * stride[a] of the side, r_a the
+// log_extent[a]-bit reversal where bit a of `reversed` is set, else the
+// identity. Elements with some i_a >= extent[a] (the side's own extent,
+// shorter under the zero-extended embedding) are absent from the side: the
+// gather reads them as zero, the scatter drops them.
 struct NdSide {
     std::uint32_t rank = 0;
     std::uint32_t reversed = 0;
     std::uint32_t log_extent[kMaxRank] = {};
+    std::uint64_t extent[kMaxRank] = {};
     std::uint64_t stride[kMaxRank] = {};
     std::uint64_t batch_stride = 0;
 };
@@ -96,16 +106,18 @@ __global__ __launch_bounds__(kThreads) void nd_boundary_kernel(const T* __restri
     for (std::uint64_t linear = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; linear < count;
          linear += std::uint64_t(gridDim.x) * kThreads) {
         std::uint64_t rest = linear, physical = 0;
+        bool present = true;
         for (int a = int(side.rank) - 1; a >= 0; --a) {
             const std::uint32_t l = side.log_extent[a];
             std::uint64_t i = rest & ((std::uint64_t{1} << l) - 1);
             rest >>= l;
+            present = present && i < side.extent[a];
             if ((side.reversed >> a) & 1u) i = __brevll(i) >> (64u - l);
             physical += i * side.stride[a];
         }
         physical += rest * side.batch_stride;
-        if constexpr (GATHER) dst[linear] = src[physical];
-        else dst[physical] = src[linear];
+        if constexpr (GATHER) dst[linear] = present ? src[physical] : T{};
+        else if (present) dst[physical] = src[linear];
     }
 }
 
@@ -192,19 +204,28 @@ class CompositeExecutor final : public Executor {
         }
         std::string joined;
         for (std::size_t i = 0; i < names.size(); ++i) joined += (i ? "," : "") + names[i];
-        algorithm = std::string(flatten ? (rank == 2 ? "rank2-kronecker" : "rankN-kronecker")
-                                        : (rank == 2 ? "rank2-transpose" : "rankN-composite")) +
+        algorithm = std::string(rank == 1   ? "zero-extended"
+                                : flatten   ? (rank == 2 ? "rank2-kronecker" : "rankN-kronecker")
+                                            : (rank == 2 ? "rank2-transpose" : "rankN-composite")) +
                     "[" + joined + "]" + (direct_in_ ? "+direct-input" : "") + (direct_out_ ? "+direct-output" : "");
         reason = flatten ? "FWHT of the flattened point count: H(n0 n1) = H(n0) (x) H(n1), same stage order"
                          : "one batched rank-1 plan per axis, innermost first, tiled transposes between";
+        if (r.embedding) reason += "; sides zero-extended to / cut from the power-of-two extents";
         json::Writer w;
         w.begin_object()
             .field("schema_version", 1u)
             .field("kind", "composition")
             .field("rank", rank)
-            .field("lowering", flatten ? "kronecker" : "transpose");
+            .field("lowering", flatten ? "kronecker" : "transpose")
+            .field("zero_extended", r.embedding);
         w.begin_array("extents");
         for (auto e : r.extents) w.value(e);
+        w.end_array();
+        w.begin_array("input_extents");
+        for (auto e : r.in_extents) w.value(e);
+        w.end_array();
+        w.begin_array("output_extents");
+        for (auto e : r.out_extents) w.value(e);
         w.end_array();
         w.begin_array("schedule");
         for (const auto& s : steps_) {
@@ -272,6 +293,9 @@ class CompositeExecutor final : public Executor {
         c.out_strides.clear();
         c.in_reversed.clear();
         c.out_reversed.clear();
+        c.embedding = false;
+        c.in_extents.clear();
+        c.out_extents.clear();
         c.n = n;
         c.log_n = log2_u64(n);
         c.batch = batch;
@@ -289,9 +313,10 @@ class CompositeExecutor final : public Executor {
     bool packed_natural(bool input) const {
         const auto& strides = input ? r_.in_strides : r_.out_strides;
         const auto& reversed = input ? r_.in_reversed : r_.out_reversed;
+        const auto& side = input ? r_.in_extents : r_.out_extents;
         std::uint64_t expect = 1;
         for (std::size_t a = r_.rank; a-- > 0;) {
-            if (strides[a] != expect || reversed[a]) return false;
+            if (strides[a] != expect || reversed[a] || side[a] != r_.extents[a]) return false;
             expect *= r_.extents[a];
         }
         return r_.batch == 1 || (input ? r_.in_batch_stride : r_.out_batch_stride) == r_.n;
@@ -302,8 +327,10 @@ class CompositeExecutor final : public Executor {
         s.rank = r_.rank;
         const auto& strides = input ? r_.in_strides : r_.out_strides;
         const auto& reversed = input ? r_.in_reversed : r_.out_reversed;
+        const auto& side = input ? r_.in_extents : r_.out_extents;
         for (std::uint32_t a = 0; a < r_.rank; ++a) {
             s.log_extent[a] = logs[a];
+            s.extent[a] = side[a];
             s.stride[a] = strides[a];
             if (reversed[a]) s.reversed |= 1u << a;
         }
@@ -339,7 +366,8 @@ class CompositeExecutor final : public Executor {
 }  // namespace
 
 std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel) {
-    require(r.rank >= 2 && r.rank <= kMaxRank && r.extents.size() == r.rank, "composite plans need rank 2 to 8");
+    require(r.rank >= 1 && r.rank <= kMaxRank && r.extents.size() == r.rank && (r.rank >= 2 || r.embedding),
+            "composite plans need rank 2 to 8 or the zero-extended embedding");
     // A flattened FWHT is one rank-1 plan; it exists up to the resident length.
     const bool flatten = r.op == Op::Fwht && !(r.inverse && r.normalize) && r.log_n <= 13;
     return std::make_unique<CompositeExecutor>(r, flatten, sel);

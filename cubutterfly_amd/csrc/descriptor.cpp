@@ -107,7 +107,25 @@ bool layout_overlaps(std::vector<std::pair<std::size_t, std::size_t>> dims) {
     return false;
 }
 
+std::size_t next_pow2(std::size_t n) {
+    std::size_t p = 1;
+    while (p < n) p = checked_mul(p, 2);
+    return p;
+}
+
+// Extents of one side. The zero-extended embedding pads every axis to the
+// next power of two on the forward output and the inverse input (reference
+// semantic_contract.cpp:43-53).
+std::vector<std::size_t> side_extents(const cubutterflyDescriptor& d, bool input) {
+    std::vector<std::size_t> e = d.extents;
+    if (d.length_mode == CUBUTTERFLY_LENGTH_ZERO_EXTENDED_EMBEDDING &&
+        input == (d.direction == CUBUTTERFLY_DIRECTION_INVERSE))
+        for (auto& n : e) n = next_pow2(n);
+    return e;
+}
+
 SideLayout side_layout(const cubutterflyDescriptor& d, bool input) {
+    const std::vector<std::size_t> extents = side_extents(d, input);
     SideLayout l;
     l.strides = input ? d.input_strides : d.output_strides;
     l.batch_stride = input ? d.input_batch_stride : d.output_batch_stride;
@@ -116,7 +134,7 @@ SideLayout side_layout(const cubutterflyDescriptor& d, bool input) {
         std::size_t stride = 1;
         for (std::size_t axis = d.rank; axis-- > 0;) {
             l.strides[axis] = stride;
-            stride = checked_mul(stride, d.extents[axis]);
+            stride = checked_mul(stride, extents[axis]);
         }
     }
     require(l.strides.size() == d.rank, "one stride per axis is required");
@@ -124,8 +142,8 @@ SideLayout side_layout(const cubutterflyDescriptor& d, bool input) {
     std::vector<std::pair<std::size_t, std::size_t>> dims;
     for (std::size_t axis = 0; axis < d.rank; ++axis) {
         require(l.strides[axis] > 0, "axis strides must be positive");
-        span = checked_add(span, checked_mul(d.extents[axis] - 1, l.strides[axis]));
-        if (d.extents[axis] > 1) dims.emplace_back(l.strides[axis], d.extents[axis]);
+        span = checked_add(span, checked_mul(extents[axis] - 1, l.strides[axis]));
+        if (extents[axis] > 1) dims.emplace_back(l.strides[axis], extents[axis]);
     }
     if (l.batch_stride == 0) l.batch_stride = span;
     checked_add(span, checked_mul(d.batch - 1, l.batch_stride));
@@ -198,9 +216,10 @@ void validate_descriptor(const cubutterflyDescriptor& d) {
             require(d.rank == 1 && is_pow2(d.extents[0]), "legacy bit reversal requires rank-one power-of-two shape");
         (void)side_bit_reversed(d, input);
         const auto& orders = input ? d.input_orders : d.output_orders;
+        const auto extents = side_extents(d, input);
         for (std::size_t axis = 0; axis < orders.size(); ++axis)
             if (orders[axis] == CUBUTTERFLY_ORDER_BIT_REVERSED)
-                require(is_pow2(d.extents[axis]), "bit-reversed order requires a power-of-two extent");
+                require(is_pow2(extents[axis]), "bit-reversed order requires a power-of-two extent");
     }
     (void)side_layout(d, true);
     (void)side_layout(d, false);
@@ -223,14 +242,18 @@ void validate_descriptor(const cubutterflyDescriptor& d) {
 Request lower_request(const cubutterflyDescriptor& d) {
     validate_descriptor(d);
     supported(d.rank <= kMaxRank, "ranks above eight are not executable");
-    supported(d.length_mode == CUBUTTERFLY_LENGTH_STANDARD, "zero-extended embedding is not executable");
+    const bool embedding = d.length_mode == CUBUTTERFLY_LENGTH_ZERO_EXTENDED_EMBEDDING;
     supported(d.execution_mode != CUBUTTERFLY_EXECUTION_XD, "XD execution requires a multidimensional descriptor");
     supported(d.fft_type == CUBUTTERFLY_FFT_C2C, "only C2C FFTs are executable");
     supported(d.input_ntt_layout != CUBUTTERFLY_NTT_LAYOUT_APPT_STATIC &&
                   d.output_ntt_layout != CUBUTTERFLY_NTT_LAYOUT_APPT_STATIC,
               "APPT static layouts are not executable");
+    // Executed (physical) extents: the power-of-two embedding of each axis.
+    std::vector<std::size_t> physical = d.extents;
+    if (embedding)
+        for (auto& e : physical) e = next_pow2(e);
     std::size_t n = 1;
-    for (auto e : d.extents) {
+    for (auto e : physical) {
         supported(is_pow2(e) && e >= 2, "only power-of-two lengths >= 2 are executable");
         n = checked_mul(n, e);
     }
@@ -238,13 +261,19 @@ Request lower_request(const cubutterflyDescriptor& d) {
     Request r;
     const SideLayout in = side_layout(d, true), out = side_layout(d, false);
     r.rank = d.rank;
-    if (d.rank == 1) {
+    r.embedding = embedding;
+    if (d.rank == 1 && !embedding) {
         r.in_stride = in.strides[0];
         r.out_stride = out.strides[0];
     } else {
-        // Rank two and above: per-axis layout for the composite plan, which
-        // brings each axis innermost in turn (reference src/c_api.cpp:4578-4600).
-        r.extents.assign(d.extents.begin(), d.extents.end());
+        // Rank two and above, and the zero-extended embedding: per-axis
+        // layout for the composite plan, which brings each axis innermost in
+        // turn (reference src/c_api.cpp:4578-4600, 5231-5327) and pads / cuts
+        // each side to its own extents.
+        r.extents.assign(physical.begin(), physical.end());
+        const auto in_ext = side_extents(d, true), out_ext = side_extents(d, false);
+        r.in_extents.assign(in_ext.begin(), in_ext.end());
+        r.out_extents.assign(out_ext.begin(), out_ext.end());
         r.in_strides.assign(in.strides.begin(), in.strides.end());
         r.out_strides.assign(out.strides.begin(), out.strides.end());
         for (bool input : {true, false}) {
@@ -265,8 +294,8 @@ Request lower_request(const cubutterflyDescriptor& d) {
     r.storage = d.storage;
     r.policy = d.algorithm_policy;
     r.explicit_algorithm = d.explicit_algorithm;
-    r.input_bit_reversed = d.rank == 1 && side_bit_reversed(d, true);
-    r.output_bit_reversed = d.rank == 1 && side_bit_reversed(d, false);
+    r.input_bit_reversed = d.rank == 1 && !embedding && side_bit_reversed(d, true);
+    r.output_bit_reversed = d.rank == 1 && !embedding && side_bit_reversed(d, false);
     r.element_bytes = storage_bytes(d.storage);
     // Strided sides, and FWHT / FFT logical orders, go through the semantic
     // boundary: gather to packed natural order, the packed transform,
@@ -290,7 +319,7 @@ Request lower_request(const cubutterflyDescriptor& d) {
     // NTT and FFT rows with a pitch, n >= 2^12: one transform per tile, each
     // at its own offset (NTT: the RNS engine's per-polynomial offsets; FFT:
     // a per-side transform pitch).
-    const bool rows_pitched = d.rank == 1 && strided && r.in_stride == 1 && r.out_stride == 1 &&
+    const bool rows_pitched = d.rank == 1 && !embedding && strided && r.in_stride == 1 && r.out_stride == 1 &&
                               (!r.in_place || r.in_batch_stride == r.out_batch_stride);
     if (d.op == CUBUTTERFLY_OPERATOR_FWHT)
         r.pitched = rows_pitched && !r.input_bit_reversed && !r.output_bit_reversed && n >= 16 &&
@@ -304,7 +333,7 @@ Request lower_request(const cubutterflyDescriptor& d) {
     const bool reversed = r.input_bit_reversed || r.output_bit_reversed;
     const bool native_orders =
         d.op == CUBUTTERFLY_OPERATOR_NTT || (d.op == CUBUTTERFLY_OPERATOR_FFT && n <= (std::size_t{1} << 14));
-    r.boundary = d.rank == 1 && !r.pitched && (strided || (reversed && !native_orders));
+    r.boundary = d.rank == 1 && !embedding && !r.pitched && (strided || (reversed && !native_orders));
     switch (d.op) {
         case CUBUTTERFLY_OPERATOR_FWHT:
             r.op = Op::Fwht;
@@ -313,7 +342,7 @@ Request lower_request(const cubutterflyDescriptor& d) {
                 supported(d.compute == CUBUTTERFLY_COMPUTE_FP32 &&
                               d.output_rounding == CUBUTTERFLY_ROUNDING_FINAL_STORAGE,
                           "FP16 FWHT requires FP32 compute with final-storage rounding");
-                supported(d.rank == 1, "FP16 FWHT is executable at rank one");
+                supported(d.rank == 1 && !embedding, "FP16 FWHT is executable at rank one, standard length");
                 r.fp16_final = true;
                 r.output_scale = static_cast<float>(d.output_scale);
                 r.allow_mma = d.arithmetic_policy == CUBUTTERFLY_ARITHMETIC_ALLOW_FP16_MMA;

@@ -90,17 +90,23 @@ struct Request {
     std::uint32_t rank = 1;
     std::vector<std::uint64_t> extents, in_strides, out_strides;
     std::vector<std::uint8_t> in_reversed, out_reversed;
+    // Zero-extended embedding (any rank): `extents` are the executed
+    // power-of-two extents, each side keeps its own (the logical extents on
+    // the forward input and the inverse output).
+    bool embedding = false;
+    std::vector<std::uint64_t> in_extents, out_extents;
     std::size_t data_bytes() const { return static_cast<std::size_t>(n * batch) * element_bytes; }
     // Bytes a side spans: the sum over axes of (extent - 1) stride, plus
     // (batch - 1) batch stride, plus one element.
     std::size_t span_bytes(bool input) const {
         const std::uint64_t bs = input ? in_batch_stride : out_batch_stride;
         std::uint64_t last = (batch - 1) * bs;
-        if (rank == 1) {
+        if (extents.empty()) {
             last += (n - 1) * (input ? in_stride : out_stride);
         } else {
             const auto& strides = input ? in_strides : out_strides;
-            for (std::size_t axis = 0; axis < extents.size(); ++axis) last += (extents[axis] - 1) * strides[axis];
+            const auto& side = input ? in_extents : out_extents;
+            for (std::size_t axis = 0; axis < side.size(); ++axis) last += (side[axis] - 1) * strides[axis];
         }
         return static_cast<std::size_t>(last + 1) * element_bytes;
     }

@@ -41,12 +41,13 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel);
 
 // Gather / packed child / scatter, for strided sides and FWHT / FFT orders.
 std::unique_ptr<Executor> make_boundary_executor(const Request& r, Selection* sel);
-// Rank >= 2: one batched rank-1 plan per axis, innermost first, with tiled
-// transposes bringing each axis innermost and the original order back.
+// Rank >= 2 and the zero-extended embedding: one batched rank-1 plan per
+// axis, innermost first, with tiled transposes bringing each axis innermost
+// and the original order back; sides padded or cut to their own extents.
 std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel);
 
 inline std::unique_ptr<Executor> plan_executor(const Request& r, Selection* sel = nullptr) {
-    if (r.rank > 1) return make_composite_executor(r, sel);
+    if (r.rank > 1 || r.embedding) return make_composite_executor(r, sel);
     if (r.boundary) return make_boundary_executor(r, sel);
     return select_leaf(r, sel);
 }

@@ -27,9 +27,17 @@ def to_host(torch, tensor, np_dtype):
 def run_plan(torch, lib, transform, host_input, stream, in_place=False, options=None):
     """Execute `transform` on host_input through the C ABI; returns the host result."""
     x = to_device(torch, host_input)
-    y = x if in_place else torch.empty_like(x)
     with cb.Plan(lib, transform, options=options, stream=stream) as plan:
         assert plan.input_size() == x.numel() * x.element_size()
+        # Output shaped like the input when the sizes agree, else flat (the
+        # zero-extended embedding changes the extents).
+        out_elems = plan.output_size() // x.element_size()
+        if in_place:
+            y = x
+        elif out_elems == x.numel():
+            y = torch.empty_like(x)
+        else:
+            y = torch.empty(out_elems, dtype=x.dtype, device="cuda")
         ws_bytes = plan.workspace_size()
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda") if ws_bytes else None
         if ws is not None:
