@@ -15,7 +15,9 @@
 #include <sys/file.h>
 #include <unistd.h>
 
+#include <atomic>
 #include <cstdio>
+#include <cstdlib>
 #include <fstream>
 #include <limits>
 
@@ -102,6 +104,50 @@ struct Event {
     }
     Event(const Event&) = delete;
     Event& operator=(const Event&) = delete;
+};
+
+// CUBUTTERFLY_PLAN_TRACE = 1 | stderr | <path>: one JSON line per search
+// event (schema cubutterfly-plan-search-trace-v1, reference
+// src/plan_search_trace.hpp:17-60). Tracing never changes the search: a sink
+// that cannot be written disables it with a note on stderr.
+class SearchTrace {
+  public:
+    SearchTrace() {
+        const char* dest = std::getenv("CUBUTTERFLY_PLAN_TRACE");
+        if (!dest || !*dest || std::string(dest) == "0") return;
+        static std::atomic<std::uint64_t> next_id{0};
+        id_ = ++next_id;
+        if (std::string(dest) == "1" || std::string(dest) == "stderr") {
+            sink_ = stderr;
+        } else {
+            sink_ = std::fopen(dest, "a");
+            owns_ = sink_ != nullptr;
+            if (!sink_) std::fprintf(stderr, "cuButterfly: CUBUTTERFLY_PLAN_TRACE disabled: cannot open %s\n", dest);
+        }
+    }
+    ~SearchTrace() {
+        if (owns_) std::fclose(sink_);
+    }
+    SearchTrace(const SearchTrace&) = delete;
+    SearchTrace& operator=(const SearchTrace&) = delete;
+    // `fields`: the members after the common ones, as JSON text without braces.
+    void event(const char* phase, const std::string& fields) {
+        if (!sink_) return;
+        const std::string line = "{\"schema\":\"cubutterfly-plan-search-trace-v1\",\"search_id\":" +
+                                 std::to_string(id_) + ",\"phase\":" + json::quote(phase) +
+                                 (fields.empty() ? "" : "," + fields) + "}\n";
+        if (std::fwrite(line.data(), 1, line.size(), sink_) != line.size() || std::fflush(sink_) != 0) {
+            std::fprintf(stderr, "cuButterfly: CUBUTTERFLY_PLAN_TRACE disabled: write failed\n");
+            if (owns_) std::fclose(sink_);
+            sink_ = nullptr;
+            owns_ = false;
+        }
+    }
+
+  private:
+    std::FILE* sink_ = nullptr;
+    bool owns_ = false;
+    std::uint64_t id_ = 0;
 };
 
 // Mean milliseconds of one execution: 3 untimed runs, then 20 between two
@@ -220,13 +266,22 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     hip_check(hipStreamIsCapturing(sel->stream, &capture), "MEASURE capture query");
     supported(capture == hipStreamCaptureStatusNone, "MEASURE cannot time candidates during stream capture");
+    SearchTrace trace;
+    const auto names = leaf_candidates(r);
+    trace.event("inventory", "\"key\":" + json::quote(key) + ",\"candidate_count\":" + std::to_string(names.size()) +
+                                 ",\"timing_protocol\":\"event-loop\",\"warmup\":3,\"repeat\":20");
     std::vector<std::unique_ptr<Executor>> built;
     std::size_t ws_bytes = 0;
-    for (const auto& name : leaf_candidates(r)) {
+    for (const auto& name : names) {
         Request v = r;
         v.variant = name;
-        built.push_back(build_leaf(v));
-        ws_bytes = std::max(ws_bytes, built.back()->workspace_bytes());
+        try {
+            built.push_back(build_leaf(v));
+            ws_bytes = std::max(ws_bytes, built.back()->workspace_bytes());
+        } catch (const NotSupported& e) {  // not a lowering here after all: skip it
+            trace.event("result", "\"candidate\":" + json::quote(name) + ",\"status\":\"rejected\",\"reason\":" +
+                                      json::quote(e.what()));
+        }
     }
     require(!built.empty(), "no candidate lowering to measure");
     const std::size_t bytes = r.data_bytes();
@@ -240,11 +295,15 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
         char text[64];
         std::snprintf(text, sizeof text, "=%.4f ms", ms);
         results += (i ? ", " : "") + built[i]->algorithm + text;
+        trace.event("result", "\"candidate\":" + json::quote(built[i]->algorithm) +
+                                  ",\"status\":\"accepted\",\"kernel_ms\":" + std::to_string(ms));
         if (ms < best_ms) {
             best_ms = ms;
             best = i;
         }
     }
+    trace.event("selected", "\"algorithm\":" + json::quote(built[best]->algorithm) +
+                                ",\"kernel_ms\":" + std::to_string(best_ms));
     store_cache(sel->cache_path, key, built[best]->algorithm);
     combine_source(*sel, CUBUTTERFLY_SELECTION_RUNTIME_MEASURED);
     note(*sel, "measured " + results);

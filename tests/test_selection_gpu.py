@@ -143,3 +143,21 @@ def test_unknown_explicit_name_is_not_supported(torch_gpu, lib):
     with pytest.raises(cb.Error) as e:
         cb.Plan(lib, fft(16, 1), options=opts)
     assert e.value.status == cb.Status.NOT_SUPPORTED
+
+
+def test_plan_trace(torch_gpu, lib, stream, tmp_path, monkeypatch):
+    # CUBUTTERFLY_PLAN_TRACE=<path>: JSON lines per search event (reference
+    # src/plan_search_trace.hpp:17-60).
+    import json
+    trace = tmp_path / "trace.jsonl"
+    monkeypatch.setenv("CUBUTTERFLY_PLAN_TRACE", str(trace))
+    with cb.Plan(lib, fft(16, 2), options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE), stream=stream,
+                 cache_path=tmp_path / "c.tsv") as plan:
+        chosen = plan.algorithm_name()
+    rows = [json.loads(line) for line in trace.read_text().splitlines()]
+    assert {r["schema"] for r in rows} == {"cubutterfly-plan-search-trace-v1"}
+    phases = [r["phase"] for r in rows]
+    assert phases[0] == "inventory" and phases[-1] == "selected"
+    results = [r for r in rows if r["phase"] == "result"]
+    assert len(results) == rows[0]["candidate_count"] and all(r["kernel_ms"] > 0 for r in results)
+    assert rows[-1]["algorithm"] == chosen
