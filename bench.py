@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Headline benchmark of the MI355X butterfly path (one GPU).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c1p|c2|c3a|c3b|c4|c5a|c5b|copy]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c1p|c2|c3a|c3b|c4|c5a|c5b|r2|copy]
                 [--no-cpu] [--verify] [--eager]
 
 A step is one call of the hot path over one batch of the named BASELINE
@@ -352,6 +352,34 @@ class FftC64(OnePlan):
                               f"{self.batch} x 2^{self.log_n} through reference_fft, iterative radix-2")
 
 
+class FftC64Rank2(FftC64):
+    """Rank-2 complex64 FFT, 4096 x 4096 (not a BASELINE line): the composite
+    plan (row transforms, tiled transposes, column transforms)."""
+
+    def __init__(self):
+        super().__init__(24, 1)
+        self.name = "r2"
+        self.description = "rank-2 complex FFT c64 forward, 4096 x 4096, batch 1, N(0,1) parts"
+
+    def transform(self, cb):
+        return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
+                            extents=[4096, 4096], batch=1)
+
+    def verify(self, torch):
+        got = self.outputs[0].cpu().numpy().reshape(4096, 4096).astype(np.complex128)
+        ref = np.fft.fft2(self.host.reshape(4096, 4096).astype(np.complex128))
+        return bool(np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5)
+
+    def cpu_sample(self, threads):
+        import oracle
+
+        def both_axes():
+            rows = oracle.fft_c64(self.host.reshape(4096, 4096), threads=threads)
+            oracle.fft_c64(np.ascontiguousarray(rows.T), threads=threads)
+
+        return self.timed_cpu(both_axes, "4096 x 4096 through reference_fft along both axes")
+
+
 class FwhtFp16(OnePlan):
     """C5: QuaRot-style FP16 FWHT, scale 1/sqrt(n), FP32 compute, one final
     FP16 rounding: 16384 x 4096 (c5a) or 524288 x 128 (c5b)."""
@@ -414,7 +442,7 @@ class DeviceCopy(Workload):
 
 WORKLOADS = {"c1": FwhtFp32, "c1p": FwhtFp32Pitched, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1), "c3b": lambda: FftC64(14, 1024),
              "c4": RnsNegacyclic, "c5a": lambda: FwhtFp16(16384, 4096), "c5b": lambda: FwhtFp16(524288, 128),
-             "copy": DeviceCopy}
+             "r2": FftC64Rank2, "copy": DeviceCopy}
 DEFAULT_WORKLOAD = "c2"
 
 

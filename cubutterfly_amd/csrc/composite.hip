@@ -10,6 +10,11 @@
 // before the moved one form the blocks, the moved axis the rows, the axes
 // after it the columns.
 //
+// A rank-2 FFT whose axes the row kernel's transposing store covers runs as
+// two row passes instead: the rows of each 2^n0 x 2^n1 block transformed and
+// stored transposed, then the rows of the transposed block, stored back in
+// the original order (two HBM round trips where the transposes take four).
+//
 // FWHT needs none of this: the Sylvester Hadamard matrix of n0 * n1 points
 // is the Kronecker product H(n0) (x) H(n1), and the innermost-first axis
 // order applies the stages from the lowest index bit to the highest, which is
@@ -166,7 +171,23 @@ class CompositeExecutor final : public Executor {
         in_side_ = side(true, logs);
         out_side_ = side(false, logs);
         std::vector<std::string> names;
-        if (flatten) {
+        if (!flatten && r.op == Op::Fft && rank == 2) {
+            // Each axis as one row pass that stores its blocks transposed:
+            // rows of the caller's layout, then rows of the transposed one,
+            // which lands back in the original order. No transpose kernels.
+            const std::uint64_t n0 = r.extents[0], n1 = r.extents[1];
+            auto rows1 = make_fft_rows_transposed(axis_request(n1, r.batch * n0), logs[0]);
+            auto rows0 = make_fft_rows_transposed(axis_request(n0, r.batch * n1), logs[1]);
+            if (rows1 && rows0) {
+                transposing_ = true;
+                children_.push_back(std::move(rows1));
+                children_.push_back(std::move(rows0));
+                steps_.push_back(Step{false, 0, 1, 0, 0, 0});
+                steps_.push_back(Step{false, 1, 0, 0, 0, 0});
+            }
+        }
+        if (transposing_) {
+        } else if (flatten) {
             children_.push_back(plan_executor(axis_request(r.n, r.batch), sel));
             steps_.push_back(Step{false, 0, 0, 0, 0, 0});
         } else {
@@ -204,19 +225,21 @@ class CompositeExecutor final : public Executor {
         }
         std::string joined;
         for (std::size_t i = 0; i < names.size(); ++i) joined += (i ? "," : "") + names[i];
-        algorithm = std::string(rank == 1   ? "zero-extended"
-                                : flatten   ? (rank == 2 ? "rank2-kronecker" : "rankN-kronecker")
-                                            : (rank == 2 ? "rank2-transpose" : "rankN-composite")) +
+        algorithm = std::string(rank == 1      ? "zero-extended"
+                                : transposing_ ? "rank2-transposing"
+                                : flatten      ? (rank == 2 ? "rank2-kronecker" : "rankN-kronecker")
+                                               : (rank == 2 ? "rank2-transpose" : "rankN-composite")) +
                     "[" + joined + "]" + (direct_in_ ? "+direct-input" : "") + (direct_out_ ? "+direct-output" : "");
-        reason = flatten ? "FWHT of the flattened point count: H(n0 n1) = H(n0) (x) H(n1), same stage order"
-                         : "one batched rank-1 plan per axis, innermost first, tiled transposes between";
+        reason = transposing_ ? "each axis one row pass with a transposing store (innermost axis first)"
+                 : flatten    ? "FWHT of the flattened point count: H(n0 n1) = H(n0) (x) H(n1), same stage order"
+                              : "one batched rank-1 plan per axis, innermost first, tiled transposes between";
         if (r.embedding) reason += "; sides zero-extended to / cut from the power-of-two extents";
         json::Writer w;
         w.begin_object()
             .field("schema_version", 1u)
             .field("kind", "composition")
             .field("rank", rank)
-            .field("lowering", flatten ? "kronecker" : "transpose")
+            .field("lowering", transposing_ ? "transposing-rows" : flatten ? "kronecker" : "transpose")
             .field("zero_extended", r.embedding);
         w.begin_array("extents");
         for (auto e : r.extents) w.value(e);
@@ -246,11 +269,22 @@ class CompositeExecutor final : public Executor {
         mapping_json = w.str();
     }
 
+    // Ping-pong buffers of the packed data the schedule touches (0, 1 or 2):
+    // the gather's target, then every step's destination but a direct last one.
+    std::size_t buffers() const {
+        std::size_t used = direct_in_ ? 0 : 1;
+        int next = direct_in_ ? 0 : 1;
+        for (std::size_t i = 0; i < steps_.size(); ++i) {
+            if (i + 1 == steps_.size() && direct_out_) break;
+            used = std::max<std::size_t>(used, std::size_t(next) + 1);
+            next ^= 1;
+        }
+        return used;
+    }
+
     std::size_t workspace_bytes() const override {
-        // Two ping-pong buffers of the packed data, then the largest child's.
-        const bool one_buffer = steps_.size() == 1 && (direct_in_ || direct_out_);
-        const std::size_t buffers = steps_.size() == 1 && direct_in_ && direct_out_ ? 0 : one_buffer ? 1 : 2;
-        return buffers * align16(r_.data_bytes()) + align16(child_ws_);
+        // The ping-pong buffers, then the largest child's workspace.
+        return buffers() * align16(r_.data_bytes()) + align16(child_ws_);
     }
 
     void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
@@ -259,8 +293,7 @@ class CompositeExecutor final : public Executor {
         require(ws_bytes == 0 || ws != nullptr, "a composite plan needs its workspace");
         auto* base = static_cast<unsigned char*>(ws);
         unsigned char* buffer[2] = {base, base + bytes};
-        const std::size_t buffers = (ws_bytes - align16(child_ws_)) / (bytes ? bytes : 1);
-        void* child_ws = child_ws_ ? base + buffers * bytes : nullptr;
+        void* child_ws = child_ws_ ? base + buffers() * bytes : nullptr;
         const std::uint64_t count = r_.n * r_.batch;
 
         // Ping-pong: the next destination is the buffer the current data is
@@ -356,6 +389,7 @@ class CompositeExecutor final : public Executor {
     }
 
     Request r_;
+    bool transposing_ = false;
     bool direct_in_ = false, direct_out_ = false;
     NdSide in_side_, out_side_;
     std::vector<std::unique_ptr<Executor>> children_;

@@ -185,9 +185,11 @@ constexpr int digit_bits_for(int lb, bool single) { return single && lb >= 13 ? 
 // One FFT pass over LT transform bits. COL: high bits, tile of 2^LI columns;
 // ROW: low bits, tile of 2^LI rows (the final pass, storing in natural order);
 // SINGLE: a one-pass transform, 2^LI whole rows per tile.
-// ORD (one-pass tiles only): bit 0 reads the input in bit-reversed logical
-// order, bit 1 writes the output in bit-reversed order (the DIF result's own
-// order, so the final store skips the reversal).
+// ORD: for one-pass tiles, bit 0 reads the input in bit-reversed logical
+// order and bit 1 writes the output in bit-reversed order (the DIF result's
+// own order, so the final store skips the reversal); for row passes, bit 2
+// reads the block's rows in natural order (a row-major 2^l1 x 2^l2 block
+// whose row transforms are written transposed: the rank-2 axis step).
 template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD = 0>
 struct FftPass {
     static constexpr int LB = LT + LI;
@@ -350,6 +352,9 @@ struct FftPass {
                 return (i - x) | brev(x, LT);
             }
             return i;
+        } else if constexpr ((ORD & 4) != 0) {  // rows k0 + rr of a row-major block, in natural order
+            const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
+            return ((k0 + (i >> LT)) << a.l2) + (i & ((1u << LT) - 1u));
         } else {  // rows bitrev(k0 + rr) of one transform, matching the transposing store
             const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
             return (brev(k0 + (i >> LT), a.l1) << a.l2) + (i & ((1u << LT) - 1u));
@@ -619,6 +624,15 @@ void add_two() {
     add<l2, row_lines(l1, l2), false, false>();
 }
 
+// Row passes over natural-order rows with the transposing store, tiles of
+// 2^14 points (2^(14 - LT) rows, at least 4 so the transposed segments are
+// 32 bytes or longer).
+template <int LT>
+void add_rows_natural() {
+    registry()[Key{LT, 14 - LT, false, false, false, 4}] = &launch<LT, 14 - LT, false, false, false, 4>;
+    registry()[Key{LT, 14 - LT, false, false, true, 4}] = &launch<LT, 14 - LT, false, false, true, 4>;
+}
+
 void register_all() {
     add<1, single_li(1), false, true>();
     add<2, single_li(2), false, true>();
@@ -644,6 +658,15 @@ void register_all() {
     add_two<22>();
     add_two<23>();
     add_two<24>();
+    add_rows_natural<4>();
+    add_rows_natural<5>();
+    add_rows_natural<6>();
+    add_rows_natural<7>();
+    add_rows_natural<8>();
+    add_rows_natural<9>();
+    add_rows_natural<10>();
+    add_rows_natural<11>();
+    add_rows_natural<12>();
 }
 
 Launch lookup(const Key& k) {
@@ -918,6 +941,73 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r) {
     supported(split > 0 && split_available(m, split, r.inverse),
               "'" + r.variant + "' is not a lowering of this FFT");
     return std::make_unique<FftExecutor>(r, split);
+}
+
+namespace {
+
+// FFTs of the rows of row-major 2^l1 x 2^l2 blocks, each block's result
+// written transposed (2^l2 x 2^l1): one row pass over natural-order rows.
+class FftRowsTransposedExecutor final : public Executor {
+  public:
+    FftRowsTransposedExecutor(const Request& r, std::uint32_t l1, Launch fn) : fn_(fn) {
+        const std::uint32_t l2 = r.log_n;
+        const int li = 14 - int(l2);
+        // The row kernel forms level twiddles as powers of the 2^(l1 + l2)-th
+        // root (w^(j << (m - h)) = the 2^h-th root's j-th power).
+        upload_twiddles(twa_, twb_, int(l1 + l2), r.inverse);
+        const std::uint64_t blocks = r.batch >> l1;
+        const std::uint64_t tiles = blocks << (l1 - std::uint32_t(li));
+        require(tiles <= 0xffffffffull && r.batch <= 0xffffffffull, "FFT batch exceeds the grid");
+        args_ = FftArgs{};
+        args_.twa = twa_.as<float2>();
+        args_.twb = twb_.as<float2>();
+        args_.l1 = l1;
+        args_.l2 = l2;
+        args_.rows = unsigned(r.batch);
+        args_.tiles = unsigned(tiles);
+        args_.scale = r.normalize ? 1.0f / float(r.n) : 1.0f;
+        args_.in_pitch = args_.out_pitch = std::uint64_t{1} << (l1 + l2);
+        algorithm = "fft-c64-rows-transposed-r16";
+        reason = "row transforms of 2^" + std::to_string(l1) + " x 2^" + std::to_string(l2) +
+                 " blocks with the transposing store of the two-pass row kernel";
+        json::Writer w;
+        w.begin_object()
+            .field("schema_version", 1u)
+            .field("operator", "fft")
+            .field("algorithm", algorithm)
+            .field("log_n", l2)
+            .field("block_rows_log", l1)
+            .field("blocks", blocks)
+            .field("direction", r.inverse ? "inverse" : "forward")
+            .end_object();
+        mapping_json = w.str();
+    }
+    void execute(const void* in, void* out, void*, hipStream_t stream) override {
+        FftArgs a = args_;
+        a.in = static_cast<const float2*>(in);
+        a.out = static_cast<float2*>(out);
+        fn_(a, stream);
+        hip_check(hipGetLastError(), "FFT pass launch");
+    }
+
+  private:
+    Launch fn_;
+    FftArgs args_{};
+    DeviceBuffer twa_, twb_;
+};
+
+}  // namespace
+
+std::unique_ptr<Executor> make_fft_rows_transposed(const Request& r, std::uint32_t l1) {
+    const int l2 = int(r.log_n);
+    // Level-twiddle tables reach 2^24-th roots (so l1 + l2 <= 24, which also
+    // keeps a block's byte offsets in 32 bits).
+    if (l2 < 4 || l2 > 12 || int(l1) < 14 - l2 || l1 + std::uint32_t(l2) > 24 ||
+        (r.batch & ((std::uint64_t{1} << l1) - 1)) != 0)
+        return nullptr;
+    const Launch fn = lookup(Key{l2, 14 - l2, false, false, r.inverse, 4});
+    if (fn == nullptr) return nullptr;
+    return std::make_unique<FftRowsTransposedExecutor>(r, l1, fn);
 }
 
 // One-pass lengths have one lowering; two-pass lengths add the neighbouring

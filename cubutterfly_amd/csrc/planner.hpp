@@ -17,6 +17,10 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r);
 std::unique_ptr<Executor> make_ntt_executor(const Request& r);
 // Candidate lowerings of a rank-1 request, the static model's choice first.
 std::vector<std::string> fwht_candidates(const Request& r);
+// FFTs (r.log_n points) of the rows of row-major 2^l1 x 2^(r.log_n) blocks
+// (r.batch rows in all), each block's result stored transposed; null where
+// no kernel covers the shape.
+std::unique_ptr<Executor> make_fft_rows_transposed(const Request& r, std::uint32_t l1);
 std::vector<std::string> fft_candidates(const Request& r);
 std::vector<std::string> ntt_candidates(const Request& r);
 

@@ -161,3 +161,39 @@ def test_mapping_reports_children(torch_gpu, lib):
         axes = [s for s in m["schedule"] if s["step"] == "axis"]
         assert [s["axis"] for s in axes] == [1, 0]
         assert plan.workspace_size() == m["workspace_bytes"] >= 2 * 2 * 64 * (1 << 13) * 8
+
+
+@pytest.mark.parametrize("extents", [(256, 256), (1024, 512), (4096, 16), (16, 4096)])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_fft_transposing_rows(torch_gpu, lib, stream, extents, inverse):
+    # Two row passes with transposing stores, no transpose kernels.
+    batch = 3
+    x = data((batch,) + extents, np.complex64, 8)
+    t = fft_t(extents, batch, inverse=inverse)
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name().startswith("rank2-transposing[fft-c64-rows-transposed-r16,")
+        m = json.loads(plan.mapping_json())
+        assert [s["step"] for s in m["schedule"]] == ["axis", "axis"]
+        assert plan.workspace_size() == batch * extents[0] * extents[1] * 8  # one intermediate
+    got = run_plan(torch_gpu, lib, t, x, stream).astype(np.complex128)
+    ref = (np.fft.ifftn if inverse else np.fft.fftn)(x.astype(np.complex128), axes=(1, 2))
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
+
+
+def test_fft_transposing_rows_strided_in_place(torch_gpu, lib, stream):
+    # In place on pitched rows: gather, the two row passes, scatter.
+    n0, n1, batch, pitch = 256, 256, 2, 256 + 8
+    span = (batch * n0 - 1) * pitch + n1
+    rng = np.random.default_rng(9)
+    flat = (rng.standard_normal(span) + 1j * rng.standard_normal(span)).astype(np.complex64)
+    t = fft_t((n0, n1), batch, in_place=True, input_strides=[pitch, 1], input_batch_stride=n0 * pitch,
+              output_strides=[pitch, 1], output_batch_stride=n0 * pitch)
+    got = run_plan(torch_gpu, lib, t, flat, stream, in_place=True)
+    rows = np.stack([flat[k * pitch: k * pitch + n1] for k in range(batch * n0)]).reshape(batch, n0, n1)
+    ref = np.fft.fftn(rows.astype(np.complex128), axes=(1, 2)).reshape(batch * n0, n1)
+    got_rows = np.stack([got[k * pitch: k * pitch + n1] for k in range(batch * n0)]).astype(np.complex128)
+    assert np.linalg.norm(got_rows - ref) / np.linalg.norm(ref) <= 1e-5
+    gaps = np.ones(span, bool)
+    for k in range(batch * n0):
+        gaps[k * pitch: k * pitch + n1] = False
+    assert np.array_equal(got[gaps], flat[gaps])
