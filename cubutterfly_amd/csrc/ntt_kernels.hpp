@@ -152,7 +152,14 @@ __device__ __forceinline__ std::uint64_t mulhi(std::uint64_t a, std::uint64_t b)
 
 // x - m if x >= m else x (x < 2m).
 __device__ __forceinline__ std::uint32_t csub(std::uint32_t x, std::uint32_t m) { return min(x, x - m); }
-__device__ __forceinline__ std::uint64_t csub(std::uint64_t x, std::uint64_t m) { return x >= m ? x - m : x; }
+// 64-bit: add the wave-uniform -m (formed once in scalar registers) rather
+// than subtract m, so the result is one 64-bit add (v_lshl_add_u64) with no
+// carry chain through VCC.
+__device__ __forceinline__ std::uint64_t csub(std::uint64_t x, std::uint64_t m) {
+    std::uint64_t nm = std::uint64_t(0) - m;
+    asm("" : "+s"(nm));  // keeps the optimiser from folding the add back into a subtract
+    return x + (x >= m ? nm : std::uint64_t(0));
+}
 
 // (a b + c) mod 2^k as one multiply-add (v_mad_u64_u32 for 32-bit words,
 // where a 32-bit multiply and a separate add would take two instructions).
