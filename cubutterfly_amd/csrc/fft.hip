@@ -440,12 +440,23 @@ struct FftPass {
         lds_barrier();
         std::uint32_t it, ot;
         staged(a, tl, t, it, ot);
+        // Unnormalised plans (scale 1) skip the products: a wave-uniform
+        // branch over two copies of the store loop.
+        if (a.scale == 1.0f) {
 #pragma unroll
-        for (int r = 0; r < kE; ++r) {
-            std::uint32_t ir, orr;
-            staged(a, Tile{}, T * std::uint32_t(r), ir, orr);
-            const float2 x = lds[L::split(it, ir)];
-            store_at(make_float2(x.x * a.scale, x.y * a.scale), dst, ot * 8u, orr * 8u);
+            for (int r = 0; r < kE; ++r) {
+                std::uint32_t ir, orr;
+                staged(a, Tile{}, T * std::uint32_t(r), ir, orr);
+                store_at(lds[L::split(it, ir)], dst, ot * 8u, orr * 8u);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < kE; ++r) {
+                std::uint32_t ir, orr;
+                staged(a, Tile{}, T * std::uint32_t(r), ir, orr);
+                const float2 x = lds[L::split(it, ir)];
+                store_at(make_float2(x.x * a.scale, x.y * a.scale), dst, ot * 8u, orr * 8u);
+            }
         }
     }
 
