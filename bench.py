@@ -154,6 +154,15 @@ class FwhtFp32Pitched(FwhtFp32):
         return ("fwht_pitched_kernel" if name.endswith("-pitched") else "fwht_resident_kernel (inside " + name + ")")
 
 
+# VALU instructions per radix-2 butterfly of the NTT pass kernels, all work
+# of a pass included (loads, twiddle chunks, exchanges): rocprofv3
+# SQ_INSTS_VALU per dispatch divided by the dispatch's butterflies / 64,
+# summed over the four passes of one call (u32 lazy: 8.6; u64 lazy: 26.1).
+# With 256 CUs x 64 lanes x 2.4 GHz this gives the integer-VALU roof that
+# binds the NTT configs before HBM does.
+VALU_LANE_OPS_PER_S = 256 * 64 * 2.4e9
+
+
 class NttNegacyclic(Workload):
     """C2: forward then inverse negacyclic NTT, u32, q = 1073479681, n = 2^16, batch 64."""
     name = "c2"
@@ -161,11 +170,13 @@ class NttNegacyclic(Workload):
     description = ("single-prime negacyclic NTT u32, n=2^16, batch 64, q=1073479681 (30-bit, q = 1 mod 2n); "
                    "one step = forward then inverse of the batch")
 
+    valu_per_butterfly = 8.6
     def __init__(self, log_n=16, batch=64):
         from cubutterfly_amd import workloads
         self.log_n, self.batch, self.q = log_n, batch, workloads.C2_MODULUS
         self.transforms_per_call = 2 * batch  # forward + inverse transforms
         self.bytes_per_call = 2 * 2 * batch * (4 << log_n)
+        self.butterflies_per_call = self.transforms_per_call * (1 << (log_n - 1)) * log_n
 
     def setup(self, torch, lib, stream):
         import cubutterfly_amd as cb
@@ -227,12 +238,14 @@ class RnsNegacyclic(Workload):
     description = ("RNS negacyclic NTT u64, n=2^16, 32 limbs of distinct 60-bit primes (q = 1 mod 2^17), "
                    "one step = forward (natural->bit_reversed) then inverse (bit_reversed->natural)")
 
+    valu_per_butterfly = 26.1
     def __init__(self, log_n=16, limbs=32):
         from cubutterfly_amd import workloads
         self.log_n, self.limbs = log_n, limbs
         self.moduli = workloads.c4_moduli()[:limbs]
         self.transforms_per_call = 2 * limbs
         self.bytes_per_call = 2 * 2 * limbs * (8 << log_n)
+        self.butterflies_per_call = self.transforms_per_call * (1 << (log_n - 1)) * log_n
 
     def setup(self, torch, lib, stream):
         from cubutterfly_amd import ntt_roots, rns, workloads
@@ -557,6 +570,19 @@ def main():
         },
         "timing": "hip graph of %d calls, replayed" % CALLS_PER_GRAPH if not args.eager else "eager calls",
     }
+    if hasattr(workload, "valu_per_butterfly"):
+        # The integer-VALU roof of the NTT configs (see VALU_LANE_OPS_PER_S).
+        rate = workload.butterflies_per_call / (ms * 1e-3)
+        peak = VALU_LANE_OPS_PER_S / workload.valu_per_butterfly
+        result["valu_roofline"] = {
+            "bound": "valu",
+            "achieved": rate,
+            "peak": peak,
+            "unit": "butterflies/s",
+            "frac": rate / peak,
+            "valu_per_butterfly": workload.valu_per_butterfly,
+            "floor_ms_per_step": workload.butterflies_per_call / peak * 1e3,
+        }
     if args.verify:
         result["verified"] = workload.verify(torch)
     if not args.no_cpu:
