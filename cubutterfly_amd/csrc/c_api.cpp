@@ -418,8 +418,9 @@ cubutterflyStatus_t cubutterflyPlanGetPhysicalExtents(cubutterflyPlan_t plan, si
     return protect([&] {
         require(plan && extents, "plan and extents must be non-null");
         const auto& r = plan->request;
-        require(capacity >= r.rank, "extent capacity is too small");
-        if (r.rank == 1) extents[0] = r.n;
+        const std::uint32_t rank = plan->descriptor.rank;
+        require(capacity >= rank, "extent capacity is too small");
+        if (rank == 1) extents[0] = r.n;  // a factored FWHT reports its one axis
         else std::copy(r.extents.begin(), r.extents.end(), extents);
     });
 }

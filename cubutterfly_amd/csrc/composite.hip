@@ -225,7 +225,8 @@ class CompositeExecutor final : public Executor {
         }
         std::string joined;
         for (std::size_t i = 0; i < names.size(); ++i) joined += (i ? "," : "") + names[i];
-        algorithm = std::string(rank == 1      ? "zero-extended"
+        algorithm = std::string(r.factored     ? "fwht-factored"
+                                : rank == 1    ? "zero-extended"
                                 : transposing_ ? "rank2-transposing"
                                 : flatten      ? (rank == 2 ? "rank2-kronecker" : "rankN-kronecker")
                                                : (rank == 2 ? "rank2-transpose" : "rankN-composite")) +
@@ -327,6 +328,7 @@ class CompositeExecutor final : public Executor {
         c.in_reversed.clear();
         c.out_reversed.clear();
         c.embedding = false;
+        c.factored = false;
         c.in_extents.clear();
         c.out_extents.clear();
         c.n = n;
@@ -400,8 +402,9 @@ class CompositeExecutor final : public Executor {
 }  // namespace
 
 std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel) {
-    require(r.rank >= 1 && r.rank <= kMaxRank && r.extents.size() == r.rank && (r.rank >= 2 || r.embedding),
-            "composite plans need rank 2 to 8 or the zero-extended embedding");
+    require(r.rank >= 1 && r.rank <= kMaxRank && r.extents.size() == r.rank &&
+                (r.rank >= 2 || r.embedding || r.factored),
+            "composite plans need rank 2 to 8, the zero-extended embedding or a factored FWHT");
     // A flattened FWHT is one rank-1 plan; it exists up to the resident length.
     const bool flatten = r.op == Op::Fwht && !(r.inverse && r.normalize) && r.log_n <= 13;
     return std::make_unique<CompositeExecutor>(r, flatten, sel);

@@ -95,13 +95,16 @@ struct Request {
     // the forward input and the inverse output).
     bool embedding = false;
     std::vector<std::uint64_t> in_extents, out_extents;
+    // A rank-1 FWHT longer than one resident tile, factored into axes of at
+    // most 2^12 points (rank and the vectors above describe the factors).
+    bool factored = false;
     std::size_t data_bytes() const { return static_cast<std::size_t>(n * batch) * element_bytes; }
     // Bytes a side spans: the sum over axes of (extent - 1) stride, plus
     // (batch - 1) batch stride, plus one element.
     std::size_t span_bytes(bool input) const {
         const std::uint64_t bs = input ? in_batch_stride : out_batch_stride;
         std::uint64_t last = (batch - 1) * bs;
-        if (extents.empty()) {
+        if (extents.empty() || factored) {
             last += (n - 1) * (input ? in_stride : out_stride);
         } else {
             const auto& strides = input ? in_strides : out_strides;

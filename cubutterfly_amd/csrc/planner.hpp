@@ -51,7 +51,7 @@ std::unique_ptr<Executor> make_boundary_executor(const Request& r, Selection* se
 std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel);
 
 inline std::unique_ptr<Executor> plan_executor(const Request& r, Selection* sel = nullptr) {
-    if (r.rank > 1 || r.embedding) return make_composite_executor(r, sel);
+    if (r.rank > 1 || r.embedding || r.factored) return make_composite_executor(r, sel);
     if (r.boundary) return make_boundary_executor(r, sel);
     return select_leaf(r, sel);
 }

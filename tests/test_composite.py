@@ -168,3 +168,21 @@ def test_fwht_composition_is_the_flat_transform():
     # axis order is what fixes the bits.
     other = along(along(x, 1, oracle.fwht_f32), 2, oracle.fwht_f32)
     assert not np.array_equal(other.view(np.uint32), flat.view(np.uint32))
+
+
+def test_long_fwht_is_factored(lib):
+    # FWHT beyond 2^13 points: axes of at most 2^12, lowest bits innermost.
+    t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
+                     extents=[1 << 20], batch=2)
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name().startswith("fwht-factored[fwht-fp32-resident-r16,")
+        assert plan.physical_extents() == [1 << 20]
+        assert plan.input_size() == plan.output_size() == 2 * (1 << 20) * 4
+        m = json.loads(plan.mapping_json())
+        assert m["extents"] == [256, 4096]
+        assert [s["axis"] for s in m["schedule"] if s["step"] == "axis"] == [1, 0]
+    fp16 = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
+                        output_rounding=cb.OutputRounding.FINAL_STORAGE, extents=[1 << 14])
+    with pytest.raises(cb.Error) as e:
+        cb.Plan(lib, fp16)
+    assert e.value.status == cb.Status.NOT_SUPPORTED
