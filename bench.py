@@ -62,6 +62,14 @@ class Workload:
     def kernel_name(self):
         return self.plans[0].algorithm_name()
 
+    # --mapping: a lowering name to plan with the EXPLICIT policy, for the
+    # workloads whose setup honours it (one plan per call).
+    mapping = None
+    takes_mapping = False
+
+    def plan_options(self, cb):
+        return cb.PlanOptions(policy=cb.AlgorithmPolicy.EXPLICIT, mapping=self.mapping) if self.mapping else None
+
     def _rotation(self, torch, bytes_per_set):
         return max(3, -(-2 * MALL_BYTES // max(1, bytes_per_set)))
 
@@ -69,6 +77,7 @@ class Workload:
 class FwhtFp32(Workload):
     name = "c1"
     dtype = "f32"
+    takes_mapping = True
     description = "FWHT fp32 unnormalized forward, batch 4096 x n=4096, integer inputs in [-8,8]"
 
     def __init__(self, log_n=12, batch=4096):
@@ -81,7 +90,7 @@ class FwhtFp32(Workload):
         from cubutterfly_amd import workloads
         t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
                          extents=[1 << self.log_n], batch=self.batch)
-        self.plans = [cb.Plan(lib, t, stream=stream)]
+        self.plans = [cb.Plan(lib, t, options=self.plan_options(cb), stream=stream)]
         host = workloads.fwht_integer_input(self.log_n, self.batch, seed=1)
         self.host = host
         sets = self._rotation(torch, self.bytes_per_call)
@@ -125,7 +134,7 @@ class FwhtFp32Pitched(FwhtFp32):
         t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
                          extents=[n], batch=self.batch, input_strides=[1], input_batch_stride=pitch,
                          output_strides=[1], output_batch_stride=pitch)
-        plan = cb.Plan(lib, t, stream=stream)
+        plan = cb.Plan(lib, t, options=self.plan_options(cb), stream=stream)
         ws = plan.workspace_size()
         if ws:
             self.workspace = torch.empty(ws, dtype=torch.uint8, device="cuda")
@@ -151,7 +160,9 @@ class FwhtFp32Pitched(FwhtFp32):
 
     def kernel_name(self):
         name = self.plans[0].algorithm_name()
-        return ("fwht_pitched_kernel" if name.endswith("-pitched") else "fwht_resident_kernel (inside " + name + ")")
+        kernel = ("fwht_wide_kernel" if "-r32" in name else
+                  "fwht_pitched_kernel" if name.endswith("-pitched") else "fwht_resident_kernel")
+        return kernel + " (inside " + name + ")"
 
 
 # VALU instructions per radix-2 butterfly of the NTT pass kernels, all work
@@ -307,9 +318,11 @@ class OnePlan(Workload):
     def make_host(self):
         raise NotImplementedError
 
+    takes_mapping = True
+
     def setup(self, torch, lib, stream):
         import cubutterfly_amd as cb
-        self.plans = [cb.Plan(lib, self.transform(cb), stream=stream)]
+        self.plans = [cb.Plan(lib, self.transform(cb), options=self.plan_options(cb), stream=stream)]
         ws_bytes = self.plans[0].workspace_size()
         if ws_bytes:
             self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
@@ -524,6 +537,8 @@ def main():
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--verify", action="store_true", help="check one output against the oracle")
     parser.add_argument("--eager", action="store_true", help="time eager submissions instead of graph replays")
+    parser.add_argument("--mapping", default=None,
+                        help="plan one-plan workloads with this lowering (EXPLICIT policy) instead of the default")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the butterfly path is single-GPU (every configuration "
@@ -538,6 +553,11 @@ def main():
     lib = cb.Library()
     stream = torch.cuda.Stream()  # default priority; plans launch on it
     workload = WORKLOADS[args.workload]()
+    if args.mapping:
+        if not workload.takes_mapping:
+            print(f"--mapping applies to one-plan workloads; {args.workload} is not one", file=sys.stderr)
+            sys.exit(2)
+        workload.mapping = args.mapping
     workload.setup(torch, lib, stream.cuda_stream)
     torch.cuda.synchronize()
 

@@ -406,6 +406,212 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_pitched_kernel(const typ
     }
 }
 
+// ---- 32 registers per thread, one row per tile (2^11 .. 2^13 points) -------
+//
+// Thread t holds 32 elements. Phase 0 butterflies element bits 0-4 (t's 32
+// consecutive elements), phase 1 bits 5-9, phase 2 bits 10 .. log n - 1. The
+// registers of phase 2 also carry element bits 0 .. P-1 (P = 15 - log n)
+// without butterflying them, so each thread ends with 2^(5-P) runs of 2^P
+// consecutive results and stores each run as one 8- to 64-byte vector: no
+// 2-byte scatter at the end, and still two LDS exchanges. Same stages in the
+// same order as the 16-register kernel, so results are bit-identical.
+// LDS image: one pad word per 32 (addr = i + i/32), which leaves every
+// 32-lane group of all four exchange accesses on 32 distinct banks (checked
+// by enumeration for log n = 11, 12, 13), with per-thread bases and
+// compile-time register offsets.
+constexpr int kLW = 5;
+constexpr int kW = 1 << kLW;
+
+__device__ __forceinline__ unsigned wide_lds_addr(unsigned i) { return i + (i >> kLW); }
+
+template <int LOG_N>
+struct WideMap {
+    static constexpr int kP = kLW - (LOG_N - 10);  // passenger bits of phase 2
+    static __device__ __forceinline__ unsigned i0(unsigned t, unsigned r) { return (t << kLW) | r; }
+    static __device__ __forceinline__ unsigned i1(unsigned t, unsigned r) {
+        return (t & 31u) | (r << 5) | ((t >> 5) << 10);
+    }
+    static __device__ __forceinline__ unsigned i2(unsigned t, unsigned r) {
+        return (r & ((1u << kP) - 1u)) | (t << kP) | ((r >> kP) << 10);
+    }
+};
+
+// Radix-2 stages on register bits [LO, HI), lowest first.
+template <int LO, int HI>
+__device__ __forceinline__ void wide_stages(float (&v)[kW]) {
+#pragma unroll
+    for (int j = LO; j < HI; ++j) {
+        const int d = 1 << j;
+#pragma unroll
+        for (int r = 0; r < kW; ++r) {
+            if ((r & d) == 0) {
+                const float a = v[r];
+                const float b = v[r + d];
+                v[r] = a + b;
+                v[r + d] = a - b;
+            }
+        }
+    }
+}
+
+// A tile's 32 elements per thread as raw 32-bit words (fp16 pairs stay
+// packed until the tile is processed, so the prefetch buffer is 16 words).
+template <class Io>
+constexpr int wide_words() {
+    return kW * int(sizeof(typename Io::T)) / 4;
+}
+
+template <class Io>
+__device__ __forceinline__ void wide_load(__amdgpu_buffer_rsrc_t r, unsigned off, unsigned (&w)[wide_words<Io>()]) {
+#pragma unroll
+    for (int k = 0; k < wide_words<Io>() / 4; ++k) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off + 16u * k), 0, 0);
+        w[4 * k + 0] = x[0];
+        w[4 * k + 1] = x[1];
+        w[4 * k + 2] = x[2];
+        w[4 * k + 3] = x[3];
+    }
+}
+
+template <class Io>
+__device__ __forceinline__ void wide_unpack(const unsigned (&w)[wide_words<Io>()], float (&v)[kW]) {
+#pragma unroll
+    for (int r = 0; r < kW; ++r) {
+        if constexpr (sizeof(typename Io::T) == 4) {
+            v[r] = __uint_as_float(w[r]);
+        } else {
+            v[r] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[r >> 1] >> (16 * (r & 1)))));
+        }
+    }
+}
+
+// Stores `run` consecutive results (run * sizeof(T) bytes: 8, 16, 32 or 64)
+// at byte offset `off` of the tile's output buffer.
+template <class Io, int RUN>
+__device__ __forceinline__ void wide_store_run(__amdgpu_buffer_rsrc_t r, unsigned off, const float* x) {
+    constexpr int kWords = RUN * int(sizeof(typename Io::T)) / 4;
+    unsigned w[kWords];
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) {
+        if constexpr (sizeof(typename Io::T) == 4) {
+            w[k] = __float_as_uint(x[k]);
+        } else {
+            const unsigned lo = __half_as_ushort(__float2half_rn(x[2 * k]));
+            const unsigned hi = __half_as_ushort(__float2half_rn(x[2 * k + 1]));
+            w[k] = lo | (hi << 16);
+        }
+    }
+    using V4 = __attribute__((ext_vector_type(4))) unsigned;
+    using V2 = __attribute__((ext_vector_type(2))) unsigned;
+    if constexpr (kWords == 2) {
+        __builtin_amdgcn_raw_buffer_store_b64(V2{w[0], w[1]}, r, static_cast<int>(off), 0, 0);
+    } else {
+#pragma unroll
+        for (int k = 0; k < kWords / 4; ++k)
+            __builtin_amdgcn_raw_buffer_store_b128(V4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]}, r,
+                                                   static_cast<int>(off + 16u * k), 0, 0);
+    }
+}
+
+// One row per tile, rows at input + k * in_pitch / output + k * out_pitch
+// (elements; packed rows have pitch n). Tiles blockIdx.x, + gridDim.x, ...;
+// WALK: the next tile's loads are issued before the current tile's
+// butterflies (for grids smaller than the row count); without it each tile
+// is loaded when its turn comes, which needs no second register buffer.
+// FP16 storage only: with 32-bit words the two prefetch buffers and the
+// exchange registers exceed 128 VGPRs and spill.
+template <int LOG_N, class Io, bool WALK>
+__global__ __launch_bounds__(1 << (LOG_N - kLW), 4) void fwht_wide_kernel(const typename Io::T* __restrict__ input,
+                                                                      typename Io::T* output, unsigned rows,
+                                                                      std::uint64_t in_pitch,
+                                                                      std::uint64_t out_pitch, float norm,
+                                                                      float scale) {
+    static_assert(LOG_N >= 11 && LOG_N <= 13, "phase 2 covers 1 to 3 bits");
+    using T = typename Io::T;
+    using M = WideMap<LOG_N>;
+    constexpr unsigned kN = 1u << LOG_N;
+    constexpr unsigned kBytes = kN * unsigned(sizeof(T));
+    constexpr int kRun = 1 << M::kP;
+    __shared__ float lds[kN + (kN >> kLW)];
+    const unsigned t = threadIdx.x;
+    const unsigned grid = gridDim.x;
+    const unsigned in_off = t * kW * unsigned(sizeof(T));
+    const unsigned out_off = (t << M::kP) * unsigned(sizeof(T));
+    unsigned tile = blockIdx.x;
+
+    auto transform = [&](float (&v)[kW], unsigned row) {
+        wide_stages<0, kLW>(v);
+        lds_barrier();  // readers of the previous tile's image are done
+#pragma unroll
+        for (int r = 0; r < kW; ++r) lds[wide_lds_addr(M::i0(t, r))] = v[r];
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < kW; ++r) v[r] = lds[wide_lds_addr(M::i1(t, r))];
+        wide_stages<0, kLW>(v);
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < kW; ++r) lds[wide_lds_addr(M::i1(t, r))] = v[r];
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < kW; ++r) v[r] = lds[wide_lds_addr(M::i2(t, r))];
+        wide_stages<M::kP, kLW>(v);
+#pragma unroll
+        for (int r = 0; r < kW; ++r) {
+            v[r] = (v[r] * norm) * scale;
+            opaque(v[r]);
+        }
+        const __amdgpu_buffer_rsrc_t dst = make_rsrc(output + std::uint64_t(row) * out_pitch, kBytes);
+#pragma unroll
+        for (int g = 0; g < kW / kRun; ++g)
+            wide_store_run<Io, kRun>(dst, out_off + (unsigned(g) << 10) * unsigned(sizeof(T)), v + g * kRun);
+    };
+    auto load = [&](unsigned row, bool valid, unsigned (&w)[wide_words<Io>()]) {
+        wide_load<Io>(make_rsrc(input + std::uint64_t(row) * in_pitch, valid ? kBytes : 0u), in_off, w);
+    };
+    // Two raw buffers in turn, the prefetch issued unconditionally (an empty
+    // range past the last tile), as in the 16-register kernel.
+    auto step = [&](unsigned (&cur)[wide_words<Io>()], unsigned (&nxt)[wide_words<Io>()]) -> bool {
+        const unsigned following = tile + grid;
+        const bool more = following < rows;
+        load(following, more, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        float v[kW];
+        wide_unpack<Io>(cur, v);
+        transform(v, tile);
+        // `cur` stays allocated through the stores (see the 16-register kernel).
+#pragma unroll
+        for (int k = 0; k < wide_words<Io>(); ++k) asm volatile("" : "+v"(cur[k]));
+        tile = following;
+        return more;
+    };
+    if constexpr (WALK) {
+        if (tile < rows) {
+            unsigned a[wide_words<Io>()], b[wide_words<Io>()];
+            load(tile, true, a);
+            for (;;) {
+                if (!step(a, b)) break;
+                if (!step(b, a)) break;
+            }
+        }
+    } else {
+        for (; tile < rows; tile += grid) {
+            unsigned w[wide_words<Io>()];
+            load(tile, true, w);
+            float v[kW];
+            wide_unpack<Io>(w, v);
+            transform(v, tile);
+        }
+    }
+}
+
+template <int LOG_N, class Io, bool WALK>
+void launch_wide(const void* in, void* out, std::uint64_t rows, std::uint64_t in_pitch, std::uint64_t out_pitch,
+                 float norm, float scale, unsigned grid, hipStream_t stream) {
+    hipLaunchKernelGGL((fwht_wide_kernel<LOG_N, Io, WALK>), dim3(grid), dim3(1u << (LOG_N - kLW)), 0, stream,
+                       static_cast<const typename Io::T*>(in), static_cast<typename Io::T*>(out),
+                       static_cast<unsigned>(rows), in_pitch, out_pitch, norm, scale);
+}
+
 using Launch = void (*)(const void*, void*, std::uint64_t, float, float, unsigned, hipStream_t);
 
 template <int LOG_N, class Io>
@@ -463,31 +669,72 @@ PitchedLaunch pitched_launcher(int log_n) {
     return pitched_table_entry<Io>(log_n, std::make_integer_sequence<int, kMaxResidentLog - kLE + 1>{});
 }
 
+// Workgroups of the walking 32-register kernel resident on the device at once.
+template <int LOG_N, class Io>
+unsigned wide_resident() {
+    static const unsigned resident = [] {
+        int per_cu = 0;
+        const void* fn = reinterpret_cast<const void*>(&fwht_wide_kernel<LOG_N, Io, true>);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 1 << (LOG_N - kLW), 0) != hipSuccess ||
+            per_cu < 1)
+            per_cu = 1;
+        return unsigned(per_cu) * unsigned(device_cu_count());
+    }();
+    return resident;
+}
+
+struct WideLaunch {
+    PitchedLaunch launch = nullptr;  // one tile per workgroup's turn
+    PitchedLaunch walk = nullptr;    // with next-tile prefetch
+    unsigned (*resident)() = nullptr;
+    explicit operator bool() const { return launch != nullptr; }
+};
+
+template <int... L>
+WideLaunch wide_table_entry(int log_n, std::integer_sequence<int, L...>) {
+    WideLaunch table[] = {WideLaunch{launch_wide<L + 11, F16Io, false>, launch_wide<L + 11, F16Io, true>,
+                                     wide_resident<L + 11, F16Io>}...};
+    return table[log_n - 11];
+}
+
+// The 32-register kernel: FP16 rows of 2^11 .. 2^13 points, row count within 32 bits.
+WideLaunch wide_launcher(const Request& r) {
+    if (!r.fp16_final || r.log_n < 11 || r.log_n > 13 || r.batch > 0xffffffffull) return {};
+    return wide_table_entry(int(r.log_n), std::make_integer_sequence<int, 3>{});
+}
+
 class FwhtExecutor final : public Executor {
   public:
-    FwhtExecutor(const Request& r, Launch launch, PitchedLaunch pitched)
-        : r_(r), launch_(launch), pitched_(pitched) {
+    // `wide`: the 32-register kernel (packed or pitched rows) in place of
+    // the 16-register ones; `persistent`: its grid sized to the resident
+    // workgroups, each walking rows with next-row prefetch.
+    FwhtExecutor(const Request& r, Launch launch, PitchedLaunch pitched, WideLaunch wide, bool persistent)
+        : r_(r), launch_(launch), pitched_(pitched), wide_(persistent ? wide.walk : wide.launch) {
         norm_ = r.normalize ? 1.0f / static_cast<float>(r.n) : 1.0f;
         scale_ = r.fp16_final ? r.output_scale : 1.0f;
-        const int lb = r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
+        const int lb = wide_ ? static_cast<int>(r.log_n) : r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
         const std::uint64_t total = r.n * r.batch;
         const std::uint64_t rows_per_tile = std::uint64_t{1} << (lb - int(r.log_n));
         const std::uint64_t tiles =
-            pitched_ ? (r.batch + rows_per_tile - 1) / rows_per_tile : (total + (1ull << lb) - 1) >> lb;
+            pitched_ || wide_ ? (r.batch + rows_per_tile - 1) / rows_per_tile : (total + (1ull << lb) - 1) >> lb;
         require(tiles <= 0xffffffffull, "FWHT batch exceeds the tile index range");
         // Grid: one workgroup per tile (measured at least as fast as a
         // persistent, occupancy-sized grid for every BASELINE shape once the
         // kernel's prefetch overlapped), capped at the launch limit; the
         // kernel walks any tiles beyond the grid with next-tile prefetch.
-        const unsigned threads = 1u << (lb - kLE);
-        const std::uint64_t lds = ((1u << lb) + ((1u << lb) >> kLE)) * 4ull;
+        const int regs_log = wide_ ? kLW : kLE;
+        const unsigned threads = 1u << (lb - regs_log);
+        const std::uint64_t lds = ((1u << lb) + ((1u << lb) >> regs_log)) * 4ull;
         grid_ = static_cast<unsigned>(std::min<std::uint64_t>(tiles, 0x7fffffffull));
-        algorithm = std::string(r.fp16_final ? "fwht-fp16-fp32-resident-r16" : "fwht-fp32-resident-r16") +
-                    (pitched_ ? "-pitched" : "");
-        reason = "whole rows resident in one workgroup (" + std::to_string(threads) +
-                 " threads x 16 registers, padded LDS exchange)" +
-                 std::string(grid_ < tiles ? ", persistent grid with next-tile prefetch" : "") +
-                 "; stage order bits 0..log n-1";
+        if (wide_ && persistent) grid_ = std::min(grid_, wide.resident());
+        algorithm = name(r, wide_ != nullptr, wide_ && persistent);
+        reason = wide_ ? "one row per workgroup (" + std::to_string(threads) +
+                             " threads x 32 registers, phases of bits 0-4, 5-9 and 10+, the last carrying the low "
+                             "element bits so results leave as 8- to 64-byte vectors)"
+                       : "whole rows resident in one workgroup (" + std::to_string(threads) +
+                             " threads x 16 registers, padded LDS exchange)";
+        reason += std::string(grid_ < tiles ? ", persistent grid with next-tile prefetch" : "") +
+                  "; stage order bits 0..log n-1";
         json::Writer w;
         w.begin_object()
             .field("schema_version", 1u)
@@ -499,16 +746,23 @@ class FwhtExecutor final : public Executor {
             .field("tiles", tiles)
             .field("grid", grid_)
             .field("threads_per_block", threads)
-            .field("registers_per_thread", unsigned(kE))
-            .field("phases", unsigned((r.log_n + kLE - 1) / kLE))
+            .field("registers_per_thread", 1u << regs_log)
+            .field("phases", wide_ ? 3u : unsigned((r.log_n + kLE - 1) / kLE))
             .field("lds_bytes", lds)
             .field("input_pitch", pitched_ ? r.in_batch_stride : r.n)
             .field("output_pitch", pitched_ ? r.out_batch_stride : r.n)
             .end_object();
         mapping_json = w.str();
     }
+    static std::string name(const Request& r, bool wide, bool persistent = false) {
+        return std::string(r.fp16_final ? "fwht-fp16-fp32-resident-r" : "fwht-fp32-resident-r") +
+               (wide ? "32" : "16") + (persistent ? "-persistent" : "") + (r.pitched ? "-pitched" : "");
+    }
     void execute(const void* in, void* out, void*, hipStream_t stream) override {
-        if (pitched_)
+        if (wide_)
+            wide_(in, out, r_.batch, pitched_ ? r_.in_batch_stride : r_.n, pitched_ ? r_.out_batch_stride : r_.n,
+                  norm_, scale_, grid_, stream);
+        else if (pitched_)
             pitched_(in, out, r_.batch, r_.in_batch_stride, r_.out_batch_stride, norm_, scale_, grid_, stream);
         else
             launch_(in, out, r_.n * r_.batch, norm_, scale_, grid_, stream);
@@ -519,6 +773,7 @@ class FwhtExecutor final : public Executor {
     Request r_;
     Launch launch_;
     PitchedLaunch pitched_;
+    PitchedLaunch wide_;
     float norm_ = 1.0f, scale_ = 1.0f;
     unsigned grid_ = 1;
 };
@@ -536,16 +791,33 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
         pitched = r.fp16_final ? pitched_launcher<F16Io>(r.log_n) : pitched_launcher<F32Io>(r.log_n);
         require(pitched != nullptr, "pitched FWHT rows need n >= 16");
     }
-    auto e = std::make_unique<FwhtExecutor>(r, launch, pitched);
-    supported(r.variant.empty() || r.variant == e->algorithm,
-              "'" + r.variant + "' is not a lowering of this FWHT (available: " + e->algorithm + ")");
-    return e;
+    const WideLaunch wide = wide_launcher(r);
+    // Default: the 32-register kernel where it measured faster (FP16 rows of
+    // 2^12 points: 55.7-56.6 us against 56.4-58.5 us for 16384 rows); other
+    // lengths keep the 16-register kernel unless MEASURE picks it.
+    const bool wide_default = wide && r.log_n == 12;
+    const bool one_per_row =
+        wide && (r.variant.empty() ? wide_default : r.variant == FwhtExecutor::name(r, true));
+    const bool persistent = wide && r.variant == FwhtExecutor::name(r, true, true);
+    std::string available = FwhtExecutor::name(r, false);
+    if (wide) available += ", " + FwhtExecutor::name(r, true) + ", " + FwhtExecutor::name(r, true, true);
+    supported(r.variant.empty() || one_per_row || persistent || r.variant == FwhtExecutor::name(r, false),
+              "'" + r.variant + "' is not a lowering of this FWHT (available: " + available + ")");
+    return std::make_unique<FwhtExecutor>(r, launch, pitched, one_per_row || persistent ? wide : WideLaunch{},
+                                          persistent);
 }
 
 std::vector<std::string> fwht_candidates(const Request& r) {
     Request v = r;
     v.variant.clear();
-    return {make_fwht_executor(v)->algorithm};
+    make_fwht_executor(v);  // the default lowering exists (throws NotSupported otherwise)
+    std::vector<std::string> names = {FwhtExecutor::name(r, false)};
+    if (wide_launcher(r)) {
+        names.push_back(FwhtExecutor::name(r, true));
+        names.push_back(FwhtExecutor::name(r, true, true));
+        if (r.log_n == 12) std::swap(names[0], names[1]);  // the default first
+    }
+    return names;
 }
 
 }  // namespace cbw

@@ -61,6 +61,18 @@ def test_fp16_final_storage_plan(lib):
         assert plan.algorithm_name() == "fwht-fp16-fp32-resident-r16"
 
 
+def test_fp16_4096_point_rows_default_to_32_registers(lib):
+    # C5a's shape: one 2^12-point row per workgroup of 128 threads x 32 registers.
+    t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
+                     extents=[4096], batch=16384, output_scale=1 / 64,
+                     output_rounding=cb.OutputRounding.FINAL_STORAGE)
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name() == "fwht-fp16-fp32-resident-r32"
+        mapping = json.loads(plan.mapping_json())
+        assert mapping["threads_per_block"] == 128 and mapping["registers_per_thread"] == 32
+        assert mapping["tiles"] == mapping["grid"] == 16384 and mapping["phases"] == 3
+
+
 def status_of(fn, *args):
     try:
         fn(*args)

@@ -61,7 +61,8 @@ def test_fp32(torch_gpu, lib, stream, log_n, batch):
 def test_fp16_final(torch_gpu, lib, stream, log_n):
     n = 1 << log_n
     name = run(torch_gpu, lib, stream, n, 45, n + 24, n + 8, fp16=True, seed=log_n)
-    assert name == "fwht-fp16-fp32-resident-r16-pitched"
+    # 2^12-point FP16 rows default to the 32-register kernel.
+    assert name == ("fwht-fp16-fp32-resident-r32-pitched" if log_n == 12 else "fwht-fp16-fp32-resident-r16-pitched")
 
 
 def test_inverse_normalised(torch_gpu, lib, stream):
