@@ -182,6 +182,8 @@ class NttNegacyclic(Workload):
                    "one step = forward then inverse of the batch")
 
     valu_per_butterfly = 8.6
+    takes_mapping = True  # both plans (the lowering names do not depend on the direction)
+
     def __init__(self, log_n=16, batch=64):
         from cubutterfly_amd import workloads
         self.log_n, self.batch, self.q = log_n, batch, workloads.C2_MODULUS
@@ -197,7 +199,7 @@ class NttNegacyclic(Workload):
             t = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
                              extents=[1 << self.log_n], batch=self.batch, modulus=self.q, word_bits=32,
                              inverse=inverse, ring=cb.NttRing.NEGACYCLIC)
-            return cb.Plan(lib, t, stream=stream)
+            return cb.Plan(lib, t, options=self.plan_options(cb), stream=stream)
 
         self.plans = [plan(False), plan(True)]
         ws_bytes = max(p.workspace_size() for p in self.plans)

@@ -173,7 +173,8 @@ struct EngineImplT {
             supported(log_n <= 20, "NTT lengths above 2^20 are not yet lowered for gfx950");
             l1 = std::uint32_t(split_l1(int(log_n)));
             l2 = log_n - l1;
-            const int col_li = kColLines;
+            require(!c.wide_columns || sizeof(W) == 4, "32-column tiles are a u32 lowering");
+            const int col_li = c.wide_columns ? kWideColLines : kColLines;
             const int rli = row_lines(int(l1), int(l2));
             const std::uint64_t col_tiles = polys << (l2 - col_li);
             const std::uint64_t row_tiles = polys << (l1 - rli);
@@ -293,7 +294,8 @@ NttEngine::NttEngine(const NttEngineConfig& c) : impl_(new Impl) {
         impl_->u64 = std::make_unique<EngineImplT<std::uint64_t>>(c);
     const bool two = passes() == 2;
     algorithm_ = std::string("ntt-u") + std::to_string(c.word_bits) + (c.negacyclic ? "-negacyclic" : "-cyclic") +
-                 (two ? "-two-pass-r16" : "-resident-r16") + (c.force_strict ? "-strict" : "");
+                 (two ? "-two-pass-r16" : "-resident-r16") + (c.force_strict ? "-strict" : "") +
+                 (two && c.wide_columns ? "-c32" : "");
     json::Writer w;
     w.begin_object()
         .field("schema_version", 1u)
@@ -335,6 +337,16 @@ void NttEngine::execute(const void* in, void* out, void* ws, hipStream_t stream)
 
 namespace {
 
+std::string join(const std::vector<std::string>& names) {
+    std::string out;
+    for (const auto& n : names) out += (out.empty() ? "" : ", ") + n;
+    return out;
+}
+
+// 32-column tiles are the static choice where they measured faster: u32
+// 2^16-point transforms (C2 step 43.9-44.7 us against 44.9-45.3 us).
+bool wide_columns_default(const Request& r) { return r.word_bits == 32 && r.log_n == 16; }
+
 // Name of the static model's lowering: resident up to 2^12, then two passes.
 std::string default_name(const Request& r) {
     return "ntt-u" + std::to_string(r.word_bits) + (r.negacyclic ? "-negacyclic" : "-cyclic") +
@@ -375,10 +387,11 @@ class NttExecutor final : public Executor {
                 c.polynomials.push_back({0u, b * r.in_batch_stride, b * r.out_batch_stride});
         }
         const std::string suffix = r.pitched ? "-pitched" : "";
-        c.force_strict = !r.variant.empty() && r.variant == default_name(r) + "-strict" + suffix;
-        supported(r.variant.empty() || c.force_strict || r.variant == default_name(r) + suffix,
-                  "'" + r.variant + "' is not a lowering of this NTT (available: " + default_name(r) + suffix +
-                      ", " + default_name(r) + "-strict" + suffix + ")");
+        const std::vector<std::string> names = ntt_candidates(r);
+        supported(r.variant.empty() || std::find(names.begin(), names.end(), r.variant) != names.end(),
+                  "'" + r.variant + "' is not a lowering of this NTT (available: " + join(names) + ")");
+        c.force_strict = r.variant == default_name(r) + "-strict" + suffix;
+        c.wide_columns = r.variant.empty() ? wide_columns_default(r) : r.variant == default_name(r) + "-c32" + suffix;
         engine_ = std::make_unique<NttEngine>(c);
         algorithm = engine_->algorithm() + (r.pitched ? "-pitched" : "");
         mapping_json = engine_->mapping_json();
@@ -402,10 +415,16 @@ std::unique_ptr<Executor> make_ntt_executor(const Request& r) { return std::make
 
 // Lazy reduction (values in [0, 2q) / [0, 4q) between stages) where the
 // modulus leaves two spare bits, and the fully reduced butterflies.
+// u32 two-pass transforms also offer 32-column tiles in the column pass
+// (`-c32`: 128-byte row segments instead of 64).
 std::vector<std::string> ntt_candidates(const Request& r) {
     const std::string suffix = r.pitched ? "-pitched" : "";
     std::vector<std::string> names{default_name(r) + suffix};
     if (r.modulus < (std::uint64_t{1} << (r.word_bits - 2))) names.push_back(default_name(r) + "-strict" + suffix);
+    if (r.word_bits == 32 && r.log_n >= 13 && r.log_n <= 20) {
+        names.push_back(default_name(r) + "-c32" + suffix);
+        if (wide_columns_default(r)) std::rotate(names.begin(), names.end() - 1, names.end());  // the default first
+    }
     return names;
 }
 

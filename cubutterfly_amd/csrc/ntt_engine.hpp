@@ -44,6 +44,7 @@ struct NttEngineConfig {
     bool output_bit_reversed = false;
     bool reduce_input = true;  // reduce arbitrary words mod q on load
     bool force_strict = false; // fully reduced butterflies even where lazy ones fit
+    bool wide_columns = false; // u32 two-pass: 32-column tiles in the column pass (`-c32`)
     std::vector<NttDomain> domains;
     std::vector<NttPolynomial> polynomials;  // empty: `batch` dense rows of domain 0
     std::uint64_t batch = 0;

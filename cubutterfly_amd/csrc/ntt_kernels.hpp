@@ -297,7 +297,7 @@ struct Pass {
     // the L2 would otherwise merge).
     static constexpr int kStoreAux = (!CT && !SINGLE) ? 17 : 0;
     static_assert(SINGLE ? (L1 == 0 && L2 == LT) : (COL ? LT == L1 : LT == L2), "pass bits");
-    static_assert(LT >= 1 && LB >= kLE && LB <= 12, "tile shape");
+    static_assert(LT >= 1 && LB >= kLE && LB <= 13, "tile shape");
 
     template <int P>
     static constexpr int tile_window() {
@@ -722,6 +722,9 @@ void add_single() {
 constexpr int split_l1(int log_n) { return log_n / 2 < 8 ? log_n / 2 : 8; }
 constexpr int kTileLog = 12;
 constexpr int kColLines = 4;
+// u32 column tiles may also hold 32 columns (128-byte row segments, 2^(l1+5)
+// words, up to 512 threads): the `-c32` lowering.
+constexpr int kWideColLines = 5;
 constexpr int row_lines(int l1, int l2) { return l1 < kTileLog - l2 ? l1 : kTileLog - l2; }
 
 template <class W, bool LAZY, int LOG_N>
@@ -730,6 +733,10 @@ void add_two_pass() {
     constexpr int rli = row_lines(l1, l2);
     add_variants<W, LAZY, l1, kColLines, true, true, false, l1, l2>();
     add_variants<W, LAZY, l1, kColLines, true, false, false, l1, l2>();
+    if constexpr (sizeof(W) == 4 && l1 + kWideColLines <= 13 && l2 >= kWideColLines) {
+        add_variants<W, LAZY, l1, kWideColLines, true, true, false, l1, l2>();
+        add_variants<W, LAZY, l1, kWideColLines, true, false, false, l1, l2>();
+    }
     add_variants<W, LAZY, l2, rli, false, true, false, l1, l2>();
     add_variants<W, LAZY, l2, rli, false, false, false, l1, l2>();
 }

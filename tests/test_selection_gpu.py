@@ -107,7 +107,7 @@ def test_every_fft_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path
         fft_ok(torch_gpu, lib, t, stream, log_n, batch, inverse, options=opts)
 
 
-@pytest.mark.parametrize("log_n", [10, 14, 16])
+@pytest.mark.parametrize("log_n", [10, 13, 14, 16, 17])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_ntt_strict_candidate(torch_gpu, lib, stream, tmp_path, log_n, inverse):
     batch = 4
@@ -115,7 +115,13 @@ def test_ntt_strict_candidate(torch_gpu, lib, stream, tmp_path, log_n, inverse):
     with cb.Plan(lib, t, options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE), stream=stream,
                  cache_path=tmp_path / "c.tsv") as plan:
         names = measured(plan)
-    assert len(names) == 2 and names[1] == names[0] + "-strict"
+    # Lazy and strict; u32 two-pass lengths add 32-column tiles, the static
+    # choice (listed first) at 2^16.
+    base = "ntt-u32-negacyclic-" + ("two-pass-r16" if log_n > 12 else "resident-r16")
+    expected = [base, base + "-strict"] + ([base + "-c32"] if log_n >= 13 else [])
+    if log_n == 16:
+        expected = expected[-1:] + expected[:-1]
+    assert names == expected
     rng = np.random.default_rng(log_n)
     x = rng.integers(0, 1 << 32, (batch, 1 << log_n), dtype=np.uint64).astype(np.uint32)
     expected = oracle.ntt_negacyclic(x.astype(np.uint64) % Q30, Q30, inverse=inverse).astype(np.uint32)
