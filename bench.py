@@ -2,7 +2,7 @@
 """Headline benchmark of the MI355X butterfly path (one GPU).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c1p|c2|c3a|c3b|c4|c5a|c5b|r2|copy]
-                [--no-cpu] [--verify] [--eager]
+                [--no-cpu] [--verify] [--eager] [--mapping LOWERING]
 
 A step is one call of the hot path over one batch of the named BASELINE
 configuration, with inputs already resident in HBM. W untimed steps, then K
@@ -12,6 +12,8 @@ Cache cannot serve them. Rank 0 prints ONE JSON line with the driver's fields
 plus `roofline` (algorithmic bytes per call / measured call time vs 8 TB/s HBM)
 and `cpu_baseline` (the CPU oracle -- a restatement of the reference CPU path --
 timed on this host over a bounded sample of the same workload).
+--mapping plans the workload with the EXPLICIT policy and the named lowering
+(c1, c1p, c2 and the one-plan workloads), for comparing lowerings.
 """
 import argparse
 import json
