@@ -30,12 +30,20 @@ def fwht(n, batch, **kw):
                         extents=[n], batch=batch, **kw)
 
 
+def fwht16(n, batch):
+    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
+                        extents=[n], batch=batch, output_scale=n ** -0.5,
+                        output_rounding=cb.OutputRounding.FINAL_STORAGE)
+
+
 CASES = {
     "fft-one-pass": (fft(1 << 12, 16), np.complex64, 1 << 16),
     "fft-two-pass": (fft(1 << 16, 2), np.complex64, 1 << 17),
     "fft-three-pass": (fft(1 << 23, 1), np.complex64, 1 << 23),
     "ntt-one-pass": (ntt(1 << 10, 32), np.uint32, 1 << 15),
     "ntt-two-pass": (ntt(1 << 16, 4, inverse=True), np.uint32, 1 << 18),
+    "ntt-two-pass-forward": (ntt(1 << 16, 4), np.uint32, 1 << 18),
+    "fwht-fp16-wide": (fwht16(4096, 64), np.float16, 1 << 18),
     "fwht": (fwht(4096, 32), np.float32, 1 << 17),
     "fwht-pitched": (fwht(1024, 8, input_strides=[1], input_batch_stride=1040, output_strides=[1],
                           output_batch_stride=1040), np.float32, 7 * 1040 + 1024),
@@ -87,5 +95,5 @@ def test_replays_match_eager(torch_gpu, lib, case):
                 plan.execute(x, y)
             torch.cuda.synchronize()
             eager = to_host(torch, y, dtype)
-            bits = {4: np.uint32, 8: np.uint64}[np.dtype(dtype).itemsize] if np.dtype(dtype).kind != "c" else np.uint64
+            bits = {2: np.uint16, 4: np.uint32, 8: np.uint64}[np.dtype(dtype).itemsize] if np.dtype(dtype).kind != "c" else np.uint64
             np.testing.assert_array_equal(got.view(bits), eager.view(bits), err_msg=f"{case} replay {replay}")
