@@ -18,8 +18,10 @@
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <fstream>
 #include <limits>
+#include <vector>
 
 #include "json.hpp"
 
@@ -92,8 +94,10 @@ struct DeviceScratch {
     ~DeviceScratch() {
         if (ptr) (void)hipFree(ptr);
     }
+    DeviceScratch(DeviceScratch&& o) noexcept : ptr(o.ptr) { o.ptr = nullptr; }
     DeviceScratch(const DeviceScratch&) = delete;
     DeviceScratch& operator=(const DeviceScratch&) = delete;
+    DeviceScratch& operator=(DeviceScratch&&) = delete;
 };
 
 struct Event {
@@ -153,12 +157,20 @@ class SearchTrace {
 // Mean milliseconds of one execution: 3 untimed runs, then 20 between two
 // events on the selection stream (the reference's host-event-loop protocol,
 // warmup 3 / repeat 20).
-double time_executor(Executor& e, const void* in, void* out, void* ws, hipStream_t stream) {
+// Mean time of one execute over `sets` rotating input / output buffers
+// (in_place: the input buffers only).
+double time_executor(Executor& e, const std::vector<DeviceScratch>& in, const std::vector<DeviceScratch>& out,
+                     bool in_place, void* ws, hipStream_t stream) {
     constexpr int kWarmup = 3, kRepeat = 20;
-    for (int i = 0; i < kWarmup; ++i) e.execute(in, out, ws, stream);
+    const std::size_t sets = in.size();
+    auto run = [&](int i) {
+        const std::size_t k = std::size_t(i) % sets;
+        e.execute(in[k].ptr, in_place ? in[k].ptr : out[k].ptr, ws, stream);
+    };
+    for (int i = 0; i < kWarmup; ++i) run(i);
     Event start, stop;
     hip_check(hipEventRecord(start.e, stream), "MEASURE event record");
-    for (int i = 0; i < kRepeat; ++i) e.execute(in, out, ws, stream);
+    for (int i = 0; i < kRepeat; ++i) run(i);
     hip_check(hipEventRecord(stop.e, stream), "MEASURE event record");
     hip_check(hipEventSynchronize(stop.e), "MEASURE synchronize");
     float ms = 0.0f;
@@ -266,10 +278,20 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     hip_check(hipStreamIsCapturing(sel->stream, &capture), "MEASURE capture query");
     supported(capture == hipStreamCaptureStatusNone, "MEASURE cannot time candidates during stream capture");
+    // Buffer sets: transforms of 16 MiB or more rotate over enough sets
+    // (at most 8) that inputs and outputs together exceed twice the 256 MB
+    // Infinity Cache, so candidates are timed at HBM speed as in steady use
+    // over large data, not on cache-resident buffers.
+    const std::size_t bytes = r.data_bytes();
+    constexpr std::size_t kCacheBytes = std::size_t{256} << 20;
+    const std::size_t sets =
+        bytes >= (std::size_t{16} << 20) ? std::min<std::size_t>(8, (2 * kCacheBytes + 2 * bytes - 1) / (2 * bytes) + 1)
+                                         : 1;
     SearchTrace trace;
     const auto names = leaf_candidates(r);
     trace.event("inventory", "\"key\":" + json::quote(key) + ",\"candidate_count\":" + std::to_string(names.size()) +
-                                 ",\"timing_protocol\":\"event-loop\",\"warmup\":3,\"repeat\":20");
+                                 ",\"timing_protocol\":\"event-loop\",\"warmup\":3,\"repeat\":20,"
+                                 "\"buffer_sets\":" + std::to_string(sets));
     std::vector<std::unique_ptr<Executor>> built;
     std::size_t ws_bytes = 0;
     for (const auto& name : names) {
@@ -284,14 +306,20 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
         }
     }
     require(!built.empty(), "no candidate lowering to measure");
-    const std::size_t bytes = r.data_bytes();
-    DeviceScratch in(bytes), out(bytes), ws(ws_bytes);
-    hip_check(hipMemsetAsync(in.ptr, 0, bytes, sel->stream), "MEASURE input fill");
+    std::vector<DeviceScratch> in, out;
+    in.reserve(sets);
+    out.reserve(sets);
+    for (std::size_t k = 0; k < sets; ++k) {
+        in.emplace_back(bytes);
+        out.emplace_back(r.in_place ? 0 : bytes);
+        hip_check(hipMemsetAsync(in.back().ptr, 0, bytes, sel->stream), "MEASURE input fill");
+    }
+    DeviceScratch ws(ws_bytes);
     std::size_t best = 0;
     double best_ms = std::numeric_limits<double>::infinity();
     std::string results;
     for (std::size_t i = 0; i < built.size(); ++i) {
-        const double ms = time_executor(*built[i], in.ptr, r.in_place ? in.ptr : out.ptr, ws.ptr, sel->stream);
+        const double ms = time_executor(*built[i], in, out, r.in_place, ws.ptr, sel->stream);
         char text[64];
         std::snprintf(text, sizeof text, "=%.4f ms", ms);
         results += (i ? ", " : "") + built[i]->algorithm + text;

@@ -167,3 +167,18 @@ def test_plan_trace(torch_gpu, lib, stream, tmp_path, monkeypatch):
     results = [r for r in rows if r["phase"] == "result"]
     assert len(results) == rows[0]["candidate_count"] and all(r["kernel_ms"] > 0 for r in results)
     assert rows[-1]["algorithm"] == chosen
+
+
+def test_measure_rotates_large_buffers(torch_gpu, lib, stream, tmp_path, monkeypatch):
+    # Transforms of 16 MiB or more are timed over rotating buffer sets whose
+    # footprint exceeds twice the 256 MB Infinity Cache (C3b's 128 MiB: 3
+    # sets); small ones on one set.
+    import json
+    for log_n, batch, sets in ((16, 2, 1), (14, 1024, 3)):
+        trace = tmp_path / f"trace{log_n}.jsonl"
+        monkeypatch.setenv("CUBUTTERFLY_PLAN_TRACE", str(trace))
+        with cb.Plan(lib, fft(log_n, batch), options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE),
+                     stream=stream, cache_path=tmp_path / "c.tsv") as plan:
+            assert plan.selection_source() == cb.SelectionSource.RUNTIME_MEASURED
+        rows = [json.loads(line) for line in trace.read_text().splitlines()]
+        assert rows[0]["phase"] == "inventory" and rows[0]["buffer_sets"] == sets
