@@ -285,8 +285,7 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     const std::size_t bytes = r.data_bytes();
     constexpr std::size_t kCacheBytes = std::size_t{256} << 20;
     const std::size_t sets =
-        bytes >= (std::size_t{16} << 20) ? std::min<std::size_t>(8, (2 * kCacheBytes + 2 * bytes - 1) / (2 * bytes) + 1)
-                                         : 1;
+        bytes >= (std::size_t{16} << 20) ? std::min<std::size_t>(8, kCacheBytes / bytes + 1) : 1;  // sets x 2 bytes > 2 x cache
     SearchTrace trace;
     const auto names = leaf_candidates(r);
     trace.event("inventory", "\"key\":" + json::quote(key) + ",\"candidate_count\":" + std::to_string(names.size()) +
