@@ -278,10 +278,11 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     hip_check(hipStreamIsCapturing(sel->stream, &capture), "MEASURE capture query");
     supported(capture == hipStreamCaptureStatusNone, "MEASURE cannot time candidates during stream capture");
-    // Buffer sets: transforms of 16 MiB or more rotate over enough sets
-    // (at most 8) that inputs and outputs together exceed twice the 256 MB
-    // Infinity Cache, so candidates are timed at HBM speed as in steady use
-    // over large data, not on cache-resident buffers.
+    // Buffer sets: transforms of 16 MiB or more rotate over enough sets that
+    // inputs and outputs together exceed twice the 256 MB Infinity Cache (at
+    // most 8 sets, so below 32 MiB part of the data stays cached), so
+    // candidates are timed at HBM speed as in steady use over large data,
+    // not on cache-resident buffers.
     const std::size_t bytes = r.data_bytes();
     constexpr std::size_t kCacheBytes = std::size_t{256} << 20;
     const std::size_t sets =
