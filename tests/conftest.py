@@ -16,7 +16,7 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def lib():
     import cubutterfly_amd as cb
-    return cb.Library()
+    return cb.Native()
 
 
 @pytest.fixture(scope="session")

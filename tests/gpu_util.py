@@ -24,10 +24,10 @@ def to_host(torch, tensor, np_dtype):
     return out.view(np_dtype)
 
 
-def run_plan(torch, lib, transform, host_input, stream, in_place=False, options=None):
+def run_plan(torch, lib, transform, host_input, stream, in_place=False, **plan_args):
     """Execute `transform` on host_input through the C ABI; returns the host result."""
     x = to_device(torch, host_input)
-    with cb.Plan(lib, transform, options=options, stream=stream) as plan:
+    with cb.Plan(lib, transform, stream=stream, **plan_args) as plan:
         assert plan.input_size() == x.numel() * x.element_size()
         # Output shaped like the input when the sizes agree, else flat (the
         # zero-extended embedding changes the extents).

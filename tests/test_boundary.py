@@ -15,14 +15,13 @@ import cubutterfly_amd as cb
 def status_of(fn, *args):
     try:
         fn(*args)
-    except cb.Error as e:
+    except cb.AbiError as e:
         return e.status
     return 0
 
 
 def fwht(n=8, batch=2, **kw):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                        extents=[n], batch=batch, **kw)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
 def align16(b):
@@ -36,14 +35,14 @@ def test_strided_input_uses_the_boundary(lib):
         assert plan.input_size() == ((8 - 1) * 2 + (3 - 1) * 20 + 1) * 4
         assert plan.output_size() == 8 * 3 * 4
         assert plan.workspace_size() == 2 * align16(8 * 3 * 4)
-        m = json.loads(plan.mapping_json())
+        m = plan.mapping()
         assert m["kind"] == "semantic-boundary" and m["input_stride"] == 2 and m["input_batch_stride"] == 20
         assert m["child"]["operator"] == "fwht"
 
 
 def test_default_batch_stride_is_the_axis_span(lib):
     with cb.Plan(lib, fwht(n=8, batch=2, output_strides=[3])) as plan:
-        assert json.loads(plan.mapping_json())["output_batch_stride"] == (8 - 1) * 3 + 1
+        assert plan.mapping()["output_batch_stride"] == (8 - 1) * 3 + 1
         assert plan.output_size() == ((8 - 1) * 3 + (8 - 1) * 3 + 1 + 1) * 4
 
 

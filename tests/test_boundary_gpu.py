@@ -79,13 +79,11 @@ def case(n, batch, dtype, seed, in_layout, out_layout, sentinel):
     return x_flat, rows, out_pos, span(n, batch, s_out, bs_out)
 
 
-def transform(op, n, batch, in_layout, out_layout, **kw):
+def transform(op, n, batch, in_layout, out_layout, storage, **kw):
     (s_in, bs_in, rev_in), (s_out, bs_out, rev_out) = in_layout, out_layout
     order = lambda rev: [cb.LogicalOrder.BIT_REVERSED if rev else cb.LogicalOrder.NATURAL]
     bs_in, bs_out = (b if b >= 0 else batch_stride_of(n, s, b) for s, b in ((s_in, bs_in), (s_out, bs_out)))
-    return cb.Transform(op=op, extents=[n], batch=batch, input_strides=[s_in], input_batch_stride=bs_in,
-                        output_strides=[s_out], output_batch_stride=bs_out, input_orders=order(rev_in),
-                        output_orders=order(rev_out), **kw)
+    return cb.describe(op, storage, [n], batch=batch, input_strides=[s_in], input_batch_stride=bs_in, output_strides=[s_out], output_batch_stride=bs_out, input_orders=order(rev_in), output_orders=order(rev_out), **kw)
 
 
 LAYOUTS = [
@@ -144,7 +142,7 @@ def test_ntt_negacyclic(torch_gpu, lib, stream, log_n, in_layout, out_layout):
     n, batch = 1 << log_n, 2
     x_flat, rows, out_pos, out_len = case(n, batch, np.uint32, 4, in_layout, out_layout, 0)
     t = transform(cb.Operator.NTT, n, batch, in_layout, out_layout, storage=cb.DataType.UINT32,
-                  compute=cb.ComputeType.UINT32, modulus=Q30, word_bits=32, ring=cb.NttRing.NEGACYCLIC)
+                  compute=cb.ComputeType.UINT32, modulus=Q30, word_bits=32, ntt_ring=cb.NttRing.NEGACYCLIC)
     if in_layout[:2] in ((1, 0),) and out_layout[:2] in ((1, 0),):
         pytest.skip("packed NTT orders are native (not a boundary plan); covered by test_ntt_gpu")
     got = run(torch_gpu, lib, stream, t, x_flat, out_len, np.uint32(0xDEADBEEF))
@@ -159,7 +157,7 @@ def test_in_place_interleaved(torch_gpu, lib, stream):
     layout = (4, 1, False)
     x_flat, rows, out_pos, out_len = case(n, batch, np.float32, 5, layout, layout, 0)
     t = transform(cb.Operator.FWHT, n, batch, layout, layout, storage=cb.DataType.FP32,
-                  compute=cb.ComputeType.FP32, in_place=True)
+                  compute=cb.ComputeType.FP32, placement=cb.Placement.IN_PLACE)
     got = run(torch_gpu, lib, stream, t, x_flat, out_len, 0, in_place=True)
     expected = x_flat.copy()
     expected[out_pos] = oracle.fwht_f32(rows)
@@ -169,31 +167,25 @@ def test_in_place_interleaved(torch_gpu, lib, stream):
 def test_fft_logical_order_plan(torch_gpu, lib):
     # One-pass lengths take bit-reversed orders natively; longer ones through
     # the boundary.
-    t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                     extents=[64], batch=2, output_orders=[cb.LogicalOrder.BIT_REVERSED],
-                     input_orders=[cb.LogicalOrder.NATURAL])
+    t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64], compute=cb.ComputeType.FP32, batch=2, output_orders=[cb.LogicalOrder.BIT_REVERSED], input_orders=[cb.LogicalOrder.NATURAL])
     with cb.Plan(lib, t) as plan:
         assert plan.algorithm_name() == "fft-c64-resident-r16-bitrev-out"
-    t.extents = [1 << 15]
+    t["shape"] = [1 << 15]
     with cb.Plan(lib, t) as plan:
         assert plan.algorithm_name().startswith("semantic-boundary[fft-c64")
-        assert json.loads(plan.mapping_json())["output_bit_reversed"] is True
+        assert plan.mapping()["output_bit_reversed"] is True
 
 
 def test_packed_ntt_orders_stay_native(torch_gpu, lib):
-    t = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
-                     extents=[64], batch=2, modulus=998244353, word_bits=32,
-                     output_order=cb.NttLayout.BIT_REVERSED)
+    t = cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [64], compute=cb.ComputeType.UINT32, batch=2, modulus=998244353, word_bits=32, ntt_output_layout=cb.NttLayout.BIT_REVERSED)
     with cb.Plan(lib, t) as plan:
         assert not plan.algorithm_name().startswith("semantic-boundary")
 
 
 def test_strided_two_pass_ntt_workspace(torch_gpu, lib):
-    t = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT64, compute=cb.ComputeType.UINT64,
-                     extents=[1 << 14], batch=2, modulus=576460756061519873, word_bits=64,
-                     input_strides=[2], input_batch_stride=1)
+    t = cb.describe(cb.Operator.NTT, cb.DataType.UINT64, [1 << 14], compute=cb.ComputeType.UINT64, batch=2, modulus=576460756061519873, word_bits=64, input_strides=[2], input_batch_stride=1)
     with cb.Plan(lib, t) as plan:
         assert plan.algorithm_name().startswith("semantic-boundary[ntt")
-        m = json.loads(plan.mapping_json())
+        m = plan.mapping()
         packed = (1 << 15) * 8
         assert plan.workspace_size() == m["workspace_bytes"] >= 2 * packed

@@ -10,12 +10,11 @@ import cubutterfly_amd as cb
 
 
 def fwht(extents, **kw):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                        extents=list(extents), **kw)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, list(extents), compute=cb.ComputeType.FP32, **kw)
 
 
 def schedule(plan):
-    return json.loads(plan.mapping_json())["schedule"]
+    return plan.mapping()["schedule"]
 
 
 def test_rank2_fwht_is_one_kronecker_plan(lib):
@@ -83,7 +82,7 @@ def test_strided_rank2_gathers_and_scatters(lib):
         assert "+direct-input" not in name and name.endswith("+direct-output")
         assert plan.input_size() == (128 + 7 * 16 + 8) * 4
         assert plan.workspace_size() == 2 * 8 * 8 * 4  # gathered buffer only
-        assert json.loads(plan.mapping_json())["direct_input_boundary"] is False
+        assert plan.mapping()["direct_input_boundary"] is False
 
 
 def test_rank2_orders_need_the_boundary(lib):
@@ -93,13 +92,11 @@ def test_rank2_orders_need_the_boundary(lib):
 
 
 def test_rank2_not_supported_cases(lib):
-    fp16 = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
-                        output_rounding=cb.OutputRounding.FINAL_STORAGE, extents=[8, 8])
-    negacyclic = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
-                              extents=[8, 8], modulus=998244353, word_bits=32, ring=cb.NttRing.NEGACYCLIC)
+    fp16 = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [8, 8], compute=cb.ComputeType.FP32, output_rounding=cb.OutputRounding.FINAL_STORAGE)
+    negacyclic = cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [8, 8], compute=cb.ComputeType.UINT32, modulus=998244353, word_bits=32, ntt_ring=cb.NttRing.NEGACYCLIC)
     odd = fwht([8, 1])
     for t in (fp16, negacyclic, odd):
-        with pytest.raises(cb.Error) as e:
+        with pytest.raises(cb.AbiError) as e:
             cb.Plan(lib, t)
         assert e.value.status == cb.Status.NOT_SUPPORTED, lib.last_error()
 
@@ -172,17 +169,15 @@ def test_fwht_composition_is_the_flat_transform():
 
 def test_long_fwht_is_factored(lib):
     # FWHT beyond 2^13 points: axes of at most 2^12, lowest bits innermost.
-    t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                     extents=[1 << 20], batch=2)
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << 20], compute=cb.ComputeType.FP32, batch=2)
     with cb.Plan(lib, t) as plan:
         assert plan.algorithm_name().startswith("fwht-factored[fwht-fp32-resident-r16,")
         assert plan.physical_extents() == [1 << 20]
         assert plan.input_size() == plan.output_size() == 2 * (1 << 20) * 4
-        m = json.loads(plan.mapping_json())
+        m = plan.mapping()
         assert m["extents"] == [256, 4096]
         assert [s["axis"] for s in m["schedule"] if s["step"] == "axis"] == [1, 0]
-    fp16 = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
-                        output_rounding=cb.OutputRounding.FINAL_STORAGE, extents=[1 << 14])
-    with pytest.raises(cb.Error) as e:
+    fp16 = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [1 << 14], compute=cb.ComputeType.FP32, output_rounding=cb.OutputRounding.FINAL_STORAGE)
+    with pytest.raises(cb.AbiError) as e:
         cb.Plan(lib, fp16)
     assert e.value.status == cb.Status.NOT_SUPPORTED

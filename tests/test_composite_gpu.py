@@ -29,20 +29,17 @@ def data(shape, dtype, seed, q=None):
 
 
 def fwht_t(extents, batch, **kw):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                        extents=list(extents), batch=batch, **kw)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, list(extents), compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
 def fft_t(extents, batch, **kw):
-    return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                        extents=list(extents), batch=batch, **kw)
+    return cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, list(extents), compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
 def ntt_t(extents, batch, word_bits, q, **kw):
     storage = cb.DataType.UINT32 if word_bits == 32 else cb.DataType.UINT64
     compute = cb.ComputeType.UINT32 if word_bits == 32 else cb.ComputeType.UINT64
-    return cb.Transform(op=cb.Operator.NTT, storage=storage, compute=compute, extents=list(extents),
-                        batch=batch, modulus=q, word_bits=word_bits, **kw)
+    return cb.describe(cb.Operator.NTT, storage, list(extents), compute=compute, batch=batch, modulus=q, word_bits=word_bits, **kw)
 
 
 @pytest.mark.parametrize("extents,inverse,prefix", [
@@ -104,7 +101,7 @@ def test_ntt_rank2_brute_force(torch_gpu, lib, stream):
 def test_in_place(torch_gpu, lib, stream):
     extents, batch = (64, 32), 2
     x = data((batch,) + extents, np.complex64, 5)
-    t = fft_t(extents, batch, in_place=True)
+    t = fft_t(extents, batch, placement=cb.Placement.IN_PLACE)
     got = run_plan(torch_gpu, lib, t, x, stream, in_place=True).astype(np.complex128)
     ref = np.fft.fftn(x.astype(np.complex128), axes=(1, 2))
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
@@ -156,7 +153,7 @@ def test_transpose_edges(torch_gpu, lib, stream):
 
 def test_mapping_reports_children(torch_gpu, lib):
     with cb.Plan(lib, ntt_t((64, 1 << 13), 2, 64, Q60)) as plan:
-        m = json.loads(plan.mapping_json())
+        m = plan.mapping()
         assert m["kind"] == "composition" and m["rank"] == 2
         axes = [s for s in m["schedule"] if s["step"] == "axis"]
         assert [s["axis"] for s in axes] == [1, 0]
@@ -172,7 +169,7 @@ def test_fft_transposing_rows(torch_gpu, lib, stream, extents, inverse):
     t = fft_t(extents, batch, inverse=inverse)
     with cb.Plan(lib, t) as plan:
         assert plan.algorithm_name().startswith("rank2-transposing[fft-c64-rows-transposed-r16,")
-        m = json.loads(plan.mapping_json())
+        m = plan.mapping()
         assert [s["step"] for s in m["schedule"]] == ["axis", "axis"]
         assert plan.workspace_size() == batch * extents[0] * extents[1] * 8  # one intermediate
     got = run_plan(torch_gpu, lib, t, x, stream).astype(np.complex128)
@@ -186,7 +183,7 @@ def test_fft_transposing_rows_strided_in_place(torch_gpu, lib, stream):
     span = (batch * n0 - 1) * pitch + n1
     rng = np.random.default_rng(9)
     flat = (rng.standard_normal(span) + 1j * rng.standard_normal(span)).astype(np.complex64)
-    t = fft_t((n0, n1), batch, in_place=True, input_strides=[pitch, 1], input_batch_stride=n0 * pitch,
+    t = fft_t((n0, n1), batch, placement=cb.Placement.IN_PLACE, input_strides=[pitch, 1], input_batch_stride=n0 * pitch,
               output_strides=[pitch, 1], output_batch_stride=n0 * pitch)
     got = run_plan(torch_gpu, lib, t, flat, stream, in_place=True)
     rows = np.stack([flat[k * pitch: k * pitch + n1] for k in range(batch * n0)]).reshape(batch, n0, n1)

@@ -11,8 +11,7 @@ import cubutterfly_amd as cb
 
 
 def fwht(extents, **kw):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                        extents=list(extents), length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING, **kw)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, list(extents), compute=cb.ComputeType.FP32, length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING, **kw)
 
 
 def test_forward_sizes_and_names(lib):
@@ -22,7 +21,7 @@ def test_forward_sizes_and_names(lib):
         assert plan.output_size() == 3 * 128 * 4
         assert plan.algorithm_name() == "zero-extended[fwht-fp32-resident-r16]+direct-output"
         assert plan.workspace_size() == 3 * 128 * 4  # the zero-filled input
-        m = json.loads(plan.mapping_json())
+        m = plan.mapping()
         assert m["zero_extended"] is True and m["input_extents"] == [100] and m["output_extents"] == [128]
 
 
@@ -48,7 +47,7 @@ def test_power_of_two_extent_is_unchanged(lib):
 
 def test_orders_need_power_of_two_side_extents(lib):
     bad = fwht([100], input_orders=[cb.LogicalOrder.BIT_REVERSED])
-    with pytest.raises(cb.Error) as e:
+    with pytest.raises(cb.AbiError) as e:
         cb.Plan(lib, bad)
     assert e.value.status == cb.Status.INVALID_VALUE
     ok = fwht([100], output_orders=[cb.LogicalOrder.BIT_REVERSED])  # the padded side
@@ -57,10 +56,8 @@ def test_orders_need_power_of_two_side_extents(lib):
 
 
 def test_not_supported_embeddings(lib):
-    fp16 = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
-                        output_rounding=cb.OutputRounding.FINAL_STORAGE, extents=[100],
-                        length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING)
+    fp16 = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [100], compute=cb.ComputeType.FP32, output_rounding=cb.OutputRounding.FINAL_STORAGE, length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING)
     for t in (fp16, fwht([1])):
-        with pytest.raises(cb.Error) as e:
+        with pytest.raises(cb.AbiError) as e:
             cb.Plan(lib, t)
         assert e.value.status == cb.Status.NOT_SUPPORTED, lib.last_error()

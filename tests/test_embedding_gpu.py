@@ -33,8 +33,7 @@ def pad(x, p):
 def test_fwht_forward(torch_gpu, lib, stream, n):
     batch = 3
     x = np.random.default_rng(n).standard_normal((batch, n)).astype(np.float32)
-    t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                     extents=[n], batch=batch, length_mode=EMB)
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch, length_mode=EMB)
     got = run_plan(torch_gpu, lib, t, x, stream)
     expected = oracle.fwht_f32(pad(x, pow2(n)))
     np.testing.assert_array_equal(got.reshape(batch, -1).view(np.uint32), expected.view(np.uint32))
@@ -43,8 +42,7 @@ def test_fwht_forward(torch_gpu, lib, stream, n):
 def test_fwht_inverse_cuts(torch_gpu, lib, stream):
     n, batch = 100, 4
     y = np.random.default_rng(1).standard_normal((batch, 128)).astype(np.float32)
-    t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                     extents=[n], batch=batch, inverse=True, length_mode=EMB)
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch, inverse=True, length_mode=EMB)
     got = run_plan(torch_gpu, lib, t, y, stream)
     expected = oracle.fwht_f32(y, inverse=True, normalize=True)[:, :n]
     np.testing.assert_array_equal(got.reshape(batch, n).view(np.uint32), expected.view(np.uint32))
@@ -57,8 +55,7 @@ def test_fft(torch_gpu, lib, stream, n, inverse):
     rng = np.random.default_rng(n + inverse)
     m = p if inverse else n
     x = (rng.standard_normal((batch, m)) + 1j * rng.standard_normal((batch, m))).astype(np.complex64)
-    t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                     extents=[n], batch=batch, inverse=inverse, length_mode=EMB)
+    t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [n], compute=cb.ComputeType.FP32, batch=batch, inverse=inverse, length_mode=EMB)
     got = run_plan(torch_gpu, lib, t, x, stream).reshape(batch, -1).astype(np.complex128)
     if inverse:
         ref = np.fft.ifft(x.astype(np.complex128), axis=-1)[:, :n]
@@ -74,8 +71,7 @@ def test_ntt(torch_gpu, lib, stream, n, inverse):
     batch, p = 3, pow2(n)
     rng = np.random.default_rng(n)
     x = rng.integers(0, Q, (batch, p if inverse else n)).astype(np.uint32)
-    t = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
-                     extents=[n], batch=batch, modulus=Q, word_bits=32, inverse=inverse, length_mode=EMB)
+    t = cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [n], compute=cb.ComputeType.UINT32, batch=batch, modulus=Q, word_bits=32, inverse=inverse, length_mode=EMB)
     got = run_plan(torch_gpu, lib, t, x, stream).reshape(batch, -1)
     if inverse:
         expected = oracle.ntt_cyclic(x.astype(np.uint64), Q, inverse=True)[:, :n]
@@ -91,8 +87,7 @@ def test_rank2_fft(torch_gpu, lib, stream, inverse):
     rng = np.random.default_rng(7)
     side = phys if inverse else shape
     x = (rng.standard_normal((batch,) + side) + 1j * rng.standard_normal((batch,) + side)).astype(np.complex64)
-    t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                     extents=list(shape), batch=batch, inverse=inverse, length_mode=EMB)
+    t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, list(shape), compute=cb.ComputeType.FP32, batch=batch, inverse=inverse, length_mode=EMB)
     got = run_plan(torch_gpu, lib, t, x, stream).astype(np.complex128)
     if inverse:
         ref = np.fft.ifftn(x.astype(np.complex128), axes=(1, 2))[:, :5, :12]
@@ -107,8 +102,7 @@ def test_strided_input(torch_gpu, lib, stream):
     n, batch = 100, 3
     rng = np.random.default_rng(3)
     flat = (rng.standard_normal(2 * n * batch) + 1j * rng.standard_normal(2 * n * batch)).astype(np.complex64)
-    t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                     extents=[n], batch=batch, length_mode=EMB, input_strides=[2], input_batch_stride=2 * n)
+    t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [n], compute=cb.ComputeType.FP32, batch=batch, length_mode=EMB, input_strides=[2], input_batch_stride=2 * n)
     span = 2 * n * (batch - 1) + 2 * (n - 1) + 1
     got = run_plan(torch_gpu, lib, t, flat[:span], stream).reshape(batch, 128).astype(np.complex128)
     rows = flat[: 2 * n * batch].reshape(batch, 2 * n)[:, ::2]

@@ -1,11 +1,14 @@
 """Complex FFT parity on the GPU through the C ABI.
 
-The contract is rel-L2 <= 1e-5 per transform (COMPLEX_FP32 storage, FP32
-compute). The truth is numpy's complex128 FFT of the same complex64 input; the
-oracle (the reference's iterative radix-2 in fp32 storage, src/reference.cpp)
-is checked beside it on the small cases, so a kernel that agrees with numpy
-but not with the reference's sign or normalisation convention fails too.
-C3 runs at full size: 1 x 2^24 and 1024 x 2^14.
+The contract is rel-L2 <= 1e-5 per transform against the reference's own
+output (COMPLEX_FP32 storage, FP32 compute): the oracle restates the
+reference CPU path (reference_fft: bit reversal, radix-2 with double-precision
+twiddles per butterfly, float storage; src/butterfly_reference.cpp:392-433),
+and every length from 2^1 to 2^24 -- C3 at full size, 1 x 2^24 and
+1024 x 2^14 -- is compared with it per transform at 1e-5. numpy's complex128
+FFT of the same complex64 input is a second, independent truth at the same
+tolerance, so a kernel that agrees with the oracle only because both share a
+mistake fails too.
 """
 import numpy as np
 import pytest
@@ -21,8 +24,7 @@ TOL = 1e-5
 
 
 def fft(log_n, batch, **kw):
-    return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                        extents=[1 << log_n], batch=batch, **kw)
+    return cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [1 << log_n], compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
 def truth(x, inverse=False, normalize=False):
@@ -45,10 +47,12 @@ def test_c3_full_size(torch_gpu, lib, stream, rows, log_n):
     print(f"case C3 fft c64 {rows} x 2^{log_n}", flush=True)
     x = workloads.complex_input(log_n, rows, seed=3).reshape(rows, 1 << log_n)
     got = run_plan(torch_gpu, lib, fft(log_n, rows), x, stream)
+    err = worst_rel_l2(got, oracle.fft_c64(x, threads=oracle.default_threads()).astype(np.complex128))
+    assert err <= TOL, f"rel-L2 vs the reference CPU path {err}"
     err = worst_rel_l2(got, truth(x))
-    assert err <= TOL, f"rel-L2 {err}"
-    # Round trip through the normalised inverse returns the input.
-    back = run_plan(torch_gpu, lib, fft(log_n, rows, inverse=True, in_place=True), got, stream, in_place=True)
+    assert err <= TOL, f"rel-L2 vs complex128 {err}"
+    # Round trip (forward and inverse errors add: a property, not the parity bar) through the normalised inverse returns the input.
+    back = run_plan(torch_gpu, lib, fft(log_n, rows, inverse=True, placement=cb.Placement.IN_PLACE), got, stream, in_place=True)
     err = worst_rel_l2(back, x.astype(np.complex128))
     assert err <= 2 * TOL, f"round trip rel-L2 {err}"
 
@@ -60,10 +64,10 @@ def test_forward_every_length(torch_gpu, lib, stream, log_n):
     x = workloads.complex_input(log_n, batch, seed=log_n).reshape(batch, 1 << log_n)
     got = run_plan(torch_gpu, lib, fft(log_n, batch), x, stream)
     err = worst_rel_l2(got, truth(x))
-    assert err <= TOL, f"rel-L2 {err}"
-    if log_n <= 18:
-        ref = oracle.fft_c64(x, threads=oracle.default_threads())
-        assert worst_rel_l2(got, ref.astype(np.complex128)) <= 2 * TOL
+    assert err <= TOL, f"rel-L2 vs complex128 {err}"
+    ref = oracle.fft_c64(x, threads=oracle.default_threads())
+    err = worst_rel_l2(got, ref.astype(np.complex128))
+    assert err <= TOL, f"rel-L2 vs the reference CPU path {err}"
 
 
 @pytest.mark.parametrize("log_n", [1, 4, 9, 12, 13, 14, 15, 17, 20, 23])
@@ -74,16 +78,16 @@ def test_inverse(torch_gpu, lib, stream, log_n, normalize):
     x = workloads.complex_input(log_n, batch, seed=100 + log_n).reshape(batch, 1 << log_n)
     got = run_plan(torch_gpu, lib, fft(log_n, batch, inverse=True, normalize_inverse=normalize), x, stream)
     err = worst_rel_l2(got, truth(x, inverse=True, normalize=normalize))
-    assert err <= TOL, f"rel-L2 {err}"
-    if log_n <= 15:
-        ref = oracle.fft_c64(x, inverse=True, normalize=normalize)
-        assert worst_rel_l2(got, ref.astype(np.complex128)) <= 2 * TOL
+    assert err <= TOL, f"rel-L2 vs complex128 {err}"
+    ref = oracle.fft_c64(x, inverse=True, normalize=normalize, threads=oracle.default_threads())
+    err = worst_rel_l2(got, ref.astype(np.complex128))
+    assert err <= TOL, f"rel-L2 vs the reference CPU path {err}"
 
 
 @pytest.mark.parametrize("log_n,batch", [(3, 1000), (11, 7), (14, 9), (16, 4), (19, 2)])
 def test_in_place(torch_gpu, lib, stream, log_n, batch):
     x = workloads.complex_input(log_n, batch, seed=9).reshape(batch, 1 << log_n)
-    got = run_plan(torch_gpu, lib, fft(log_n, batch, in_place=True), x, stream, in_place=True)
+    got = run_plan(torch_gpu, lib, fft(log_n, batch, placement=cb.Placement.IN_PLACE), x, stream, in_place=True)
     assert worst_rel_l2(got, truth(x)) <= TOL
 
 

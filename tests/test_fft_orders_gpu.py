@@ -27,9 +27,7 @@ def test_orders(torch_gpu, lib, stream, log_n, rin, rout, inverse):
     rng = np.random.default_rng(log_n * 4 + rin * 2 + rout)
     x = (rng.standard_normal((batch, n)) + 1j * rng.standard_normal((batch, n))).astype(np.complex64)
     order = lambda rev: [cb.LogicalOrder.BIT_REVERSED if rev else cb.LogicalOrder.NATURAL]
-    t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                     extents=[n], batch=batch, inverse=inverse, input_orders=order(rin),
-                     output_orders=order(rout))
+    t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [n], compute=cb.ComputeType.FP32, batch=batch, inverse=inverse, input_orders=order(rin), output_orders=order(rout))
     with cb.Plan(lib, t) as plan:
         name = plan.algorithm_name()
         assert not name.startswith("semantic-boundary") and "-bitrev-" in name, name
@@ -51,10 +49,8 @@ def test_round_trip_through_bit_reversed_spectrum(torch_gpu, lib, stream):
     n, batch = 1 << 14, 8
     rng = np.random.default_rng(11)
     x = (rng.standard_normal((batch, n)) + 1j * rng.standard_normal((batch, n))).astype(np.complex64)
-    fwd = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                       extents=[n], batch=batch, output_orders=[cb.LogicalOrder.BIT_REVERSED])
-    inv = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                       extents=[n], batch=batch, inverse=True, input_orders=[cb.LogicalOrder.BIT_REVERSED])
+    fwd = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [n], compute=cb.ComputeType.FP32, batch=batch, output_orders=[cb.LogicalOrder.BIT_REVERSED])
+    inv = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [n], compute=cb.ComputeType.FP32, batch=batch, inverse=True, input_orders=[cb.LogicalOrder.BIT_REVERSED])
     spectrum = run_plan(torch_gpu, lib, fwd, x, stream)
     back = run_plan(torch_gpu, lib, inv, spectrum, stream).astype(np.complex128)
     assert np.linalg.norm(back - x) / np.linalg.norm(x) <= 1e-5

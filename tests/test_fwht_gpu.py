@@ -19,14 +19,11 @@ THREADS = oracle.default_threads()
 
 
 def fwht32(n, batch, **kw):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                        extents=[n], batch=batch, **kw)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
 def fwht16(n, batch, scale, **kw):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
-                        extents=[n], batch=batch, output_scale=scale,
-                        output_rounding=cb.OutputRounding.FINAL_STORAGE, **kw)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [n], compute=cb.ComputeType.FP32, batch=batch, output_scale=scale, output_rounding=cb.OutputRounding.FINAL_STORAGE, **kw)
 
 
 def random_floats(rows, n, seed):
@@ -53,7 +50,7 @@ def test_fp32_random_floats_bit_exact(torch_gpu, lib, stream, log_n, batch):
 @pytest.mark.parametrize("log_n,batch", [(5, 129), (7, 1000), (12, 3), (13, 2)])
 def test_fp32_inverse_normalised_in_place(torch_gpu, lib, stream, log_n, batch):
     x = random_floats(batch, 1 << log_n, seed=7)
-    got = run_plan(torch_gpu, lib, fwht32(1 << log_n, batch, inverse=True, in_place=True), x, stream,
+    got = run_plan(torch_gpu, lib, fwht32(1 << log_n, batch, inverse=True, placement=cb.Placement.IN_PLACE), x, stream,
                    in_place=True)
     expected = oracle.fwht_f32(x, inverse=True, normalize=True)
     np.testing.assert_array_equal(got.view(np.uint32), expected.view(np.uint32))

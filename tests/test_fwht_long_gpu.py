@@ -13,8 +13,7 @@ pytestmark = pytest.mark.gpu
 
 
 def fwht(n, batch, **kw):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                        extents=[n], batch=batch, **kw)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
 @pytest.mark.parametrize("log_n,batch", [(14, 8), (16, 4), (20, 2), (24, 1)])
@@ -27,7 +26,7 @@ def test_forward_bit_exact(torch_gpu, lib, stream, log_n, batch):
 
 def test_inverse_normalised_and_in_place(torch_gpu, lib, stream):
     x = np.random.default_rng(3).standard_normal((3, 1 << 16)).astype(np.float32)
-    got = run_plan(torch_gpu, lib, fwht(1 << 16, 3, inverse=True, in_place=True), x, stream, in_place=True)
+    got = run_plan(torch_gpu, lib, fwht(1 << 16, 3, inverse=True, placement=cb.Placement.IN_PLACE), x, stream, in_place=True)
     expected = oracle.fwht_f32(x, inverse=True, normalize=True, threads=oracle.default_threads())
     np.testing.assert_array_equal(got.view(np.uint32), expected.view(np.uint32))
 

@@ -20,11 +20,9 @@ def run(torch, lib, stream, n, batch, in_pitch, out_pitch, fp16=False, inverse=F
     span_out = (batch - 1) * out_pitch + n
     x = rng.standard_normal(span_in).astype(dtype)
     rows = np.stack([x[b * in_pitch: b * in_pitch + n] for b in range(batch)])
-    kw = dict(storage=cb.DataType.FP16, output_rounding=cb.OutputRounding.FINAL_STORAGE,
-              output_scale=n ** -0.5) if fp16 else dict(storage=cb.DataType.FP32)
-    t = cb.Transform(op=cb.Operator.FWHT, compute=cb.ComputeType.FP32, extents=[n], batch=batch,
-                     input_strides=[1], input_batch_stride=in_pitch, output_strides=[1],
-                     output_batch_stride=out_pitch, inverse=inverse, in_place=in_place, **kw)
+    kw = dict(output_rounding=cb.OutputRounding.FINAL_STORAGE,
+              output_scale=n ** -0.5) if fp16 else {}
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP16 if fp16 else cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch, input_strides=[1], input_batch_stride=in_pitch, output_strides=[1], output_batch_stride=out_pitch, inverse=inverse, placement=int(in_place), **kw)
     sentinel = dtype(-3.0)
     xd = to_device(torch, x)
     yd = xd if in_place else to_device(torch, np.full(span_out, sentinel, dtype))

@@ -16,14 +16,13 @@ pytestmark = pytest.mark.gpu
 
 
 def transform(log_n, batch, fp16, inverse=False, in_place=False, **layout):
-    kw = dict(storage=cb.DataType.FP16, output_rounding=cb.OutputRounding.FINAL_STORAGE,
-              output_scale=(1 << log_n) ** -0.5) if fp16 else dict(storage=cb.DataType.FP32)
-    return cb.Transform(op=cb.Operator.FWHT, compute=cb.ComputeType.FP32, extents=[1 << log_n], batch=batch,
-                        inverse=inverse, in_place=in_place, **kw, **layout)
+    kw = dict(output_rounding=cb.OutputRounding.FINAL_STORAGE,
+              output_scale=(1 << log_n) ** -0.5) if fp16 else {}
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP16 if fp16 else cb.DataType.FP32, [1 << log_n], compute=cb.ComputeType.FP32, batch=batch, inverse=inverse, placement=int(in_place), **kw, **layout)
 
 
 def explicit(name):
-    return cb.PlanOptions(policy=cb.AlgorithmPolicy.EXPLICIT, mapping=name)
+    return {"algorithm": name}
 
 
 def wide_name(fp16=True, pitched=False):
@@ -56,10 +55,10 @@ def test_packed(torch_gpu, lib, stream, fp16, log_n, inverse):
     batch = 300 + log_n
     x = inputs(log_n, batch, fp16, seed=log_n + 10 * fp16)
     t = transform(log_n, batch, fp16, inverse=inverse)
-    with cb.Plan(lib, t, options=explicit(wide_name(fp16))) as plan:
+    with cb.Plan(lib, t, **explicit(wide_name(fp16))) as plan:
         assert plan.algorithm_name() == wide_name(fp16)
         assert plan.workspace_size() == 0
-    got = run_plan(torch_gpu, lib, t, x, stream, options=explicit(wide_name(fp16)))
+    got = run_plan(torch_gpu, lib, t, x, stream, **explicit(wide_name(fp16)))
     np.testing.assert_array_equal(bits(got), bits(expected(x, log_n, fp16, inverse)))
 
 
@@ -68,7 +67,7 @@ def test_in_place(torch_gpu, lib, stream, fp16):
     log_n, batch = 12, 97
     x = inputs(log_n, batch, fp16, seed=5)
     t = transform(log_n, batch, fp16, in_place=True)
-    got = run_plan(torch_gpu, lib, t, x, stream, in_place=True, options=explicit(wide_name(fp16)))
+    got = run_plan(torch_gpu, lib, t, x, stream, in_place=True, **explicit(wide_name(fp16)))
     np.testing.assert_array_equal(bits(got), bits(expected(x, log_n, fp16, False)))
 
 
@@ -87,7 +86,7 @@ def test_pitched(torch_gpu, lib, stream, fp16, log_n):
                   output_batch_stride=out_pitch)
     xd = to_device(torch_gpu, x)
     yd = to_device(torch_gpu, np.full((batch - 1) * out_pitch + n, sentinel, dtype))
-    with cb.Plan(lib, t, options=explicit(wide_name(fp16, pitched=True)), stream=stream) as plan:
+    with cb.Plan(lib, t, **explicit(wide_name(fp16, pitched=True)), stream=stream) as plan:
         assert plan.algorithm_name() == wide_name(fp16, pitched=True)
         plan.execute(xd, yd)
         torch_gpu.cuda.synchronize()
@@ -101,7 +100,7 @@ def test_pitched(torch_gpu, lib, stream, fp16, log_n):
 
 def test_measure_lists_both_lowerings(torch_gpu, lib, stream, tmp_path):
     t = transform(12, 256, True)
-    with cb.Plan(lib, t, options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE), stream=stream,
+    with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream,
                  cache_path=tmp_path / "c.tsv") as plan:
         reason = plan.selection_reason()
         name = plan.algorithm_name()
@@ -112,8 +111,8 @@ def test_measure_lists_both_lowerings(torch_gpu, lib, stream, tmp_path):
 @pytest.mark.parametrize("log_n,fp16", [(10, True), (14, True), (12, False)])
 def test_other_shapes_refuse_the_wide_lowering(lib, log_n, fp16):
     # Only FP16 rows of 2^11..2^13 points (FP32 words would spill the registers).
-    with pytest.raises(cb.Error) as e:
-        cb.Plan(lib, transform(log_n, 8, fp16), options=explicit(wide_name(fp16)))
+    with pytest.raises(cb.AbiError) as e:
+        cb.Plan(lib, transform(log_n, 8, fp16), **explicit(wide_name(fp16)))
     assert e.value.status == cb.Status.NOT_SUPPORTED
 
 
@@ -125,9 +124,9 @@ def test_persistent_walk(torch_gpu, lib, stream, fp16, log_n, batch):
     name = wide_name(fp16).replace("-r32", "-r32-persistent")
     x = inputs(log_n, batch, fp16, seed=batch)
     t = transform(log_n, batch, fp16)
-    with cb.Plan(lib, t, options=explicit(name)) as plan:
+    with cb.Plan(lib, t, **explicit(name)) as plan:
         assert plan.algorithm_name() == name
-        grid = json.loads(plan.mapping_json())["grid"]
+        grid = plan.mapping()["grid"]
     assert grid < batch
-    got = run_plan(torch_gpu, lib, t, x, stream, options=explicit(name))
+    got = run_plan(torch_gpu, lib, t, x, stream, **explicit(name))
     np.testing.assert_array_equal(bits(got), bits(expected(x, log_n, fp16, False)))

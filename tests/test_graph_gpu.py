@@ -16,24 +16,19 @@ Q30 = 1073479681
 
 
 def fft(n, batch, **kw):
-    return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                        extents=[n] if isinstance(n, int) else n, batch=batch, **kw)
+    return cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [n] if isinstance(n, int) else n, compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
 def ntt(n, batch, **kw):
-    return cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
-                        extents=[n], batch=batch, modulus=Q30, word_bits=32, ring=cb.NttRing.NEGACYCLIC, **kw)
+    return cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [n], compute=cb.ComputeType.UINT32, batch=batch, modulus=Q30, word_bits=32, ntt_ring=cb.NttRing.NEGACYCLIC, **kw)
 
 
 def fwht(n, batch, **kw):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                        extents=[n], batch=batch, **kw)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
 def fwht16(n, batch):
-    return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
-                        extents=[n], batch=batch, output_scale=n ** -0.5,
-                        output_rounding=cb.OutputRounding.FINAL_STORAGE)
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [n], compute=cb.ComputeType.FP32, batch=batch, output_scale=n ** -0.5, output_rounding=cb.OutputRounding.FINAL_STORAGE)
 
 
 CASES = {

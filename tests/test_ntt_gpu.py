@@ -26,8 +26,7 @@ Q63 = 9223372036752015361             # largest prime < 2^63 with 2^21 | q - 1 (
 def ntt(n, batch, q, bits, inverse=False, ring=cb.NttRing.CYCLIC, **kw):
     storage = cb.DataType.UINT32 if bits == 32 else cb.DataType.UINT64
     compute = cb.ComputeType.UINT32 if bits == 32 else cb.ComputeType.UINT64
-    return cb.Transform(op=cb.Operator.NTT, storage=storage, compute=compute, extents=[n], batch=batch,
-                        modulus=q, word_bits=bits, inverse=inverse, ring=ring, **kw)
+    return cb.describe(cb.Operator.NTT, storage, [n], compute=compute, batch=batch, modulus=q, word_bits=bits, inverse=inverse, ntt_ring=ring, **kw)
 
 
 def as_words(a, bits):
@@ -89,7 +88,7 @@ def test_bit_reversed_layouts(torch_gpu, lib, stream, q, bits, log_n, inverse):
     x = as_words(workloads.ntt_input(log_n, batch, q, seed=5), bits)
     natural = run_plan(torch_gpu, lib, ntt(n, batch, q, bits, inverse=inverse), x, stream)
     out_rev = run_plan(torch_gpu, lib, ntt(n, batch, q, bits, inverse=inverse,
-                                           output_order=cb.NttLayout.BIT_REVERSED), x, stream)
+                                           ntt_output_layout=cb.NttLayout.BIT_REVERSED), x, stream)
     np.testing.assert_array_equal(out_rev, natural[:, perm])
     in_rev = run_plan(torch_gpu, lib, ntt(n, batch, q, bits, inverse=inverse,
                                           input_orders=[cb.LogicalOrder.BIT_REVERSED],
@@ -112,7 +111,7 @@ def test_non_canonical_inputs_are_reduced(torch_gpu, lib, stream, q, bits, log_n
 @pytest.mark.parametrize("log_n", [6, 16])
 def test_in_place(torch_gpu, lib, stream, log_n):
     x = workloads.ntt_input(log_n, 4, Q30, seed=2).astype(np.uint32)
-    t = ntt(1 << log_n, 4, Q30, 32, ring=cb.NttRing.NEGACYCLIC, in_place=True)
+    t = ntt(1 << log_n, 4, Q30, 32, ring=cb.NttRing.NEGACYCLIC, placement=cb.Placement.IN_PLACE)
     got = run_plan(torch_gpu, lib, t, x, stream, in_place=True)
     np.testing.assert_array_equal(got.astype(np.uint64), oracle.ntt_negacyclic(x.astype(np.uint64), Q30))
 
@@ -123,7 +122,7 @@ def test_explicit_psi(torch_gpu, lib, stream):
     w = oracle.find_primitive_root(log_n, q)
     psi = pow(oracle.find_psi(log_n, q, w), 3, q)
     x = workloads.ntt_input(log_n, 3, q, seed=9)
-    got = run_plan(torch_gpu, lib, ntt(1 << log_n, 3, q, 32, ring=cb.NttRing.NEGACYCLIC, psi=psi),
+    got = run_plan(torch_gpu, lib, ntt(1 << log_n, 3, q, 32, ring=cb.NttRing.NEGACYCLIC, ntt_psi=psi),
                    x.astype(np.uint32), stream)
     expected = oracle.rns(x, [q] * 3, [psi] * 3)  # natural-order negacyclic with explicit root
     np.testing.assert_array_equal(got.astype(np.uint64), expected)

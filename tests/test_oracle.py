@@ -7,11 +7,14 @@ formulations, and library routines (numpy float16, numpy.fft). Each check is
 chosen so that a plausible mistake -- a dropped term, a wrong sign or index, a
 transposed operand, a different stage order or root -- fails it.
 """
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
 import oracle
-from cubutterfly_amd import workloads
+from cubutterfly_amd import ntt_roots, workloads
 
 # Reference moduli fixtures: tests/test_ntt.cpp:251 and friends,
 # tests/test_rns_ntt.cu:19, tests/test_crypto_ntt_host.py:21-26, include/cuntt/ntt.hpp:17.
@@ -201,6 +204,24 @@ def test_is_prime_and_roots(q):
         assert oracle.find_psi(log_n, q, w) == brute_psi(log_n, q, w)
 
 
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def test_roots_match_the_references_recorded_roots():
+    # The reference's benchmark runner records the root it handed each timed
+    # NTT backend (experiments/snapshots/*/identities.json, snapshot.json):
+    # find_primitive_power_of_two_root(log2 n, q) for 11 (q, n) pairs, C2's
+    # modulus at n = 2^16 among them. tests/golden/extract_reference_roots.py
+    # wrote them; the root convention every bit-exact NTT test rests on is
+    # pinned by these values, not only by brute_root's restatement.
+    records = json.loads((GOLDEN / "reference_roots.json").read_text())["records"]
+    assert len(records) == 11 and any(r["modulus"] == workloads.C2_MODULUS and r["n"] == 1 << 16 for r in records)
+    for r in records:
+        log_n = r["n"].bit_length() - 1
+        assert oracle.find_primitive_root(log_n, r["modulus"]) == r["root"], r
+        assert ntt_roots.primitive_root(log_n, r["modulus"]) == r["root"], r
+
+
 def test_is_prime_small_range():
     def naive(v):
         return v >= 2 and all(v % d for d in range(2, int(v ** 0.5) + 1))
@@ -306,3 +327,28 @@ def test_rns_agrees_with_negacyclic_channel_for_the_benchmark_root():
     psi = brute_psi(log_n, q, w)
     x = workloads.ntt_input(log_n, 2, q, seed=6)
     np.testing.assert_array_equal(oracle.rns(x, [q, q], [psi, psi]), oracle.ntt_negacyclic(x, q))
+
+
+# ---------------------------------------------------------------- input generators
+
+def test_mt19937_64_matches_the_cpp_standard():
+    # [rand.predef]: the 10000th consecutive output of a default-constructed
+    # std::mt19937_64 (seed 5489) is 9981545732273789042. Every NTT input
+    # (the reference's make_input, crypto_ntt_bench.cu:436-448) comes from
+    # this generator.
+    values = workloads.MT19937_64(5489).random(10000)
+    assert int(values[-1]) == 9981545732273789042
+    # Drawing in pieces gives the same stream as one draw.
+    g = workloads.MT19937_64(5489)
+    pieces = np.concatenate([g.random(k) for k in (1, 311, 312, 313, 9063)])
+    np.testing.assert_array_equal(pieces, values)
+
+
+def test_ntt_input_follows_make_input():
+    # First four words {0, 1, q-1, q-2}, then mt19937_64 % q from the seed
+    # seed ^ (0x9e3779b97f4a7c15 * (channel + 1)) (crypto_ntt_bench.cu:436-448).
+    q = workloads.C2_MODULUS
+    x = workloads.ntt_input(4, 2, q, seed=7, channel=3)
+    assert list(map(int, x.ravel()[:4])) == [0, 1, q - 1, q - 2]
+    g = workloads.MT19937_64(7 ^ ((0x9E3779B97F4A7C15 * 4) & ((1 << 64) - 1)))
+    np.testing.assert_array_equal(x.ravel()[4:], g.random(28) % np.uint64(q))

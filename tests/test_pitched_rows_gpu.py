@@ -49,9 +49,7 @@ def test_fft(torch_gpu, lib, stream, log_n, inverse):
     rng = np.random.default_rng(log_n)
     span_in, span_out = (batch - 1) * in_pitch + n, (batch - 1) * out_pitch + n
     x = (rng.standard_normal(span_in) + 1j * rng.standard_normal(span_in)).astype(np.complex64)
-    t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                     extents=[n], batch=batch, inverse=inverse, input_strides=[1], input_batch_stride=in_pitch,
-                     output_strides=[1], output_batch_stride=out_pitch)
+    t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [n], compute=cb.ComputeType.FP32, batch=batch, inverse=inverse, input_strides=[1], input_batch_stride=in_pitch, output_strides=[1], output_batch_stride=out_pitch)
     sentinel = np.complex64(7 - 7j)
     name, got = execute(torch_gpu, lib, stream, t, x, span_out, sentinel, False)
     assert name.endswith("-pitched"), name
@@ -72,9 +70,7 @@ def test_fft_in_place(torch_gpu, lib, stream, log_n):
     rng = np.random.default_rng(5)
     span = (batch - 1) * pitch + n
     x = (rng.standard_normal(span) + 1j * rng.standard_normal(span)).astype(np.complex64)
-    t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                     extents=[n], batch=batch, in_place=True, input_strides=[1], input_batch_stride=pitch,
-                     output_strides=[1], output_batch_stride=pitch)
+    t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [n], compute=cb.ComputeType.FP32, batch=batch, placement=cb.Placement.IN_PLACE, input_strides=[1], input_batch_stride=pitch, output_strides=[1], output_batch_stride=pitch)
     name, got = execute(torch_gpu, lib, stream, t, x, span, 0, True)
     assert name.endswith("-pitched")
     ref = oracle.fft_c64(rows_of(x, batch, pitch, n), threads=oracle.default_threads())
@@ -98,10 +94,7 @@ def test_ntt_negacyclic(torch_gpu, lib, stream, word_bits, q, log_n, inverse):
     x = rng.integers(0, q, span_in).astype(dtype)
     storage = cb.DataType.UINT32 if word_bits == 32 else cb.DataType.UINT64
     compute = cb.ComputeType.UINT32 if word_bits == 32 else cb.ComputeType.UINT64
-    t = cb.Transform(op=cb.Operator.NTT, storage=storage, compute=compute, extents=[n], batch=batch,
-                     modulus=q, word_bits=word_bits, ring=cb.NttRing.NEGACYCLIC, inverse=inverse,
-                     input_strides=[1], input_batch_stride=in_pitch, output_strides=[1],
-                     output_batch_stride=out_pitch)
+    t = cb.describe(cb.Operator.NTT, storage, [n], compute=compute, batch=batch, modulus=q, word_bits=word_bits, ntt_ring=cb.NttRing.NEGACYCLIC, inverse=inverse, input_strides=[1], input_batch_stride=in_pitch, output_strides=[1], output_batch_stride=out_pitch)
     sentinel = dtype(0xDEADBEEF)
     name, got = execute(torch_gpu, lib, stream, t, x, span_out, sentinel, False)
     assert name.endswith("-pitched"), name
@@ -115,10 +108,7 @@ def test_ntt_bit_reversed_output_and_in_place(torch_gpu, lib, stream):
     rng = np.random.default_rng(9)
     span = (batch - 1) * pitch + n
     x = rng.integers(0, Q30, span).astype(np.uint32)
-    t = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
-                     extents=[n], batch=batch, modulus=Q30, word_bits=32, ring=cb.NttRing.NEGACYCLIC,
-                     output_order=cb.NttLayout.BIT_REVERSED, in_place=True, input_strides=[1],
-                     input_batch_stride=pitch, output_strides=[1], output_batch_stride=pitch)
+    t = cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [n], compute=cb.ComputeType.UINT32, batch=batch, modulus=Q30, word_bits=32, ntt_ring=cb.NttRing.NEGACYCLIC, ntt_output_layout=cb.NttLayout.BIT_REVERSED, placement=cb.Placement.IN_PLACE, input_strides=[1], input_batch_stride=pitch, output_strides=[1], output_batch_stride=pitch)
     name, got = execute(torch_gpu, lib, stream, t, x, span, 0, True)
     assert name.endswith("-pitched")
     natural = oracle.ntt_negacyclic(rows_of(x, batch, pitch, n).astype(np.uint64), Q30)
@@ -130,9 +120,7 @@ def test_ntt_bit_reversed_output_and_in_place(torch_gpu, lib, stream):
 def test_short_rows_keep_the_boundary(torch_gpu, lib, stream):
     n, batch, pitch = 1 << 10, 3, (1 << 10) + 4
     x = np.arange((batch - 1) * pitch + n, dtype=np.uint32) % Q30
-    t = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
-                     extents=[n], batch=batch, modulus=Q30, word_bits=32, input_strides=[1],
-                     input_batch_stride=pitch)
+    t = cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [n], compute=cb.ComputeType.UINT32, batch=batch, modulus=Q30, word_bits=32, input_strides=[1], input_batch_stride=pitch)
     name, got = execute(torch_gpu, lib, stream, t, x, batch * n, 0, False)
     assert name.startswith("semantic-boundary[")
     expected = oracle.ntt_cyclic(rows_of(x, batch, pitch, n).astype(np.uint64), Q30).astype(np.uint32).ravel()

@@ -5,6 +5,7 @@ import json
 
 import pytest
 
+import cubutterfly_amd as cb
 from cubutterfly_amd import rns, workloads
 import oracle
 
@@ -13,17 +14,17 @@ Q = 1152921504606584833
 
 def good(log_n=12):
     psi = oracle.find_primitive_root(log_n + 1, Q)
-    return rns.config(log_n, [(Q, psi)])
+    return rns.request(log_n, [(Q, psi)])
 
 
 @pytest.fixture(scope="module")
 def lib():
-    return rns.Library()
+    return cb.Native()
 
 
 def rejected(lib, cfg):
-    with pytest.raises(rns.Error) as info:
-        rns.Plan(lib, cfg)
+    with pytest.raises(cb.AbiError) as info:
+        rns.RnsPlan(lib, cfg)
     assert info.value.status == 1, str(info.value)
     return str(info.value)
 
@@ -52,19 +53,19 @@ def test_schema_and_enums(lib):
     rejected(lib, cfg)
     import ctypes as ct
     handle = ct.c_void_p()
-    with pytest.raises(rns.Error) as info:  # truncated JSON straight to the native parser
-        lib._call("Create", b'{"schema_version": 1, "log_n": 12', ct.byref(handle))
+    with pytest.raises(cb.AbiError) as info:  # truncated JSON straight to the native parser
+        lib("RnsCreate", b'{"schema_version": 1, "log_n": 12', ct.byref(handle))
     assert info.value.status == 1 and not handle.value
 
 
 def test_domain_validation(lib):
     for log_n in (11, 21):
-        rejected(lib, rns.config(log_n, [(Q, 3)]))
-    rejected(lib, rns.config(12, [(Q + 2, 3)]))            # not prime
-    rejected(lib, rns.config(12, [(Q, 1)]))                # root of order 1
+        rejected(lib, rns.request(log_n, [(Q, 3)]))
+    rejected(lib, rns.request(12, [(Q + 2, 3)]))            # not prime
+    rejected(lib, rns.request(12, [(Q, 1)]))                # root of order 1
     w = oracle.find_primitive_root(12, Q)
-    rejected(lib, rns.config(12, [(Q, w)]))                # order n: a cyclic root for a negacyclic ring
-    rejected(lib, rns.config(12, [(Q, 0)]))
+    rejected(lib, rns.request(12, [(Q, w)]))                # order n: a cyclic root for a negacyclic ring
+    rejected(lib, rns.request(12, [(Q, 0)]))
     cfg = good()
     cfg["polynomials"][0]["domain"] = 1
     rejected(lib, cfg)

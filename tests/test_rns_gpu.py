@@ -13,6 +13,7 @@ import json
 import numpy as np
 import pytest
 
+import cubutterfly_amd as cb
 import oracle
 from cubutterfly_amd import rns, workloads
 from gpu_util import to_device, to_host
@@ -25,7 +26,7 @@ PRIMES = [1152921504577486849, 576460756061519873]  # tests/test_rns_ntt.cu:19
 
 @pytest.fixture(scope="module")
 def rlib():
-    return rns.Library()
+    return cb.Native()
 
 
 def bitrev_perm(log_n):
@@ -36,13 +37,13 @@ def bitrev_perm(log_n):
     return rev
 
 
-def run(torch, rlib, cfg, host_in, out_words, placement, stream_obj):
+def run(torch, rlib, cfg, host_in, out_words, in_place, stream_obj):
     stream = stream_obj.cuda_stream
     x = to_device(torch, host_in)
-    y = x if placement == rns.Placement.IN_PLACE else to_device(torch, np.full(out_words, SENTINEL))
-    with rns.Plan(rlib, cfg) as plan:
-        plan.prepare(placement=placement, stream=stream)
-        plan.execute(x, y, stream=stream)
+    y = x if in_place else to_device(torch, np.full(out_words, SENTINEL))
+    with rns.RnsPlan(rlib, cfg) as plan:
+        plan.prepare(stream, in_place=in_place)
+        plan.execute(x, y, stream)
         torch.cuda.synchronize()
         info = plan.info()
     return to_host(torch, y, np.uint64), info
@@ -55,13 +56,13 @@ def test_c4_full_size_round_trip(torch_gpu, rlib):
     roots = [oracle.find_primitive_root(log_n + 1, q) for q in moduli]
     x = np.stack([workloads.ntt_input(log_n, 1, q, seed=1, channel=i)[0] for i, q in enumerate(moduli)])
     stream = torch_gpu.cuda.Stream()
-    fwd_cfg = rns.config(log_n, list(zip(moduli, roots)))
-    got, info = run(torch_gpu, rlib, fwd_cfg, x.ravel(), x.size, rns.Placement.SEPARATE, stream)
+    fwd_cfg = rns.request(log_n, list(zip(moduli, roots)))
+    got, info = run(torch_gpu, rlib, fwd_cfg, x.ravel(), x.size, False, stream)
     expected = oracle.rns(x, moduli, roots, output_bit_reversed=True, threads=oracle.default_threads())
     np.testing.assert_array_equal(got.reshape(32, n), expected)
     assert info["prepared"] and info["placement"] == "separate"
-    inv_cfg = rns.config(log_n, list(zip(moduli, roots)), inverse=True)
-    back, _ = run(torch_gpu, rlib, inv_cfg, got, x.size, rns.Placement.IN_PLACE, stream)
+    inv_cfg = rns.request(log_n, list(zip(moduli, roots)), inverse=True)
+    back, _ = run(torch_gpu, rlib, inv_cfg, got, x.size, True, stream)
     np.testing.assert_array_equal(back.reshape(32, n), x)
 
 
@@ -76,7 +77,7 @@ def reference_layout(log_n, negacyclic, inverse, in_rev, out_rev):
     slots = [(1, 3, 5), (0, 0, 2), (0, 6, 0), (1, 2, 6), (0, 5, 3)]  # (domain, input slot, output slot)
     polys = [{"domain": d, "input_offset": i * (n + 17) + 11, "output_offset": o * (n + 17) + 11}
              for d, i, o in slots]
-    cfg = rns.config(log_n, domains, polys, inverse=inverse, ring="negacyclic" if negacyclic else "cyclic",
+    cfg = rns.request(log_n, domains, polynomials=polys, inverse=inverse, ring="negacyclic" if negacyclic else "cyclic",
                      input_order="bit_reversed" if in_rev else "natural",
                      output_order="bit_reversed" if out_rev else "natural")
     words = 7 * (n + 17) + 29
@@ -108,13 +109,12 @@ def expected_layout(cfg, domains, polys, data, in_place):
 @pytest.mark.parametrize("negacyclic", [True, False])
 @pytest.mark.parametrize("inverse", [False, True])
 @pytest.mark.parametrize("in_rev,out_rev", [(False, True), (True, False), (False, False), (True, True)])
-@pytest.mark.parametrize("placement", [rns.Placement.SEPARATE, rns.Placement.IN_PLACE])
-def test_reference_layout(torch_gpu, rlib, log_n, negacyclic, inverse, in_rev, out_rev, placement):
+@pytest.mark.parametrize("in_place", [False, True])
+def test_reference_layout(torch_gpu, rlib, log_n, negacyclic, inverse, in_rev, out_rev, in_place):
     print(f"case rns layout log_n={log_n} neg={negacyclic} inv={inverse} in_rev={in_rev} "
-          f"out_rev={out_rev} placement={int(placement)}", flush=True)
+          f"out_rev={out_rev} in_place={in_place}", flush=True)
     cfg, domains, polys, data = reference_layout(log_n, negacyclic, inverse, in_rev, out_rev)
-    in_place = placement == rns.Placement.IN_PLACE
-    got, _ = run(torch_gpu, rlib, cfg, data, data.size, placement, torch_gpu.cuda.Stream())
+    got, _ = run(torch_gpu, rlib, cfg, data, data.size, in_place, torch_gpu.cuda.Stream())
     np.testing.assert_array_equal(got, expected_layout(cfg, domains, polys, data, in_place))
 
 
@@ -127,11 +127,11 @@ def test_graph_replay_matches_eager(torch_gpu, rlib):
     y = to_device(torch_gpu, np.full(data.size, SENTINEL))
     blank = y.clone()
     expected = expected_layout(cfg, domains, polys, data, False)
-    with rns.Plan(rlib, cfg) as plan:
-        plan.prepare(stream=stream.cuda_stream)
+    with rns.RnsPlan(rlib, cfg) as plan:
+        plan.prepare(stream.cuda_stream)
         graph = torch_gpu.cuda.CUDAGraph()
         with torch_gpu.cuda.graph(graph, stream=stream):
-            plan.execute(x, y, stream=stream.cuda_stream)
+            plan.execute(x, y, stream.cuda_stream)
         for _ in range(3):
             y.copy_(blank)  # eager work between replays
             torch_gpu.cuda.synchronize()
@@ -144,28 +144,28 @@ def test_graph_replay_matches_eager(torch_gpu, rlib):
 def test_prepare_cache_contract(torch_gpu, rlib, tmp_path):
     cfg, _, _, _ = reference_layout(12, True, False, False, True)
     stream = torch_gpu.cuda.Stream().cuda_stream
-    with rns.Plan(rlib, cfg) as plan:
-        with pytest.raises(rns.Error):  # REQUIRE without a record
-            plan.prepare(cache_directory=str(tmp_path), policy=rns.CachePolicy.REQUIRE, stream=stream)
-    with rns.Plan(rlib, cfg) as plan:
-        plan.prepare(cache_directory=str(tmp_path), policy=rns.CachePolicy.PREFER, stream=stream)
+    with rns.RnsPlan(rlib, cfg) as plan:
+        with pytest.raises(cb.AbiError):  # REQUIRE without a record
+            plan.prepare(stream, cache_dir=tmp_path, cache="require")
+    with rns.RnsPlan(rlib, cfg) as plan:
+        plan.prepare(stream, cache_dir=tmp_path, cache="prefer")
         first = plan.info()
         assert not first["cache_hit"] and first["kernel_ms"] > 0
-        with pytest.raises(rns.Error):
-            plan.prepare(stream=stream)  # already prepared
+        with pytest.raises(cb.AbiError):
+            plan.prepare(stream)  # already prepared
     records = list(tmp_path.glob("rns-v1-*.json"))
     assert len(records) == 1 and records[0].stem == first["cache_key"]
-    with rns.Plan(rlib, cfg) as plan:
-        plan.prepare(cache_directory=str(tmp_path), policy=rns.CachePolicy.REQUIRE, stream=stream)
+    with rns.RnsPlan(rlib, cfg) as plan:
+        plan.prepare(stream, cache_dir=tmp_path, cache="require")
         hit = plan.info()
         assert hit["cache_hit"] and hit["kernel_ms"] == first["kernel_ms"]
     # A record whose identity differs is refused, not replayed.
     record = json.loads(records[0].read_text())
     record["identity"]["placement"] = "in_place"
     records[0].write_text(json.dumps(record))
-    with rns.Plan(rlib, cfg) as plan:
-        with pytest.raises(rns.Error) as info:
-            plan.prepare(cache_directory=str(tmp_path), policy=rns.CachePolicy.PREFER, stream=stream)
+    with rns.RnsPlan(rlib, cfg) as plan:
+        with pytest.raises(cb.AbiError) as info:
+            plan.prepare(stream, cache_dir=tmp_path, cache="prefer")
         assert "identity" in str(info.value)
 
 
@@ -173,9 +173,27 @@ def test_execute_contract(torch_gpu, rlib):
     cfg, _, _, data = reference_layout(12, True, False, False, True)
     x = to_device(torch_gpu, data)
     y = to_device(torch_gpu, data)
-    with rns.Plan(rlib, cfg) as plan:
-        with pytest.raises(rns.Error):
+    with rns.RnsPlan(rlib, cfg) as plan:
+        with pytest.raises(cb.AbiError) as info:
             plan.execute(x, y)  # not prepared
-        plan.prepare(placement=rns.Placement.SEPARATE)
-        with pytest.raises(ValueError):
+        assert info.value.status == 1
+        plan.prepare()
+        with pytest.raises(cb.AbiError) as info:
             plan.execute(x, x)  # aliasing differs from the prepared placement
+        assert info.value.status == 1 and "placement" in info.value.detail
+
+
+def test_prepare_refuses_stream_capture(torch_gpu, rlib):
+    # Preparation times kernels on private buffers, which a capturing stream
+    # cannot do (reference src/rns_ntt.cu:89-94): status 1, plan unprepared.
+    cfg, _, _, data = reference_layout(12, True, False, False, True)
+    s = torch_gpu.cuda.Stream()
+    with rns.RnsPlan(rlib, cfg) as plan:
+        graph = torch_gpu.cuda.CUDAGraph()
+        with torch_gpu.cuda.graph(graph, stream=s):
+            with pytest.raises(cb.AbiError) as info:
+                plan.prepare(s.cuda_stream)
+        assert info.value.status == 1 and "capture" in info.value.detail
+        assert not plan.info()["prepared"]
+        plan.prepare(s.cuda_stream)  # outside capture it prepares normally
+        assert plan.info()["prepared"]

@@ -18,14 +18,11 @@ Q30 = 1073479681  # 2^30 - 2^18 + 1: lazy reduction fits, so strict is a candida
 
 
 def fft(log_n, batch, inverse=False):
-    return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                        extents=[1 << log_n], batch=batch, inverse=inverse)
+    return cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [1 << log_n], compute=cb.ComputeType.FP32, batch=batch, inverse=inverse)
 
 
 def ntt(log_n, batch, inverse=False):
-    return cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
-                        extents=[1 << log_n], batch=batch, modulus=Q30, word_bits=32,
-                        ring=cb.NttRing.NEGACYCLIC, inverse=inverse)
+    return cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [1 << log_n], compute=cb.ComputeType.UINT32, batch=batch, modulus=Q30, word_bits=32, ntt_ring=cb.NttRing.NEGACYCLIC, inverse=inverse)
 
 
 def measured(plan):
@@ -40,10 +37,10 @@ def records(path):
     return [line.split("\t") for line in text.splitlines()]
 
 
-def fft_ok(torch, lib, t, stream, log_n, batch, inverse, options=None):
+def fft_ok(torch, lib, t, stream, log_n, batch, inverse, **plan_args):
     rng = np.random.default_rng(log_n)
     x = (rng.standard_normal((batch, 1 << log_n)) + 1j * rng.standard_normal((batch, 1 << log_n))).astype(np.complex64)
-    got = run_plan(torch, lib, t, x, stream, options=options).astype(np.complex128)
+    got = run_plan(torch, lib, t, x, stream, **plan_args).astype(np.complex128)
     ref = oracle.fft_c64(x, inverse=inverse, normalize=inverse, threads=oracle.default_threads()).astype(np.complex128)
     err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert err <= 1e-5, err
@@ -52,7 +49,7 @@ def fft_ok(torch, lib, t, stream, log_n, batch, inverse, options=None):
 def test_measure_records_and_default_replays(torch_gpu, lib, stream, tmp_path):
     cache = tmp_path / "selection.tsv"
     t = fft(16, 8)
-    with cb.Plan(lib, t, options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE), stream=stream,
+    with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream,
                  cache_path=cache) as plan:
         assert plan.selection_source() == cb.SelectionSource.RUNTIME_MEASURED
         names = measured(plan)
@@ -71,7 +68,7 @@ def test_measure_records_and_default_replays(torch_gpu, lib, stream, tmp_path):
     with cb.Plan(lib, t, cache_path=cache) as plan:
         assert plan.algorithm_name() == other
         assert plan.selection_source() == cb.SelectionSource.USER_CACHE
-    fft_ok(torch_gpu, lib, t, stream, 16, 8, False, options=cb.PlanOptions(mapping=other))
+    fft_ok(torch_gpu, lib, t, stream, 16, 8, False, algorithm=other)
     # An unterminated final record is not replayed.
     with open(cache, "a") as f:
         f.write(f"{key}\t{chosen}")
@@ -94,17 +91,17 @@ def test_measure_records_and_default_replays(torch_gpu, lib, stream, tmp_path):
 def test_every_fft_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path, log_n, inverse):
     batch = 1 << max(0, 18 - log_n)
     t = fft(log_n, batch, inverse)
-    with cb.Plan(lib, t, options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE), stream=stream,
+    with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream,
                  cache_path=tmp_path / "c.tsv") as plan:
         names = measured(plan)
     # The static model's choice comes first: three passes from 2^23.
     assert names[0].startswith("fft-c64-three-pass-r16" if log_n >= 23 else "fft-c64-two-pass-r16")
     for name in names:
-        opts = cb.PlanOptions(policy=cb.AlgorithmPolicy.EXPLICIT, mapping=name)
-        with cb.Plan(lib, t, options=opts) as plan:
+        opts = {"algorithm": name}
+        with cb.Plan(lib, t, **opts) as plan:
             assert plan.algorithm_name() == name
             assert plan.selection_source() == cb.SelectionSource.EXPLICIT
-        fft_ok(torch_gpu, lib, t, stream, log_n, batch, inverse, options=opts)
+        fft_ok(torch_gpu, lib, t, stream, log_n, batch, inverse, **opts)
 
 
 @pytest.mark.parametrize("log_n", [10, 13, 14, 16, 17])
@@ -112,7 +109,7 @@ def test_every_fft_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path
 def test_ntt_strict_candidate(torch_gpu, lib, stream, tmp_path, log_n, inverse):
     batch = 4
     t = ntt(log_n, batch, inverse)
-    with cb.Plan(lib, t, options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE), stream=stream,
+    with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream,
                  cache_path=tmp_path / "c.tsv") as plan:
         names = measured(plan)
     # Lazy and strict; u32 two-pass lengths add 32-column tiles, the static
@@ -126,16 +123,15 @@ def test_ntt_strict_candidate(torch_gpu, lib, stream, tmp_path, log_n, inverse):
     x = rng.integers(0, 1 << 32, (batch, 1 << log_n), dtype=np.uint64).astype(np.uint32)
     expected = oracle.ntt_negacyclic(x.astype(np.uint64) % Q30, Q30, inverse=inverse).astype(np.uint32)
     for name in names:
-        opts = cb.PlanOptions(policy=cb.AlgorithmPolicy.EXPLICIT, mapping=name)
-        got = run_plan(torch_gpu, lib, t, x, stream, options=opts)
+        opts = {"algorithm": name}
+        got = run_plan(torch_gpu, lib, t, x, stream, **opts)
         np.testing.assert_array_equal(got, expected, err_msg=name)
 
 
 def test_measure_composite_children(torch_gpu, lib, stream, tmp_path):
     cache = tmp_path / "c.tsv"
-    t = cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                     extents=[64, 1 << 15], batch=1)
-    with cb.Plan(lib, t, options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE), stream=stream,
+    t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64, 1 << 15], compute=cb.ComputeType.FP32, batch=1)
+    with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream,
                  cache_path=cache) as plan:
         assert plan.selection_source() == cb.SelectionSource.RUNTIME_MEASURED
         assert plan.algorithm_name().startswith("rank2-transpose[")
@@ -145,9 +141,9 @@ def test_measure_composite_children(torch_gpu, lib, stream, tmp_path):
 
 
 def test_unknown_explicit_name_is_not_supported(torch_gpu, lib):
-    opts = cb.PlanOptions(policy=cb.AlgorithmPolicy.EXPLICIT, mapping="fft-c64-two-pass-r16-3x13")
-    with pytest.raises(cb.Error) as e:
-        cb.Plan(lib, fft(16, 1), options=opts)
+    opts = {"algorithm": "fft-c64-two-pass-r16-3x13"}
+    with pytest.raises(cb.AbiError) as e:
+        cb.Plan(lib, fft(16, 1), **opts)
     assert e.value.status == cb.Status.NOT_SUPPORTED
 
 
@@ -157,7 +153,7 @@ def test_plan_trace(torch_gpu, lib, stream, tmp_path, monkeypatch):
     import json
     trace = tmp_path / "trace.jsonl"
     monkeypatch.setenv("CUBUTTERFLY_PLAN_TRACE", str(trace))
-    with cb.Plan(lib, fft(16, 2), options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE), stream=stream,
+    with cb.Plan(lib, fft(16, 2), policy=cb.AlgorithmPolicy.MEASURE, stream=stream,
                  cache_path=tmp_path / "c.tsv") as plan:
         chosen = plan.algorithm_name()
     rows = [json.loads(line) for line in trace.read_text().splitlines()]
@@ -177,8 +173,74 @@ def test_measure_rotates_large_buffers(torch_gpu, lib, stream, tmp_path, monkeyp
     for log_n, batch, sets in ((16, 2, 1), (14, 1024, 3)):
         trace = tmp_path / f"trace{log_n}.jsonl"
         monkeypatch.setenv("CUBUTTERFLY_PLAN_TRACE", str(trace))
-        with cb.Plan(lib, fft(log_n, batch), options=cb.PlanOptions(policy=cb.AlgorithmPolicy.MEASURE),
+        with cb.Plan(lib, fft(log_n, batch), policy=cb.AlgorithmPolicy.MEASURE,
                      stream=stream, cache_path=tmp_path / "c.tsv") as plan:
             assert plan.selection_source() == cb.SelectionSource.RUNTIME_MEASURED
         rows = [json.loads(line) for line in trace.read_text().splitlines()]
         assert rows[0]["phase"] == "inventory" and rows[0]["buffer_sets"] == sets
+
+
+def _rows(flat, batch, pitch, n):
+    return np.stack([flat[b * pitch: b * pitch + n] for b in range(batch)])
+
+
+@pytest.mark.parametrize("case", ["fwht-c1p", "ntt-pitched"])
+def test_measure_of_pitched_rows_sizes_scratch_by_the_span(torch_gpu, lib, stream, tmp_path, monkeypatch, case):
+    # A pitched leaf addresses row b at b * pitch, (batch - 1) * pitch + n
+    # elements per side: MEASURE's scratch buffers must span that much, and
+    # the measured plan must compute what the EXPLICIT plan of the same
+    # lowering computes.
+    import json
+    from gpu_util import to_device, to_host
+    rng = np.random.default_rng(11)
+    if case == "fwht-c1p":
+        n, batch, pitch, dtype = 4096, 4096, 4096 + 64, np.float32
+        t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], batch, compute=cb.ComputeType.FP32,
+                        input_strides=[1], input_batch_stride=pitch, output_strides=[1], output_batch_stride=pitch)
+        x = rng.integers(-8, 9, (batch - 1) * pitch + n).astype(np.float32)
+    else:
+        n, batch, pitch, dtype = 1 << 16, 4, (1 << 16) + 256, np.uint32
+        t = cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [n], batch, compute=cb.ComputeType.UINT32,
+                        modulus=Q30, word_bits=32, ntt_ring=cb.NttRing.NEGACYCLIC, input_strides=[1],
+                        input_batch_stride=pitch, output_strides=[1], output_batch_stride=pitch)
+        x = rng.integers(0, Q30, (batch - 1) * pitch + n, dtype=np.uint64).astype(np.uint32)
+    span = x.size * x.itemsize
+    trace = tmp_path / "trace.jsonl"
+    monkeypatch.setenv("CUBUTTERFLY_PLAN_TRACE", str(trace))
+    results = {}
+    for label, args in (("measure", {"policy": cb.AlgorithmPolicy.MEASURE, "cache_path": tmp_path / "c.tsv"}),
+                        ("explicit", None)):
+        if args is None:
+            args = {"algorithm": results["measure"][0]}
+        xd = to_device(torch_gpu, x)
+        yd = torch_gpu.zeros_like(xd)
+        with cb.Plan(lib, t, stream=stream, **args) as plan:
+            assert plan.input_size() == plan.output_size() == span
+            ws = plan.workspace_size()
+            if ws:
+                plan.set_workspace(torch_gpu.empty(ws, dtype=torch_gpu.uint8, device="cuda"), ws)
+            plan.execute(xd, yd)
+            torch_gpu.cuda.synchronize()
+            results[label] = (plan.algorithm_name(), _rows(to_host(torch_gpu, yd, dtype), batch, pitch, n))
+    inventory = json.loads(trace.read_text().splitlines()[0])
+    assert inventory["phase"] == "inventory"
+    assert inventory["input_bytes"] == span and inventory["output_bytes"] == span
+    assert inventory["scratch_bytes"] >= inventory["buffer_sets"] * 2 * span
+    assert results["measure"][0].endswith("-pitched")
+    np.testing.assert_array_equal(results["measure"][1], results["explicit"][1])
+    if case == "fwht-c1p":
+        np.testing.assert_array_equal(results["explicit"][1], oracle.fwht_f32(_rows(x, batch, pitch, n), threads=16))
+    else:
+        expected = oracle.ntt_negacyclic(_rows(x, batch, pitch, n).astype(np.uint64), Q30)
+        np.testing.assert_array_equal(results["explicit"][1].astype(np.uint64), expected)
+
+
+def test_measure_refuses_stream_capture(torch_gpu, lib):
+    # MEASURE times candidates on the device, which a capturing stream cannot
+    # do: plan creation reports NOT_SUPPORTED and the capture stays valid.
+    s = torch_gpu.cuda.Stream()
+    graph = torch_gpu.cuda.CUDAGraph()
+    with torch_gpu.cuda.graph(graph, stream=s):
+        with pytest.raises(cb.AbiError) as e:
+            cb.Plan(lib, fft(16, 1), policy=cb.AlgorithmPolicy.MEASURE, stream=s.cuda_stream)
+        assert e.value.status == cb.Status.NOT_SUPPORTED and "capture" in e.value.detail
