@@ -228,8 +228,11 @@ std::string selection_key(const Request& r) {
         .field("psi", r.psi)
         .field("input_bit_reversed", r.input_bit_reversed)
         .field("output_bit_reversed", r.output_bit_reversed)
+        .field("pitched", r.pitched)
+        .field("input_batch_stride", r.pitched ? r.in_batch_stride : 0)
+        .field("output_batch_stride", r.pitched ? r.out_batch_stride : 0)
         .end_object();
-    return "cubutterfly-gfx950-selection-v1|" + device_identity() + "|" + w.str();
+    return "cubutterfly-gfx950-selection-v2|" + device_identity() + "|" + w.str();
 }
 
 std::unique_ptr<Executor> build_leaf(const Request& r) {
@@ -278,20 +281,29 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     hip_check(hipStreamIsCapturing(sel->stream, &capture), "MEASURE capture query");
     supported(capture == hipStreamCaptureStatusNone, "MEASURE cannot time candidates during stream capture");
+    // Scratch sides span what the kernels address: a pitched leaf reads and
+    // writes row b at b * batch stride, up to (batch - 1) * pitch + n elements.
+    const std::size_t in_bytes = r.in_place ? std::max(r.span_bytes(true), r.span_bytes(false)) : r.span_bytes(true);
+    const std::size_t out_bytes = r.in_place ? 0 : r.span_bytes(false);
+    const std::size_t footprint = in_bytes + out_bytes;
     // Buffer sets: transforms of 16 MiB or more rotate over enough sets that
-    // inputs and outputs together exceed twice the 256 MB Infinity Cache (at
-    // most 8 sets, so below 32 MiB part of the data stays cached), so
-    // candidates are timed at HBM speed as in steady use over large data,
-    // not on cache-resident buffers.
-    const std::size_t bytes = r.data_bytes();
+    // their footprint exceeds twice the 256 MB Infinity Cache (at most 8
+    // sets, so below 32 MiB part of the data stays cached), so candidates
+    // are timed at HBM speed as in steady use over large data. The search
+    // stays within max(512 MiB, min(2 GiB, free / 4)) of scratch (the
+    // reference's tuning budget); beyond it, fewer sets.
     constexpr std::size_t kCacheBytes = std::size_t{256} << 20;
-    const std::size_t sets =
-        bytes >= (std::size_t{16} << 20) ? std::min<std::size_t>(8, kCacheBytes / bytes + 1) : 1;  // sets x 2 bytes > 2 x cache
+    std::size_t sets = r.data_bytes() >= (std::size_t{16} << 20)
+                           ? std::min<std::size_t>(8, (2 * kCacheBytes) / footprint + 1)
+                           : 1;
+    std::size_t free_bytes = 0, total_bytes = 0;
+    if (hipMemGetInfo(&free_bytes, &total_bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        free_bytes = 0;
+    }
+    const std::size_t budget = std::max(std::size_t{512} << 20, std::min(std::size_t{2} << 30, free_bytes / 4));
     SearchTrace trace;
     const auto names = leaf_candidates(r);
-    trace.event("inventory", "\"key\":" + json::quote(key) + ",\"candidate_count\":" + std::to_string(names.size()) +
-                                 ",\"timing_protocol\":\"event-loop\",\"warmup\":3,\"repeat\":20,"
-                                 "\"buffer_sets\":" + std::to_string(sets));
     std::vector<std::unique_ptr<Executor>> built;
     std::size_t ws_bytes = 0;
     for (const auto& name : names) {
@@ -306,20 +318,37 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
         }
     }
     require(!built.empty(), "no candidate lowering to measure");
+    while (sets > 1 && sets * footprint + ws_bytes > budget) --sets;
+    trace.event("inventory", "\"key\":" + json::quote(key) + ",\"candidate_count\":" + std::to_string(names.size()) +
+                                 ",\"timing_protocol\":\"event-loop\",\"warmup\":3,\"repeat\":20," +
+                                 "\"buffer_sets\":" + std::to_string(sets) + ",\"input_bytes\":" +
+                                 std::to_string(in_bytes) + ",\"output_bytes\":" + std::to_string(out_bytes) +
+                                 ",\"workspace_bytes\":" + std::to_string(ws_bytes) + ",\"scratch_bytes\":" +
+                                 std::to_string(sets * footprint + ws_bytes));
     std::vector<DeviceScratch> in, out;
-    in.reserve(sets);
-    out.reserve(sets);
-    for (std::size_t k = 0; k < sets; ++k) {
-        in.emplace_back(bytes);
-        out.emplace_back(r.in_place ? 0 : bytes);
-        hip_check(hipMemsetAsync(in.back().ptr, 0, bytes, sel->stream), "MEASURE input fill");
+    std::unique_ptr<DeviceScratch> ws;
+    try {
+        in.reserve(sets);
+        out.reserve(sets);
+        for (std::size_t k = 0; k < sets; ++k) {
+            in.emplace_back(in_bytes);
+            out.emplace_back(out_bytes);
+            hip_check(hipMemsetAsync(in.back().ptr, 0, in_bytes, sel->stream), "MEASURE input fill");
+        }
+        ws = std::make_unique<DeviceScratch>(ws_bytes);
+    } catch (const std::bad_alloc&) {
+        // Not enough device memory to time the candidates: keep the static
+        // model's lowering and say so, instead of failing the plan.
+        trace.event("selected", "\"algorithm\":null,\"reason\":\"scratch allocation failed\"");
+        note(*sel, "MEASURE skipped: could not allocate " + std::to_string(sets * footprint + ws_bytes) +
+                       " bytes of scratch; static model used");
+        return build_leaf(r);
     }
-    DeviceScratch ws(ws_bytes);
     std::size_t best = 0;
     double best_ms = std::numeric_limits<double>::infinity();
     std::string results;
     for (std::size_t i = 0; i < built.size(); ++i) {
-        const double ms = time_executor(*built[i], in, out, r.in_place, ws.ptr, sel->stream);
+        const double ms = time_executor(*built[i], in, out, r.in_place, ws->ptr, sel->stream);
         char text[64];
         std::snprintf(text, sizeof text, "=%.4f ms", ms);
         results += (i ? ", " : "") + built[i]->algorithm + text;
