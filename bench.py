@@ -1,23 +1,31 @@
 #!/usr/bin/env python3
-"""Headline benchmark of the MI355X butterfly path (one GPU).
+"""Benchmark of the MI355X butterfly path (one GPU): every BASELINE configuration.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c1p|c2|c3a|c3b|c4|c5a|c5b|r2|copy]
-                [--no-cpu] [--verify] [--eager] [--mapping LOWERING]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|c1|c2|c3a|c3b|c4|c5a|c5b|c1p|r2|copy]
+                [--headline c5a] [--no-cpu] [--verify] [--eager] [--mapping LOWERING]
 
-A step is one call of the hot path over one batch of the named BASELINE
-configuration, with inputs already resident in HBM. W untimed steps, then K
-timed steps bracketed by torch.cuda.synchronize(); the timed calls rotate over
-enough input/output buffer sets (> 256 MiB in total) that the 256 MB Infinity
-Cache cannot serve them. Rank 0 prints ONE JSON line with the driver's fields
-plus `roofline` (algorithmic bytes per call / measured call time vs 8 TB/s HBM)
-and `cpu_baseline` (the CPU oracle -- a restatement of the reference CPU path --
-timed on this host over a bounded sample of the same workload).
---mapping plans the workload with the EXPLICIT policy and the named lowering
-(c1, c1p, c2 and the one-plan workloads), for comparing lowerings.
+A step is one call of the hot path over one batch of a BASELINE configuration
+(C2 and C4: forward then inverse), inputs already resident in HBM. Per
+configuration: W untimed eager calls, then a HIP graph of 20 calls captured and
+replayed R = max(7, ceil(K / 20)) times back to back, each replay bracketed by
+HIP events on the plans' stream; the time per call is the MEDIAN replay / 20
+(the reference's protocol: 10 warmups, a graph of 20 calls, median of 7
+replays). The calls rotate over buffer sets larger than twice the 256 MB
+Infinity Cache, so inputs come from HBM.
+
+The default runs all seven BASELINE configurations. Rank 0 prints ONE JSON
+line: the driver's fields for the headline configuration (--headline, default
+C5a, one of the largest single-GPU configurations at 268 MB per call) plus
+`per_config`, one entry per configuration with its roofline (algorithmic
+bytes per call / median call time against 8 TB/s HBM, and the HBM traffic
+counted by rocprofv3 for it) and its CPU baseline: the CPU oracle -- a C
+restatement of the reference CPU path -- timed on this host at 1 thread and
+at all threads, median of 7 bounded runs after one warmup.
 """
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -29,24 +37,45 @@ sys.path.insert(0, ROOT)
 METRIC = "transforms/s + achieved HBM GB/s (% of peak) per operator, 1x MI355X"
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
+CALLS_PER_GRAPH = 20
+MIN_REPLAYS = 7
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5a", "c5b"]
+DEFAULT_HEADLINE = "c5a"
+
+# VALU instructions per radix-2 butterfly of the NTT pass kernels, all work
+# of a pass included (loads, twiddle chunks, exchanges): rocprofv3
+# SQ_INSTS_VALU per dispatch divided by the dispatch's butterflies / 64,
+# summed over the passes of one call. With 256 CUs x 64 lanes x 2.4 GHz this
+# gives the integer-VALU roof that binds the NTT configurations before HBM.
+VALU_LANE_OPS_PER_S = 256 * 64 * 2.4e9
 
 
-def _np_to_torch(torch, a):
-    if a.dtype == np.uint32:
-        a = a.view(np.int32)
-    elif a.dtype == np.uint64:
-        a = a.view(np.int64)
-    return torch.from_numpy(np.ascontiguousarray(a))
+def _device_copy(torch, a):
+    view = a.view(np.int32) if a.dtype == np.uint32 else a.view(np.int64) if a.dtype == np.uint64 else a
+    return torch.from_numpy(np.ascontiguousarray(view)).to("cuda")
+
+
+def _rotation(bytes_per_set):
+    """Buffer sets so that the rotated footprint exceeds twice the Infinity Cache."""
+    return max(3, -(-2 * MALL_BYTES // max(1, bytes_per_set)))
 
 
 class Workload:
-    """One BASELINE configuration: plans, resident buffers, a call, its bytes."""
+    """One configuration: plans, rotated device buffers, a call, its bytes,
+    and the CPU oracle over a slice of its rows."""
 
     name = ""
     dtype = ""
     description = ""
     transforms_per_call = 0
     bytes_per_call = 0  # algorithmic: compulsory input read + output write
+    rows = 0            # independent transforms (rows / limbs) in one batch
+    mapping = None      # --mapping: plan with this lowering (EXPLICIT)
+    takes_mapping = True
+
+    def plan_args(self):
+        return {"algorithm": self.mapping} if self.mapping else {}
 
     def setup(self, torch, lib, stream):
         raise NotImplementedError
@@ -54,141 +83,126 @@ class Workload:
     def call(self, index):
         raise NotImplementedError
 
-    def cpu_sample(self, threads):
-        """Returns (seconds, transforms, description) for a bounded CPU run."""
+    def cpu_run(self, rows, threads):
+        """Runs the reference CPU path over the first `rows` rows; returns
+        the transforms computed."""
         raise NotImplementedError
-
-    def config(self):
-        return {"workload": self.description}
 
     def kernel_name(self):
         return self.plans[0].algorithm_name()
 
-    # --mapping: a lowering name to plan with the EXPLICIT policy, for the
-    # workloads whose setup honours it (one plan per call).
-    mapping = None
-    takes_mapping = False
+    def _bind_workspace(self, torch, plans):
+        need = max(p.workspace_size() for p in plans)
+        if need:
+            self.workspace = torch.empty(need, dtype=torch.uint8, device="cuda")
+            for p in plans:
+                if p.workspace_size():
+                    p.set_workspace(self.workspace, need)
 
-    def plan_options(self, cb):
-        return cb.PlanOptions(policy=cb.AlgorithmPolicy.EXPLICIT, mapping=self.mapping) if self.mapping else None
+    def _rotate(self, torch, src, bytes_per_set, extra=()):
+        sets = _rotation(bytes_per_set)
+        self.inputs = [src.clone() for _ in range(sets)]
+        self.outputs = [torch.empty_like(src) for _ in range(sets)]
+        for name in extra:
+            setattr(self, name, [torch.empty_like(src) for _ in range(sets)])
 
-    def _rotation(self, torch, bytes_per_set):
-        return max(3, -(-2 * MALL_BYTES // max(1, bytes_per_set)))
 
+class OnePlan(Workload):
+    """A configuration served by one plan over packed rows."""
 
-class FwhtFp32(Workload):
-    name = "c1"
-    dtype = "f32"
-    takes_mapping = True
-    description = "FWHT fp32 unnormalized forward, batch 4096 x n=4096, integer inputs in [-8,8]"
+    def descriptor(self, cb):
+        raise NotImplementedError
 
-    def __init__(self, log_n=12, batch=4096):
-        self.log_n, self.batch = log_n, batch
-        self.transforms_per_call = batch
-        self.bytes_per_call = 2 * batch * (4 << log_n)
+    def make_host(self):
+        raise NotImplementedError
 
     def setup(self, torch, lib, stream):
         import cubutterfly_amd as cb
-        from cubutterfly_amd import workloads
-        t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                         extents=[1 << self.log_n], batch=self.batch)
-        self.plans = [cb.Plan(lib, t, options=self.plan_options(cb), stream=stream)]
-        host = workloads.fwht_integer_input(self.log_n, self.batch, seed=1)
-        self.host = host
-        sets = self._rotation(torch, self.bytes_per_call)
-        src = _np_to_torch(torch, host).to("cuda")
-        self.inputs = [src.clone() for _ in range(sets)]
-        self.outputs = [torch.empty_like(src) for _ in range(sets)]
+        self.plans = [cb.Plan(lib, self.descriptor(cb), stream=stream, **self.plan_args())]
+        self._bind_workspace(torch, self.plans)
+        self.host = self.make_host()
+        self._rotate(torch, _device_copy(torch, self.host), self.bytes_per_call)
 
     def call(self, index):
         k = index % len(self.inputs)
         self.plans[0].execute(self.inputs[k], self.outputs[k])
 
-    def verify(self, torch):
+
+class FwhtFp32(OnePlan):
+    name, dtype = "c1", "f32"
+    description = "C1: FWHT fp32 unnormalized forward, batch 4096 x n=4096, integer inputs in [-8,8]"
+
+    def __init__(self, log_n=12, batch=4096):
+        self.log_n, self.rows = log_n, batch
+        self.transforms_per_call = batch
+        self.bytes_per_call = 2 * batch * (4 << log_n)
+
+    def descriptor(self, cb):
+        return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << self.log_n], self.rows,
+                           compute=cb.ComputeType.FP32)
+
+    def make_host(self):
+        from cubutterfly_amd import workloads
+        return workloads.fwht_integer_input(self.log_n, self.rows, seed=1)
+
+    def verify(self):
         import oracle
         got = self.outputs[0].cpu().numpy()
         return bool(np.array_equal(got, oracle.fwht_f32(self.host, threads=oracle.default_threads())))
 
-    def cpu_sample(self, threads):
+    def cpu_run(self, rows, threads):
         import oracle
-        reps, elapsed = 0, 0.0
-        while elapsed < 10.0:
-            t0 = time.perf_counter()
-            oracle.fwht_f32(self.host, threads=threads)
-            elapsed += time.perf_counter() - t0
-            reps += 1
-        return elapsed, reps * self.batch, f"{reps} full C1 batches (4096 x 4096) through reference_fwht"
+        oracle.fwht_f32(self.host[:rows], threads=threads)
+        return rows
 
 
 class FwhtFp32Pitched(FwhtFp32):
-    """C1's transform on pitched rows (row stride n + 64 on both sides): the
-    FWHT kernel reads and writes the pitched rows directly."""
+    """C1's transform on rows pitched by n + 64 on both sides (not a BASELINE
+    line): the FWHT kernel reads and writes the pitched rows directly."""
     name = "c1p"
-    description = ("FWHT fp32 unnormalized forward, batch 4096 x n=4096, rows pitched at n + 64 on both sides "
-                   "(pitched-row FWHT kernel), integer inputs in [-8,8]")
+    description = "C1 on rows pitched at n + 64 elements on both sides (pitched-row FWHT kernel)"
     PAD = 64
+
+    def descriptor(self, cb):
+        n = 1 << self.log_n
+        pitch = n + self.PAD
+        return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], self.rows, compute=cb.ComputeType.FP32,
+                           input_strides=[1], input_batch_stride=pitch, output_strides=[1],
+                           output_batch_stride=pitch)
 
     def setup(self, torch, lib, stream):
         import cubutterfly_amd as cb
         from cubutterfly_amd import workloads
         n = 1 << self.log_n
         pitch = n + self.PAD
-        t = cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP32, compute=cb.ComputeType.FP32,
-                         extents=[n], batch=self.batch, input_strides=[1], input_batch_stride=pitch,
-                         output_strides=[1], output_batch_stride=pitch)
-        plan = cb.Plan(lib, t, options=self.plan_options(cb), stream=stream)
-        ws = plan.workspace_size()
-        if ws:
-            self.workspace = torch.empty(ws, dtype=torch.uint8, device="cuda")
-            plan.set_workspace(self.workspace, ws)
-        self.plans = [plan]
-        self.host = workloads.fwht_integer_input(self.log_n, self.batch, seed=1)
-        padded = np.zeros((self.batch, pitch), dtype=np.float32)
+        self.plans = [cb.Plan(lib, self.descriptor(cb), stream=stream, **self.plan_args())]
+        self._bind_workspace(torch, self.plans)
+        self.host = workloads.fwht_integer_input(self.log_n, self.rows, seed=1)
+        padded = np.zeros((self.rows, pitch), dtype=np.float32)
         padded[:, :n] = self.host
-        flat = padded.reshape(-1)[: (self.batch - 1) * pitch + n]
-        sets = self._rotation(torch, self.bytes_per_call)
-        src = _np_to_torch(torch, np.ascontiguousarray(flat)).to("cuda")
-        self.inputs = [src.clone() for _ in range(sets)]
-        self.outputs = [torch.zeros_like(src) for _ in range(sets)]
+        flat = padded.reshape(-1)[: (self.rows - 1) * pitch + n]
+        self._rotate(torch, _device_copy(torch, flat), self.bytes_per_call)
 
-    def verify(self, torch):
+    def verify(self):
         import oracle
         n, pitch = 1 << self.log_n, (1 << self.log_n) + self.PAD
         flat = self.outputs[0].cpu().numpy()
-        got = np.zeros((self.batch, pitch), dtype=np.float32).reshape(-1)
+        got = np.zeros(self.rows * pitch, dtype=np.float32)
         got[: flat.size] = flat
-        got = got.reshape(self.batch, pitch)[:, :n]
+        got = got.reshape(self.rows, pitch)[:, :n]
         return bool(np.array_equal(got, oracle.fwht_f32(self.host, threads=oracle.default_threads())))
-
-    def kernel_name(self):
-        name = self.plans[0].algorithm_name()
-        kernel = ("fwht_wide_kernel" if "-r32" in name else
-                  "fwht_pitched_kernel" if name.endswith("-pitched") else "fwht_resident_kernel")
-        return kernel + " (inside " + name + ")"
-
-
-# VALU instructions per radix-2 butterfly of the NTT pass kernels, all work
-# of a pass included (loads, twiddle chunks, exchanges): rocprofv3
-# SQ_INSTS_VALU per dispatch divided by the dispatch's butterflies / 64,
-# summed over the four passes of one call (u32 lazy: 8.6; u64 lazy: 26.1).
-# With 256 CUs x 64 lanes x 2.4 GHz this gives the integer-VALU roof that
-# binds the NTT configs before HBM does.
-VALU_LANE_OPS_PER_S = 256 * 64 * 2.4e9
 
 
 class NttNegacyclic(Workload):
     """C2: forward then inverse negacyclic NTT, u32, q = 1073479681, n = 2^16, batch 64."""
-    name = "c2"
-    dtype = "u32"
-    description = ("single-prime negacyclic NTT u32, n=2^16, batch 64, q=1073479681 (30-bit, q = 1 mod 2n); "
+    name, dtype = "c2", "u32"
+    description = ("C2: single-prime negacyclic NTT u32, n=2^16, batch 64, q=1073479681 (30-bit, q = 1 mod 2n); "
                    "one step = forward then inverse of the batch")
-
     valu_per_butterfly = 8.6
-    takes_mapping = True  # both plans (the lowering names do not depend on the direction)
 
     def __init__(self, log_n=16, batch=64):
         from cubutterfly_amd import workloads
-        self.log_n, self.batch, self.q = log_n, batch, workloads.C2_MODULUS
+        self.log_n, self.rows, self.q = log_n, batch, workloads.C2_MODULUS
         self.transforms_per_call = 2 * batch  # forward + inverse transforms
         self.bytes_per_call = 2 * 2 * batch * (4 << log_n)
         self.butterflies_per_call = self.transforms_per_call * (1 << (log_n - 1)) * log_n
@@ -198,30 +212,23 @@ class NttNegacyclic(Workload):
         from cubutterfly_amd import workloads
 
         def plan(inverse):
-            t = cb.Transform(op=cb.Operator.NTT, storage=cb.DataType.UINT32, compute=cb.ComputeType.UINT32,
-                             extents=[1 << self.log_n], batch=self.batch, modulus=self.q, word_bits=32,
-                             inverse=inverse, ring=cb.NttRing.NEGACYCLIC)
-            return cb.Plan(lib, t, options=self.plan_options(cb), stream=stream)
+            d = cb.describe(cb.Operator.NTT, cb.DataType.UINT32, [1 << self.log_n], self.rows,
+                            compute=cb.ComputeType.UINT32, modulus=self.q, word_bits=32, inverse=inverse,
+                            ntt_ring=cb.NttRing.NEGACYCLIC)
+            return cb.Plan(lib, d, stream=stream, **self.plan_args())
 
         self.plans = [plan(False), plan(True)]
-        ws_bytes = max(p.workspace_size() for p in self.plans)
-        self.workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
-        for p in self.plans:
-            if p.workspace_size():
-                p.set_workspace(self.workspace, ws_bytes)
-        self.host = workloads.ntt_input(self.log_n, self.batch, self.q, seed=1).astype(np.uint32)
-        src = _np_to_torch(torch, self.host).to("cuda")
-        sets = self._rotation(torch, 3 * src.numel() * 4)
-        self.inputs = [src.clone() for _ in range(sets)]
-        self.spectra = [torch.empty_like(src) for _ in range(sets)]
-        self.outputs = [torch.empty_like(src) for _ in range(sets)]
+        self._bind_workspace(torch, self.plans)
+        self.host = workloads.ntt_input(self.log_n, self.rows, self.q, seed=1).astype(np.uint32)
+        src = _device_copy(torch, self.host)
+        self._rotate(torch, src, 3 * src.numel() * 4, extra=("spectra",))
 
     def call(self, index):
         k = index % len(self.inputs)
         self.plans[0].execute(self.inputs[k], self.spectra[k])
         self.plans[1].execute(self.spectra[k], self.outputs[k])
 
-    def verify(self, torch):
+    def verify(self):
         import oracle
         spectrum = self.spectra[0].cpu().numpy().view(np.uint32).astype(np.uint64)
         back = self.outputs[0].cpu().numpy().view(np.uint32)
@@ -231,32 +238,25 @@ class NttNegacyclic(Workload):
     def kernel_name(self):
         return self.plans[0].algorithm_name() + " (forward) + inverse"
 
-    def cpu_sample(self, threads):
+    def cpu_run(self, rows, threads):
         import oracle
-        x = self.host.astype(np.uint64)
-        reps, elapsed = 0, 0.0
-        while elapsed < 10.0:
-            t0 = time.perf_counter()
-            y = oracle.ntt_negacyclic(x, self.q, threads=threads)
-            oracle.ntt_negacyclic(y, self.q, inverse=True, threads=threads)
-            elapsed += time.perf_counter() - t0
-            reps += 1
-        return elapsed, reps * 2 * self.batch, (f"{reps} full C2 steps (64 x 2^16 forward + inverse) through the "
-                                                "crypto-benchmark composition: psi twist + reference_ntt DIT")
+        y = oracle.ntt_negacyclic(self.host[:rows].astype(np.uint64), self.q, threads=threads)
+        oracle.ntt_negacyclic(y, self.q, inverse=True, threads=threads)
+        return 2 * rows
 
 
 class RnsNegacyclic(Workload):
     """C4: RNS negacyclic NTT, 32 limbs x n = 2^16 of 60-bit primes, forward
     (natural -> bit-reversed) then inverse (bit-reversed -> natural)."""
-    name = "c4"
-    dtype = "u64"
-    description = ("RNS negacyclic NTT u64, n=2^16, 32 limbs of distinct 60-bit primes (q = 1 mod 2^17), "
+    name, dtype = "c4", "u64"
+    description = ("C4: RNS negacyclic NTT u64, n=2^16, 32 limbs of distinct 60-bit primes (q = 1 mod 2^17), "
                    "one step = forward (natural->bit_reversed) then inverse (bit_reversed->natural)")
-
     valu_per_butterfly = 26.1
+    takes_mapping = False
+
     def __init__(self, log_n=16, limbs=32):
         from cubutterfly_amd import workloads
-        self.log_n, self.limbs = log_n, limbs
+        self.log_n, self.rows = log_n, limbs
         self.moduli = workloads.c4_moduli()[:limbs]
         self.transforms_per_call = 2 * limbs
         self.bytes_per_call = 2 * 2 * limbs * (8 << log_n)
@@ -264,30 +264,26 @@ class RnsNegacyclic(Workload):
 
     def setup(self, torch, lib, stream):
         from cubutterfly_amd import ntt_roots, rns, workloads
-        rlib = rns.Library()
         # psi_i: the reference's rule, smallest-candidate primitive 2n-th root.
         self.roots = [ntt_roots.primitive_root(self.log_n + 1, q) for q in self.moduli]
         domains = list(zip(self.moduli, self.roots))
         self.plans = []
         for inverse in (False, True):
-            plan = rns.Plan(rlib, rns.config(self.log_n, domains, inverse=inverse))
-            plan.prepare(placement=rns.Placement.SEPARATE, stream=stream, repetitions=3)
+            plan = rns.RnsPlan(lib, rns.request(self.log_n, domains, inverse=inverse))
+            plan.prepare(stream, repetitions=3)
             self.plans.append(plan)
         self.stream = stream
         self.host = np.stack([workloads.ntt_input(self.log_n, 1, q, seed=1, channel=i)[0]
                               for i, q in enumerate(self.moduli)])
-        src = _np_to_torch(torch, self.host).to("cuda")
-        sets = self._rotation(torch, 3 * src.numel() * 8)
-        self.inputs = [src.clone() for _ in range(sets)]
-        self.spectra = [torch.empty_like(src) for _ in range(sets)]
-        self.outputs = [torch.empty_like(src) for _ in range(sets)]
+        src = _device_copy(torch, self.host)
+        self._rotate(torch, src, 3 * src.numel() * 8, extra=("spectra",))
 
     def call(self, index):
         k = index % len(self.inputs)
-        self.plans[0].execute(self.inputs[k], self.spectra[k], stream=self.stream)
-        self.plans[1].execute(self.spectra[k], self.outputs[k], stream=self.stream)
+        self.plans[0].execute(self.inputs[k], self.spectra[k], self.stream)
+        self.plans[1].execute(self.spectra[k], self.outputs[k], self.stream)
 
-    def verify(self, torch):
+    def verify(self):
         import oracle
         spectrum = self.spectra[0].cpu().numpy().view(np.uint64)
         back = self.outputs[0].cpu().numpy().view(np.uint64)
@@ -298,57 +294,13 @@ class RnsNegacyclic(Workload):
     def kernel_name(self):
         return self.plans[0].info()["mapping"]["algorithm"] + " (forward) + inverse"
 
-    def cpu_sample(self, threads):
+    def cpu_run(self, rows, threads):
         import oracle
-        reps, elapsed = 0, 0.0
-        while elapsed < 10.0:
-            t0 = time.perf_counter()
-            y = oracle.rns(self.host, self.moduli, self.roots, output_bit_reversed=True, threads=threads)
-            oracle.rns(y, self.moduli, self.roots, inverse=True, input_bit_reversed=True, threads=threads)
-            elapsed += time.perf_counter() - t0
-            reps += 1
-        return elapsed, reps * 2 * self.limbs, (f"{reps} full C4 steps (32 limbs x 2^16 forward + inverse) through "
-                                                "the reference RNS oracle (tests/test_rns_ntt.cu:62-111)")
-
-
-class OnePlan(Workload):
-    """A configuration served by one plan: host input -> rotated device sets."""
-
-    elem_bytes = 0
-
-    def transform(self, cb):
-        raise NotImplementedError
-
-    def make_host(self):
-        raise NotImplementedError
-
-    takes_mapping = True
-
-    def setup(self, torch, lib, stream):
-        import cubutterfly_amd as cb
-        self.plans = [cb.Plan(lib, self.transform(cb), options=self.plan_options(cb), stream=stream)]
-        ws_bytes = self.plans[0].workspace_size()
-        if ws_bytes:
-            self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
-            self.plans[0].set_workspace(self.workspace, ws_bytes)
-        self.host = self.make_host()
-        src = _np_to_torch(torch, self.host).to("cuda")
-        sets = self._rotation(torch, self.bytes_per_call)
-        self.inputs = [src.clone() for _ in range(sets)]
-        self.outputs = [torch.empty_like(src) for _ in range(sets)]
-
-    def call(self, index):
-        k = index % len(self.inputs)
-        self.plans[0].execute(self.inputs[k], self.outputs[k])
-
-    def timed_cpu(self, fn, what):
-        reps, elapsed = 0, 0.0
-        while elapsed < 10.0:
-            t0 = time.perf_counter()
-            fn()
-            elapsed += time.perf_counter() - t0
-            reps += 1
-        return elapsed, reps * self.transforms_per_call, f"{reps} full batches ({what})"
+        y = oracle.rns(self.host[:rows], self.moduli[:rows], self.roots[:rows], output_bit_reversed=True,
+                       threads=threads)
+        oracle.rns(y, self.moduli[:rows], self.roots[:rows], inverse=True, input_bit_reversed=True,
+                   threads=threads)
+        return 2 * rows
 
 
 class FftC64(OnePlan):
@@ -356,58 +308,55 @@ class FftC64(OnePlan):
     dtype = "c64"
 
     def __init__(self, log_n, batch):
-        self.log_n, self.batch = log_n, batch
+        self.log_n, self.rows = log_n, batch
         self.name = "c3a" if batch == 1 else "c3b"
-        self.description = f"complex FFT c64 forward, batch {batch} x n=2^{log_n}, N(0,1) real and imaginary parts"
+        self.description = (f"{self.name.upper()}: complex FFT c64 forward, batch {batch} x n=2^{log_n}, "
+                            "N(0,1) real and imaginary parts")
         self.transforms_per_call = batch
         self.bytes_per_call = 2 * batch * (8 << log_n)
 
-    def transform(self, cb):
-        return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                            extents=[1 << self.log_n], batch=self.batch)
+    def descriptor(self, cb):
+        return cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [1 << self.log_n], self.rows,
+                           compute=cb.ComputeType.FP32)
 
     def make_host(self):
         from cubutterfly_amd import workloads
-        return workloads.complex_input(self.log_n, self.batch, seed=3).reshape(self.batch, 1 << self.log_n)
+        return workloads.complex_input(self.log_n, self.rows, seed=3).reshape(self.rows, 1 << self.log_n)
 
-    def verify(self, torch):
+    def verify(self):
+        import oracle
         got = self.outputs[0].cpu().numpy().astype(np.complex128)
-        ref = np.fft.fft(self.host.astype(np.complex128), axis=-1)
+        ref = oracle.fft_c64(self.host, threads=oracle.default_threads()).astype(np.complex128)
         err = np.linalg.norm(got - ref, axis=-1) / np.linalg.norm(ref, axis=-1)
         return bool(np.max(err) <= 1e-5)
 
-    def cpu_sample(self, threads):
+    def cpu_run(self, rows, threads):
         import oracle
-        return self.timed_cpu(lambda: oracle.fft_c64(self.host, threads=threads),
-                              f"{self.batch} x 2^{self.log_n} through reference_fft, iterative radix-2")
+        oracle.fft_c64(self.host[:rows], threads=threads)
+        return rows
 
 
 class FftC64Rank2(FftC64):
-    """Rank-2 complex64 FFT, 4096 x 4096 (not a BASELINE line): the composite
-    plan (row transforms, tiled transposes, column transforms)."""
+    """Rank-2 complex64 FFT, 4096 x 4096 (not a BASELINE line)."""
 
     def __init__(self):
         super().__init__(24, 1)
         self.name = "r2"
         self.description = "rank-2 complex FFT c64 forward, 4096 x 4096, batch 1, N(0,1) parts"
 
-    def transform(self, cb):
-        return cb.Transform(op=cb.Operator.FFT, storage=cb.DataType.COMPLEX_FP32, compute=cb.ComputeType.FP32,
-                            extents=[4096, 4096], batch=1)
+    def descriptor(self, cb):
+        return cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [4096, 4096], 1, compute=cb.ComputeType.FP32)
 
-    def verify(self, torch):
+    def verify(self):
         got = self.outputs[0].cpu().numpy().reshape(4096, 4096).astype(np.complex128)
         ref = np.fft.fft2(self.host.reshape(4096, 4096).astype(np.complex128))
         return bool(np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5)
 
-    def cpu_sample(self, threads):
+    def cpu_run(self, rows, threads):
         import oracle
-
-        def both_axes():
-            rows = oracle.fft_c64(self.host.reshape(4096, 4096), threads=threads)
-            oracle.fft_c64(np.ascontiguousarray(rows.T), threads=threads)
-
-        return self.timed_cpu(both_axes, "4096 x 4096 through reference_fft along both axes")
+        first = oracle.fft_c64(self.host.reshape(4096, 4096), threads=threads)
+        oracle.fft_c64(np.ascontiguousarray(first.T), threads=threads)
+        return 1
 
 
 class FwhtFp16(OnePlan):
@@ -418,46 +367,43 @@ class FwhtFp16(OnePlan):
     def __init__(self, rows, n):
         self.rows, self.n = rows, n
         self.name = "c5a" if n == 4096 else "c5b"
-        self.description = (f"FWHT fp16 storage / fp32 compute, {rows} x n={n}, output scale 1/sqrt(n), "
-                            "final-storage rounding, activations with outlier channels")
+        self.description = (f"{self.name.upper()}: FWHT fp16 storage / fp32 compute, {rows} x n={n}, output scale "
+                            "1/sqrt(n), final-storage rounding, N(0,1) activations with x50 outlier channels")
         self.transforms_per_call = rows
         self.bytes_per_call = 2 * rows * n * 2
         self.scale = float(np.float32(1.0 / np.sqrt(n)))
 
-    def transform(self, cb):
-        return cb.Transform(op=cb.Operator.FWHT, storage=cb.DataType.FP16, compute=cb.ComputeType.FP32,
-                            extents=[self.n], batch=self.rows, output_scale=self.scale,
-                            output_rounding=cb.OutputRounding.FINAL_STORAGE)
+    def descriptor(self, cb):
+        return cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [self.n], self.rows, compute=cb.ComputeType.FP32,
+                           output_scale=self.scale, output_rounding=cb.OutputRounding.FINAL_STORAGE)
 
     def make_host(self):
         from cubutterfly_amd import workloads
         return workloads.quarot_input(self.rows, self.n, seed=5)
 
-    def verify(self, torch):
+    def verify(self):
         import oracle
         got = self.outputs[0].cpu().numpy().view(np.float16).astype(np.float32)
         ref = oracle.fwht_f16_final(self.host, self.scale, threads=oracle.default_threads()).astype(np.float32)
         return bool(np.max(np.abs(got - ref)) <= 2e-3)
 
-    def cpu_sample(self, threads):
+    def cpu_run(self, rows, threads):
         import oracle
-        return self.timed_cpu(lambda: oracle.fwht_f16_final(self.host, self.scale, threads=threads),
-                              f"{self.rows} x {self.n} through reference_fwht in fp32 + one fp16 rounding")
+        oracle.fwht_f16_final(self.host[:rows], self.scale, threads=threads)
+        return rows
 
 
 class DeviceCopy(Workload):
     """Calibration probe, not a BASELINE config: a plain device-to-device copy
     of 128 MiB, the known-size reference for rocprofv3 FETCH_SIZE/WRITE_SIZE."""
-    name = "copy"
-    dtype = "u8"
+    name, dtype = "copy", "u8"
     description = "plain device copy of 134217728 bytes (HBM traffic counter calibration)"
     transforms_per_call = 1
     bytes_per_call = 2 * 134217728
+    takes_mapping = False
 
     def setup(self, torch, lib, stream):
-        sets = self._rotation(torch, self.bytes_per_call)
-        self.inputs = [torch.ones(134217728 // 4, dtype=torch.float32, device="cuda") for _ in range(sets)]
-        self.outputs = [torch.empty_like(self.inputs[0]) for _ in range(sets)]
+        self._rotate(torch, torch.ones(134217728 // 4, dtype=torch.float32, device="cuda"), self.bytes_per_call)
 
     def call(self, index):
         k = index % len(self.inputs)
@@ -466,87 +412,202 @@ class DeviceCopy(Workload):
     def kernel_name(self):
         return "torch copy_"
 
-    def cpu_sample(self, threads):
-        return 1.0, 0, "no CPU baseline for the calibration copy"
 
-
-WORKLOADS = {"c1": FwhtFp32, "c1p": FwhtFp32Pitched, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1), "c3b": lambda: FftC64(14, 1024),
-             "c4": RnsNegacyclic, "c5a": lambda: FwhtFp16(16384, 4096), "c5b": lambda: FwhtFp16(524288, 128),
-             "r2": FftC64Rank2, "copy": DeviceCopy}
-DEFAULT_WORKLOAD = "c2"
-
-
-CALLS_PER_GRAPH = 20
-TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+WORKLOADS = {"c1": FwhtFp32, "c1p": FwhtFp32Pitched, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1),
+             "c3b": lambda: FftC64(14, 1024), "c4": RnsNegacyclic, "c5a": lambda: FwhtFp16(16384, 4096),
+             "c5b": lambda: FwhtFp16(524288, 128), "r2": FftC64Rank2, "copy": DeviceCopy}
 
 
 def measured_traffic(name):
-    """HBM bytes per call (read + write) for a workload, from the rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary in profiles/ (scaled by the copy-kernel
+    """HBM bytes per call (read, write) for a configuration, from the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/ (scaled by the copy
     calibration recorded there), or None when no measurement exists."""
     try:
         with open(TRAFFIC_TABLE) as f:
             for line in f:
                 fields = line.split()
                 if len(fields) == 3 and fields[0] == name:
-                    return int(fields[1]) + int(fields[2])
+                    return int(fields[1]), int(fields[2])
     except OSError:
         pass
     return None
 
 
-def time_calls(torch, workload, stream, steps, warmup, use_graph=True):
-    """Milliseconds per call. W eager warmup calls; then, as the reference
-    times it (a graph of 20 calls replayed, docs/fwht_native_repair_20261107.md:20),
-    the K timed calls run as replays of a captured HIP graph of 20 calls so
-    host submission is not measured. Events are recorded on the plans' stream."""
+def time_graph_replays(torch, workload, stream, steps, warmup):
+    """Per-call milliseconds of each replay of a 20-call graph (the median is
+    the reported figure) and the number of timed calls."""
     with torch.cuda.stream(stream):
         for i in range(warmup):
             workload.call(i)
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    if use_graph:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(CALLS_PER_GRAPH):
-                workload.call(i)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(CALLS_PER_GRAPH):
+            workload.call(i)
+    torch.cuda.synchronize()
+    replays = max(MIN_REPLAYS, -(-steps // CALLS_PER_GRAPH))
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+    with torch.cuda.stream(stream):  # replay() launches on the current stream
+        graph.replay()  # the first replay uploads the graph
         torch.cuda.synchronize()
-        replays = max(1, -(-steps // CALLS_PER_GRAPH))
-        # replay() launches on the current stream: make it the plans' stream.
-        with torch.cuda.stream(stream):
-            graph.replay()  # first replay uploads the graph
-            torch.cuda.synchronize()
+        for start, stop in marks:
             start.record(stream)
-            for _ in range(replays):
-                graph.replay()
+            graph.replay()
             stop.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(stop) / (replays * CALLS_PER_GRAPH), replays * CALLS_PER_GRAPH
+    torch.cuda.synchronize()
+    per_call = [start.elapsed_time(stop) / CALLS_PER_GRAPH for start, stop in marks]
+    del graph
+    return per_call, replays * CALLS_PER_GRAPH
+
+
+def time_eager(torch, workload, stream, steps, warmup):
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            workload.call(i)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     with torch.cuda.stream(stream):
         for i in range(steps):
             workload.call(warmup + i)
     stop.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps, steps
+    return [start.elapsed_time(stop) / steps], steps
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_rate(workload, threads, target_s=0.25, reps=7):
+    """Transforms/s of the CPU oracle over a bounded slice of the workload's
+    rows: the slice is sized to about `target_s` per run; one warmup, then the
+    median of `reps` runs (3 runs and no warmup when one row alone takes more
+    than a second). Returns (rate, sample description)."""
+    total = workload.rows
+    rows = max(1, min(total, threads))
+    t0 = time.perf_counter()
+    workload.cpu_run(rows, threads)
+    elapsed = time.perf_counter() - t0
+    while elapsed < 0.02 and rows < total:
+        rows = min(total, rows * 4)
+        t0 = time.perf_counter()
+        workload.cpu_run(rows, threads)
+        elapsed = time.perf_counter() - t0
+    slow = elapsed > 1.0
+    if not slow:
+        rows = max(1, min(total, int(rows * target_s / elapsed)))
+        if rows >= threads:
+            rows -= rows % threads
+        workload.cpu_run(rows, threads)  # warmup at the sampled size
+    runs = 3 if slow else reps
+    times, transforms = [], 0
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        transforms = workload.cpu_run(rows, threads)
+        times.append(time.perf_counter() - t0)
+    median = statistics.median(times)
+    sample = (f"{rows} of {total} rows per run, median of {runs} runs" + ("" if slow else " after 1 warmup")
+              + f", {threads} thread{'s' if threads > 1 else ''}, {median * 1e3:.1f} ms per run")
+    return transforms / median, sample
+
+
+def measure(torch, lib, name, args, mapping=None):
+    """Times one configuration on the GPU; returns its per_config entry."""
+    workload = WORKLOADS[name]()
+    if mapping:
+        if not workload.takes_mapping:
+            raise SystemExit(f"--mapping does not apply to {name}")
+        workload.mapping = mapping
+    stream = torch.cuda.Stream()  # default priority; plans launch on it
+    workload.setup(torch, lib, stream.cuda_stream)
+    torch.cuda.synchronize()
+    timer = time_eager if args.eager else time_graph_replays
+    per_call, timed = timer(torch, workload, stream, args.steps, args.warmup)
+    ms = statistics.median(per_call)
+    achieved = workload.bytes_per_call / (ms * 1e-3) / 1e9
+    traffic = measured_traffic(name)
+    entry = {
+        "config": name,
+        "workload": workload.description,
+        "dtype": workload.dtype,
+        "kernel": workload.kernel_name(),
+        "ms_per_call": ms,
+        "ms_per_call_replays": per_call,
+        "timed_calls": timed,
+        "transforms_per_call": workload.transforms_per_call,
+        "transforms_per_s": workload.transforms_per_call / (ms * 1e-3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None if traffic is None else sum(traffic),
+            "traffic_read_write": traffic,
+            "algorithmic_bytes_per_call": workload.bytes_per_call,
+        },
+    }
+    if traffic is not None:
+        entry["roofline"]["traffic_over_algorithmic"] = sum(traffic) / workload.bytes_per_call
+    if hasattr(workload, "valu_per_butterfly"):
+        rate = workload.butterflies_per_call / (ms * 1e-3)
+        peak = VALU_LANE_OPS_PER_S / workload.valu_per_butterfly
+        entry["valu_roofline"] = {"bound": "valu", "achieved": rate, "peak": peak, "unit": "butterflies/s",
+                                  "frac": rate / peak, "valu_per_butterfly": workload.valu_per_butterfly,
+                                  "floor_ms_per_call": workload.butterflies_per_call / peak * 1e3}
+    if args.verify and hasattr(workload, "verify"):
+        entry["verified"] = workload.verify()
+    # Device buffers go before the CPU leg and the next configuration.
+    for attr in ("inputs", "outputs", "spectra", "workspace"):
+        if hasattr(workload, attr):
+            delattr(workload, attr)
+    for plan in getattr(workload, "plans", []):
+        plan.close()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    if not args.no_cpu and hasattr(workload, "host"):
+        import oracle
+        threads = oracle.default_threads()
+        one, one_sample = cpu_rate(workload, 1)
+        entry["cpu_baseline"] = {"value_1core": one, "sample_1core": one_sample, "unit": "transforms/s",
+                                 "kind": "port", "cpu_model": cpu_model()}
+        if workload.rows > 1 and threads > 1:
+            many, many_sample = cpu_rate(workload, threads)
+            entry["cpu_baseline"].update(value=many, cores=threads, sample=many_sample)
+        else:
+            entry["cpu_baseline"].update(value=one, cores=1, sample=one_sample + " (one transform: 1 core only)")
+    print(f"# {name}: {ms * 1e3:.2f} us per call, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})",
+          file=sys.stderr, flush=True)
+    return entry
 
 
 def main():
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=200)
-    parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
-    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    parser.add_argument("--verify", action="store_true", help="check one output against the oracle")
+    parser.add_argument("--steps", type=int, default=140)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--workload", default="all", choices=["all"] + sorted(WORKLOADS))
+    parser.add_argument("--headline", default=DEFAULT_HEADLINE, choices=BASELINE_CONFIGS)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    parser.add_argument("--verify", action="store_true", help="check each output against the oracle")
     parser.add_argument("--eager", action="store_true", help="time eager submissions instead of graph replays")
-    parser.add_argument("--mapping", default=None,
-                        help="plan one-plan workloads with this lowering (EXPLICIT policy) instead of the default")
+    parser.add_argument("--mapping", default=None, help="plan a single --workload with this lowering (EXPLICIT)")
     args = parser.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: the butterfly path is single-GPU (every configuration "
-              "shards by rows/limbs with no communication); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: every configuration of the butterfly path runs on one GPU and "
+              "shards by rows or limbs without communication; multi-GPU runs are not part of this build",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.mapping and args.workload == "all":
+        print("--mapping needs a single --workload", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -554,72 +615,33 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
-    lib = cb.Library()
-    stream = torch.cuda.Stream()  # default priority; plans launch on it
-    workload = WORKLOADS[args.workload]()
-    if args.mapping:
-        if not workload.takes_mapping:
-            print(f"--mapping applies to one-plan workloads; {args.workload} is not one", file=sys.stderr)
-            sys.exit(2)
-        workload.mapping = args.mapping
-    workload.setup(torch, lib, stream.cuda_stream)
-    torch.cuda.synchronize()
-
-    ms, timed = time_calls(torch, workload, stream, args.steps, args.warmup, use_graph=not args.eager)
-    transforms_per_s = workload.transforms_per_call / (ms * 1e-3)
-    achieved = workload.bytes_per_call / (ms * 1e-3) / 1e9
+    lib = cb.Native()
+    names = BASELINE_CONFIGS if args.workload == "all" else [args.workload]
+    entries = [measure(torch, lib, name, args, args.mapping) for name in names]
+    head = next((e for e in entries if e["config"] == args.headline), entries[0])
     result = {
         "metric": METRIC,
-        "value": transforms_per_s,
+        "value": head["transforms_per_s"],
         "unit": "transforms/s",
         "n_gpus": 1,
-        "steps": timed,
+        "steps": head["timed_calls"],
         "warmup": args.warmup,
-        "ms_per_step": ms,
+        "ms_per_step": head["ms_per_call"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": workload.dtype,
+        "dtype": head["dtype"],
         "data": "synthetic (seeded splitmix64 / mt19937_64 generators)",
-        "config": workload.config(),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": workload.kernel_name(),
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(workload.name),
-            "algorithmic_bytes_per_call": workload.bytes_per_call,
-        },
-        "timing": "hip graph of %d calls, replayed" % CALLS_PER_GRAPH if not args.eager else "eager calls",
+        "config": {"workload": head["workload"], "headline": head["config"],
+                   "configs_measured": [e["config"] for e in entries]},
+        "roofline": dict(head["roofline"], kernel=head["kernel"]),
+        "timing": ("eager calls" if args.eager else
+                   f"median of >= {MIN_REPLAYS} replays of a HIP graph of {CALLS_PER_GRAPH} calls, "
+                   "HIP events on the plans' stream"),
+        "per_config": entries,
     }
-    if hasattr(workload, "valu_per_butterfly"):
-        # The integer-VALU roof of the NTT configs (see VALU_LANE_OPS_PER_S).
-        rate = workload.butterflies_per_call / (ms * 1e-3)
-        peak = VALU_LANE_OPS_PER_S / workload.valu_per_butterfly
-        result["valu_roofline"] = {
-            "bound": "valu",
-            "achieved": rate,
-            "peak": peak,
-            "unit": "butterflies/s",
-            "frac": rate / peak,
-            "valu_per_butterfly": workload.valu_per_butterfly,
-            "floor_ms_per_step": workload.butterflies_per_call / peak * 1e3,
-        }
-    if args.verify:
-        result["verified"] = workload.verify(torch)
-    if not args.no_cpu:
-        import oracle
-        threads = oracle.default_threads()
-        seconds, transforms, sample = workload.cpu_sample(threads)
-        result["cpu_baseline"] = {
-            "value": transforms / seconds,
-            "unit": "transforms/s",
-            "cores": threads,
-            "kind": "port",
-            "sample": sample + f"; {seconds:.1f} s on {threads} host threads",
-        }
+    if "cpu_baseline" in head:
+        result["cpu_baseline"] = head["cpu_baseline"]
     print(json.dumps(result), flush=True)
 
 

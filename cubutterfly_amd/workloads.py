@@ -7,6 +7,8 @@ seeded with seed ^ (0x9e3779b97f4a7c15 * (channel + 1)), the first four words of
 the channel fixed to {0, 1, q-1, q-2}, then random() % q.
 """
 import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -123,13 +125,48 @@ def complex_input(log_n, batch, seed=1):
     return out.reshape(batch, n)
 
 
-def quarot_input(rows, n, seed=1, outlier_seed=7):
-    """fp16 [rows, n]: N(0,1), columns with splitmix64 % 1000 == 0 scaled x50 (RNE)."""
-    re, im = normal_pairs(seed, (rows * n + 1) // 2)
-    x = np.concatenate([re, im])[: rows * n].reshape(rows, n)
-    outliers = (splitmix64(outlier_seed, n) % np.uint64(1000)) == 0
-    x[:, outliers] *= 50.0
-    return x.astype(np.float32).astype(np.float16)
+def _box_muller_part(seed, pairs, first, count, imaginary):
+    """The real (cos) or imaginary (sin) parts of pairs first..first+count-1
+    of normal_pairs(seed, pairs)."""
+    u1 = _uniform01(seed, count, first)
+    u2 = _uniform01(seed, count, pairs + first)
+    r = np.sqrt(-2.0 * np.log1p(-u1))
+    theta = 2.0 * math.pi * u2
+    return r * (np.sin(theta) if imaginary else np.cos(theta))
+
+
+def _workers():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def quarot_input(rows, n, seed=1, outlier_seed=7, chunk=1 << 21):
+    """fp16 [rows, n]: N(0,1), columns with splitmix64 % 1000 == 0 scaled x50 (RNE).
+
+    Element k of the flat array is the real part of Box-Muller pair k for
+    k < P = ceil(rows * n / 2), else the imaginary part of pair k - P (the
+    real parts of all pairs, then their imaginary parts). Chunks of `chunk`
+    elements are generated on a thread pool (numpy releases the GIL); the
+    values are those of one sequential pass."""
+    total = rows * n
+    pairs = (total + 1) // 2
+    scale = np.where((splitmix64(outlier_seed, n) % np.uint64(1000)) == 0, 50.0, 1.0)
+    out = np.empty(total, dtype=np.float16)
+
+    def fill(start):
+        stop = min(total, start + chunk)
+        part = np.empty(stop - start)
+        lo, hi = start, min(stop, pairs)
+        if lo < hi:
+            part[: hi - lo] = _box_muller_part(seed, pairs, lo, hi - lo, False)
+        lo = max(start, pairs)
+        if lo < stop:
+            part[lo - start:] = _box_muller_part(seed, pairs, lo - pairs, stop - lo, True)
+        part *= scale[np.arange(start, stop) % n]
+        out[start:stop] = part.astype(np.float32).astype(np.float16)
+
+    with ThreadPoolExecutor(_workers()) as pool:
+        list(pool.map(fill, range(0, total, chunk)))
+    return out.reshape(rows, n)
 
 
 def _is_prime(q):
