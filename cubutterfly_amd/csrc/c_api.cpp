@@ -85,12 +85,16 @@ void log_event(cubutterflyHandle_t handle, cubutterflyLogLevel_t level, const ch
     if (handle && handle->logger) handle->logger(level, event, message.c_str(), handle->logger_data);
 }
 
-void execute_plan(cubutterflyHandle_t handle, cubutterflyPlan_t plan, const void* input, void* output) {
+void check_execution(cubutterflyHandle_t handle, cubutterflyPlan_t plan, const void* input, void* output) {
     require(handle != nullptr && plan != nullptr && input != nullptr && output != nullptr,
             "execution arguments must be non-null");
     require(plan->request.in_place ? input == output : input != output,
             plan->request.in_place ? "in-place execution requires identical pointers"
                                    : "out-of-place execution requires distinct pointers");
+}
+
+void execute_plan(cubutterflyHandle_t handle, cubutterflyPlan_t plan, const void* input, void* output) {
+    check_execution(handle, plan, input, output);
     require(plan->workspace_bytes == 0 || plan->workspace != nullptr,
             "plan requires a workspace; bind one with cubutterflyPlanSetWorkspace");
     plan->executor->execute(input, output, plan->workspace, handle->stream);
@@ -99,6 +103,23 @@ void execute_plan(cubutterflyHandle_t handle, cubutterflyPlan_t plan, const void
 }
 
 }  // namespace
+
+namespace cbw {
+
+cubutterflyStatus_t guarded_call(void (*body)(void*), void* context) noexcept {
+    return protect([&] { body(context); });
+}
+
+void execute_plan_with_workspace(cubutterflyHandle_t handle, cubutterflyPlan_t plan, const void* input, void* output,
+                                 void* workspace, std::size_t capacity, const char* what) {
+    check_execution(handle, plan, input, output);
+    if (plan->workspace_bytes > capacity)
+        throw std::invalid_argument("plan needs " + std::to_string(plan->workspace_bytes) + " bytes of workspace; " +
+                                    what + " holds " + std::to_string(capacity));
+    plan->executor->execute(input, output, plan->workspace_bytes ? workspace : nullptr, handle->stream);
+}
+
+}  // namespace cbw
 
 extern "C" {
 

@@ -36,6 +36,28 @@ CUBUTTERFLYAPI cubutterflyStatus_t cubutterflySetNttRing(cubutterflyDescriptor_t
                                                         cubutterflyNttRing_t ring,
                                                         uint64_t psi);
 
+/* Bytes of the library-owned device array that cubutterflyExecuteNoAlloc
+ * uses as the plan's workspace: 32 MiB, held by each GPU the library runs on
+ * until the process ends. */
+#define CUBUTTERFLY_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* cubutterflyExecute without any device allocation and without the workspace
+ * bound by cubutterflyPlanSetWorkspace: the plan's workspace is carved from a
+ * static device array of CUBUTTERFLY_NOALLOC_SCRATCH_BYTES per GPU instead.
+ * No counterpart in the reference's ABI; it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). A plan whose PlanGetWorkspaceSize exceeds the array is
+ * rejected with INVALID_VALUE before any work is queued; plans without a
+ * workspace run exactly as with cubutterflyExecute. Same pointer, placement,
+ * stream and asynchrony rules as cubutterflyExecute. All calls on one GPU
+ * share that GPU's array: calls that may overlap on one device (other
+ * streams, other host threads) race on it and must be serialised by the
+ * caller. */
+CUBUTTERFLYAPI cubutterflyStatus_t cubutterflyExecuteNoAlloc(cubutterflyHandle_t handle,
+                                                            cubutterflyPlan_t plan,
+                                                            const void* input,
+                                                            void* output);
+
 #ifdef __cplusplus
 }
 #endif
