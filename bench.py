@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X butterfly path (one GPU): every BASELINE configuration.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|c1|c2|c3a|c3b|c4|c5a|c5b|c1p|r2|copy]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|c1|c2|c3a|c3b|c4|c5a|c5b|...]
                 [--headline c5a] [--no-cpu] [--verify] [--eager] [--mapping LOWERING]
 
 A step is one call of the hot path over one batch of a BASELINE configuration
@@ -364,18 +364,22 @@ class FwhtFp16(OnePlan):
     FP16 rounding: 16384 x 4096 (c5a) or 524288 x 128 (c5b)."""
     dtype = "f16"
 
-    def __init__(self, rows, n):
-        self.rows, self.n = rows, n
-        self.name = "c5a" if n == 4096 else "c5b"
+    def __init__(self, rows, n, mma=False):
+        self.rows, self.n, self.mma = rows, n, mma
+        self.name = ("c5a" if n == 4096 else "c5b") + ("_mma" if mma else "")
         self.description = (f"{self.name.upper()}: FWHT fp16 storage / fp32 compute, {rows} x n={n}, output scale "
-                            "1/sqrt(n), final-storage rounding, N(0,1) activations with x50 outlier channels")
+                            "1/sqrt(n), final-storage rounding, N(0,1) activations with x50 outlier channels"
+                            + (", ALLOW_FP16_MMA (MFMA 16x16 Hadamard blocks; not the bit-exact default)"
+                               if mma else ""))
         self.transforms_per_call = rows
         self.bytes_per_call = 2 * rows * n * 2
         self.scale = float(np.float32(1.0 / np.sqrt(n)))
 
     def descriptor(self, cb):
+        policy = cb.ArithmeticPolicy.ALLOW_FP16_MMA if self.mma else cb.ArithmeticPolicy.STRICT
         return cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [self.n], self.rows, compute=cb.ComputeType.FP32,
-                           output_scale=self.scale, output_rounding=cb.OutputRounding.FINAL_STORAGE)
+                           output_scale=self.scale, output_rounding=cb.OutputRounding.FINAL_STORAGE,
+                           arithmetic_policy=policy)
 
     def make_host(self):
         from cubutterfly_amd import workloads
@@ -384,7 +388,10 @@ class FwhtFp16(OnePlan):
     def verify(self):
         import oracle
         got = self.outputs[0].cpu().numpy().view(np.float16).astype(np.float32)
-        ref = oracle.fwht_f16_final(self.host, self.scale, threads=oracle.default_threads()).astype(np.float32)
+        ref16 = oracle.fwht_f16_final(self.host, self.scale, threads=oracle.default_threads())
+        ref = ref16.astype(np.float32)
+        if self.mma:  # within 2e-3 or one fp16 ulp of the oracle (different accumulation order)
+            return bool(np.all(np.abs(got - ref) <= np.maximum(2e-3, np.spacing(np.abs(ref16)).astype(np.float32))))
         return bool(np.max(np.abs(got - ref)) <= 2e-3)
 
     def cpu_run(self, rows, threads):
@@ -415,7 +422,8 @@ class DeviceCopy(Workload):
 
 WORKLOADS = {"c1": FwhtFp32, "c1p": FwhtFp32Pitched, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1),
              "c3b": lambda: FftC64(14, 1024), "c4": RnsNegacyclic, "c5a": lambda: FwhtFp16(16384, 4096),
-             "c5b": lambda: FwhtFp16(524288, 128), "r2": FftC64Rank2, "copy": DeviceCopy}
+             "c5b": lambda: FwhtFp16(524288, 128), "c5a_mma": lambda: FwhtFp16(16384, 4096, mma=True),
+             "c5b_mma": lambda: FwhtFp16(524288, 128, mma=True), "r2": FftC64Rank2, "copy": DeviceCopy}
 
 
 def measured_traffic(name):

@@ -784,6 +784,14 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
     supported(r.log_n <= kMaxResidentLog,
               "FWHT lengths above 2^" + std::to_string(kMaxResidentLog) + " are not yet lowered for gfx950");
     supported(!r.allow_mma || r.fp16_final, "MFMA Hadamard blocks require FP16 storage");
+    // ALLOW_FP16_MMA: the MFMA Hadamard-block kernel is the default where it
+    // covers the request; the stage-ordered VALU kernels stay candidates.
+    const bool mfma = r.allow_mma && fwht_mfma_covers(r);
+    if (r.variant == fwht_mfma_name()) {
+        supported(r.allow_mma, "'" + r.variant + "' needs the ALLOW_FP16_MMA arithmetic policy");
+        supported(mfma, "'" + r.variant + "' covers packed FP16 rows of 2 to 4096 points only");
+    }
+    if (mfma && (r.variant.empty() || r.variant == fwht_mfma_name())) return make_fwht_mfma_executor(r);
     const Launch launch = r.fp16_final ? resident_launcher<F16Io>(r.log_n) : resident_launcher<F32Io>(r.log_n);
     require(launch != nullptr, "FWHT length has no launcher");
     PitchedLaunch pitched = nullptr;
@@ -803,8 +811,12 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
     if (wide) available += ", " + FwhtExecutor::name(r, true) + ", " + FwhtExecutor::name(r, true, true);
     supported(r.variant.empty() || one_per_row || persistent || r.variant == FwhtExecutor::name(r, false),
               "'" + r.variant + "' is not a lowering of this FWHT (available: " + available + ")");
-    return std::make_unique<FwhtExecutor>(r, launch, pitched, one_per_row || persistent ? wide : WideLaunch{},
-                                          persistent);
+    auto e = std::make_unique<FwhtExecutor>(r, launch, pitched, one_per_row || persistent ? wide : WideLaunch{},
+                                            persistent);
+    if (r.allow_mma && !mfma)
+        e->reason += "; ALLOW_FP16_MMA requested, but the MFMA Hadamard-block kernel covers packed rows of 2 to 4096 "
+                     "points only: stage-ordered VALU kernel used";
+    return e;
 }
 
 std::vector<std::string> fwht_candidates(const Request& r) {
@@ -817,6 +829,7 @@ std::vector<std::string> fwht_candidates(const Request& r) {
         names.push_back(FwhtExecutor::name(r, true, true));
         if (r.log_n == 12) std::swap(names[0], names[1]);  // the default first
     }
+    if (r.allow_mma && fwht_mfma_covers(r)) names.insert(names.begin(), fwht_mfma_name());
     return names;
 }
 

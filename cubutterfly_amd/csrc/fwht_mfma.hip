@@ -1,0 +1,248 @@
+// FP16 FWHT through MFMA 16 x 16 Hadamard blocks (the ALLOW_FP16_MMA policy,
+// reference include/cubutterfly/cubutterfly.h:86-90): FP16 storage, FP32
+// accumulation, one final RNE narrowing after the output scale -- the
+// final-storage contract of src/butterfly.cu:1452-1470, 1882-1897 -- for rows
+// of 2 .. 4096 points.
+//
+// H(2^m) = H(2^a) (x) H(2^b) (x) ... for the Sylvester matrix, so the
+// transform factors into one 16 x 16 block contraction per 4-bit group of the
+// element index. A wave owns a tile of 4096 consecutive elements, index
+// e = i2 * 256 + i1 * 16 + i0 (whole rows: the row bits sit above bit m - 1).
+// Per block of fixed i2 (16 blocks per tile):
+//
+//   1. Contraction along i0 on the matrix cores: A[i1][i0] is the fp16 input
+//      itself (v_mfma_f32_16x16x16_f16 wants lane l to supply A[l % 16]
+//      [4 (l / 16) + j], which is 4 consecutive halves, one 8-byte load), B is
+//      the 16 x 16 block M0 = I (x) H(2^t0) (t0 transform bits in the group).
+//      The fp32 result D0[i1][k0] lands in lane l as rows 4 (l / 16) + r,
+//      column l % 16.
+//   2. Contraction along i1 on the matrix cores: the transposed block D0^T
+//      has lane l supplying D0^T[l % 16][4 (l / 16) + j] = D0[4 (l / 16) + j]
+//      [l % 16] -- exactly lane l's accumulator registers, so no data moves
+//      between lanes. The fp32 values enter the fp16 operand as an exact-ish
+//      split, D0 / 16 = hi + lo (two fp16 parts, 22 significant bits; the
+//      1/16 keeps |hi| below the fp16 range for any fp16 input), and
+//      D1 = 16 (hi M1 + lo M1) accumulates both products in fp32.
+//   3. Bits 8 .. 11 (i2), when they are transform bits: after all 16 blocks
+//      each lane holds, for its four (k0, k1), the 16 values over i2 -- a
+//      radix-2 transform in registers (VALU, fp32, bits in stage order).
+//
+// The output element (k2, k1, k0) of lane l, register r is k2 * 256 +
+// (l % 16) * 16 + 4 (l / 16) + r: four consecutive halves, one 8-byte store.
+// No LDS is used. Accumulation order differs from the radix-2 stage order of
+// the STRICT kernels, so results can differ from them by one fp16 ulp where a
+// value sits near a rounding boundary; this lowering is taken only when the
+// caller allows MFMA arithmetic.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "buffer.hpp"
+#include "json.hpp"
+#include "planner.hpp"
+
+namespace cbw {
+namespace {
+
+using half4 = __attribute__((ext_vector_type(4))) _Float16;
+using pk16 = __attribute__((ext_vector_type(2))) __fp16;  // v_cvt_pkrtz_f16_f32 result
+using float4v = __attribute__((ext_vector_type(4))) float;
+
+constexpr int kTileLog = 12;         // elements per wave tile
+constexpr int kWavesPerBlock = 4;    // tiles per workgroup
+constexpr int kMaxLog = kTileLog;    // longest row this lowering covers
+
+// Lane l's B operand of the 16 x 16 block I (x) H(2^t): B[k][j] for
+// k = 4 (l / 16) + 0..3 and j = l % 16. Entries are 0 or +-1 (exact in fp16).
+__device__ __forceinline__ half4 hadamard_block(unsigned lane, int t) {
+    const unsigned j = lane & 15u, k0 = 4u * (lane >> 4);
+    const unsigned low = (1u << t) - 1u;
+    half4 b;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const unsigned k = k0 + unsigned(q);
+        const bool same_block = (k & ~low) == (j & ~low);
+        const bool negative = __popc(k & j & low) & 1u;
+        b[q] = same_block ? (negative ? _Float16(-1.0f) : _Float16(1.0f)) : _Float16(0.0f);
+    }
+    return b;
+}
+
+// Hides a value from the optimiser (no code): keeps the fp32 product and the
+// fp16 narrowing two separate roundings.
+__device__ __forceinline__ void opaque(float& x) { asm volatile("" : "+v"(x)); }
+
+template <int LOG_N>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void fwht_mfma_kernel(const __half* __restrict__ input,
+                                                                        __half* output, std::uint64_t total,
+                                                                        float norm, float scale) {
+    constexpr int t0 = LOG_N < 4 ? LOG_N : 4;                        // transform bits among 0..3
+    constexpr int t1 = LOG_N <= 4 ? 0 : (LOG_N < 8 ? LOG_N - 4 : 4);  // among 4..7
+    constexpr int t2 = LOG_N <= 8 ? 0 : LOG_N - 8;                    // among 8..11
+    const unsigned lane = threadIdx.x & 63u;
+    const std::uint64_t tile = std::uint64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const std::uint64_t first = tile << kTileLog;
+    if (first >= total) return;  // whole wave: no tile here
+    // The tile's span (the last tile of a batch may be partial: the range
+    // check zero-fills its loads and drops its stores past the data).
+    const std::uint64_t left = total - first;
+    const unsigned bytes = unsigned((left < (1u << kTileLog) ? left : (1u << kTileLog)) * sizeof(__half));
+    const __amdgpu_buffer_rsrc_t src = make_rsrc(input + first, bytes);
+    const __amdgpu_buffer_rsrc_t dst = make_rsrc(output + first, bytes);
+    // Element offset of lane l's four halves within block i2: i1 = l % 16,
+    // i0 = 4 (l / 16) .. +3 on the way in; k1 = l % 16, k0 likewise out.
+    const unsigned lane_bytes = ((lane & 15u) * 16u + 4u * (lane >> 4)) * unsigned(sizeof(__half));
+
+    const half4 m0 = hadamard_block(lane, t0);
+    const half4 m1 = hadamard_block(lane, t1 > 0 ? t1 : 1);
+
+    using U2 = __attribute__((ext_vector_type(2))) unsigned;
+    half4 a[16];
+#pragma unroll
+    for (int i2 = 0; i2 < 16; ++i2) {
+        const U2 raw = __builtin_amdgcn_raw_buffer_load_b64(src, int(lane_bytes + 512u * i2), 0, 0);
+        a[i2] = __builtin_bit_cast(half4, raw);
+    }
+
+    float v[16][4];
+#pragma unroll
+    for (int i2 = 0; i2 < 16; ++i2) {
+        const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        float4v d = __builtin_amdgcn_mfma_f32_16x16x16f16(a[i2], m0, zero, 0, 0, 0);
+        if constexpr (t1 > 0) {
+            // D0 / 16 = hi + lo; D1 = 16 (hi + lo) M1.
+            float s[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] = d[r] * 0.0625f;
+            const pk16 h01 = __builtin_amdgcn_cvt_pkrtz(s[0], s[1]);
+            const pk16 h23 = __builtin_amdgcn_cvt_pkrtz(s[2], s[3]);
+            const pk16 l01 = __builtin_amdgcn_cvt_pkrtz(s[0] - float(h01[0]), s[1] - float(h01[1]));
+            const pk16 l23 = __builtin_amdgcn_cvt_pkrtz(s[2] - float(h23[0]), s[3] - float(h23[1]));
+            const U2 hi_bits = {__builtin_bit_cast(unsigned, h01), __builtin_bit_cast(unsigned, h23)};
+            const U2 lo_bits = {__builtin_bit_cast(unsigned, l01), __builtin_bit_cast(unsigned, l23)};
+            const half4 hi = __builtin_bit_cast(half4, hi_bits);
+            const half4 lo = __builtin_bit_cast(half4, lo_bits);
+            d = __builtin_amdgcn_mfma_f32_16x16x16f16(hi, m1, zero, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x16f16(lo, m1, d, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[i2][r] = d[r] * 16.0f;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[i2][r] = d[r];
+        }
+    }
+    // Bits 8 .. 8 + t2 - 1 across the 16 blocks, in stage order.
+#pragma unroll
+    for (int b = 0; b < t2; ++b) {
+        const int dist = 1 << b;
+#pragma unroll
+        for (int i2 = 0; i2 < 16; ++i2) {
+            if ((i2 & dist) == 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float x = v[i2][r], y = v[i2 + dist][r];
+                    v[i2][r] = x + y;
+                    v[i2 + dist][r] = x - y;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int k2 = 0; k2 < 16; ++k2) {
+        unsigned short h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float y = (v[k2][r] * norm) * scale;
+            opaque(y);
+            h[r] = __half_as_ushort(__float2half_rn(y));
+        }
+        if constexpr (t1 > 0) {
+            const U2 packed = {unsigned(h[0]) | (unsigned(h[1]) << 16), unsigned(h[2]) | (unsigned(h[3]) << 16)};
+            __builtin_amdgcn_raw_buffer_store_b64(packed, dst, int(lane_bytes + 512u * k2), 0, 0);
+        } else {
+            // Rows of <= 16 points: no second contraction, so lane l holds
+            // D0 rows i1 = 4 (l / 16) + r at column k0 = l % 16, 16 elements apart.
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const unsigned e = 256u * k2 + 16u * (4u * (lane >> 4) + unsigned(r)) + (lane & 15u);
+                __builtin_amdgcn_raw_buffer_store_b16(h[r], dst, int(e * sizeof(__half)), 0, 0);
+            }
+        }
+    }
+}
+
+using MfmaLaunch = void (*)(const void*, void*, std::uint64_t, float, float, unsigned, hipStream_t);
+
+template <int LOG_N>
+void launch_mfma(const void* in, void* out, std::uint64_t total, float norm, float scale, unsigned grid,
+                 hipStream_t stream) {
+    hipLaunchKernelGGL(fwht_mfma_kernel<LOG_N>, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream,
+                       static_cast<const __half*>(in), static_cast<__half*>(out), total, norm, scale);
+}
+
+template <int... L>
+MfmaLaunch mfma_entry(int log_n, std::integer_sequence<int, L...>) {
+    static constexpr MfmaLaunch table[] = {&launch_mfma<L + 1>...};
+    return table[log_n - 1];
+}
+
+class FwhtMfmaExecutor final : public Executor {
+  public:
+    FwhtMfmaExecutor(const Request& r, MfmaLaunch launch) : r_(r), launch_(launch) {
+        norm_ = r.normalize ? 1.0f / static_cast<float>(r.n) : 1.0f;
+        scale_ = r.output_scale;
+        total_ = r.n * r.batch;
+        const std::uint64_t tiles = (total_ + (1ull << kTileLog) - 1) >> kTileLog;
+        const std::uint64_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+        require(blocks <= 0x7fffffffull, "FWHT batch exceeds the MFMA lowering's grid");
+        grid_ = static_cast<unsigned>(blocks);
+        algorithm = fwht_mfma_name();
+        reason = "MFMA 16x16 Hadamard blocks (v_mfma_f32_16x16x16_f16, fp32 accumulation; fp32 intermediates enter "
+                 "the second contraction as hi + lo fp16 parts), bits 8+ butterflied in registers; one 4096-element "
+                 "tile per wave, no LDS; accumulation order differs from the radix-2 stage order";
+        const int t0 = r.log_n < 4 ? int(r.log_n) : 4;
+        const int t1 = r.log_n <= 4 ? 0 : (r.log_n < 8 ? int(r.log_n) - 4 : 4);
+        json::Writer w;
+        w.begin_object()
+            .field("schema_version", 1u)
+            .field("operator", "fwht")
+            .field("algorithm", algorithm)
+            .field("log_n", r.log_n)
+            .field("batch", r.batch)
+            .field("tile_elements", std::uint64_t{1} << kTileLog)
+            .field("tiles", tiles)
+            .field("grid", grid_)
+            .field("threads_per_block", 64u * kWavesPerBlock)
+            .field("mfma_per_tile", 16u * (t1 > 0 ? 3u : 1u))
+            .field("contraction_bits", unsigned(t0 + t1))
+            .field("register_bits", unsigned(r.log_n > 8 ? r.log_n - 8 : 0))
+            .field("lds_bytes", 0u)
+            .end_object();
+        mapping_json = w.str();
+    }
+    void execute(const void* in, void* out, void*, hipStream_t stream) override {
+        launch_(in, out, total_, norm_, scale_, grid_, stream);
+        hip_check(hipGetLastError(), "FWHT MFMA launch");
+    }
+
+  private:
+    Request r_;
+    MfmaLaunch launch_;
+    float norm_ = 1.0f, scale_ = 1.0f;
+    std::uint64_t total_ = 0;
+    unsigned grid_ = 1;
+};
+
+}  // namespace
+
+std::string fwht_mfma_name() { return "fwht-fp16-mfma16"; }
+
+bool fwht_mfma_covers(const Request& r) {
+    return r.fp16_final && !r.pitched && r.log_n >= 1 && r.log_n <= kMaxLog;
+}
+
+std::unique_ptr<Executor> make_fwht_mfma_executor(const Request& r) {
+    supported(fwht_mfma_covers(r), "the MFMA Hadamard-block FWHT covers packed FP16 rows of 2 to 4096 points");
+    return std::make_unique<FwhtMfmaExecutor>(r, mfma_entry(int(r.log_n), std::make_integer_sequence<int, kMaxLog>{}));
+}
+
+}  // namespace cbw

@@ -17,6 +17,12 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r);
 std::unique_ptr<Executor> make_ntt_executor(const Request& r);
 // Candidate lowerings of a rank-1 request, the static model's choice first.
 std::vector<std::string> fwht_candidates(const Request& r);
+// The MFMA Hadamard-block FP16 FWHT (ALLOW_FP16_MMA): its name, whether it
+// covers a request (packed FP16 final-storage rows of 2 .. 4096 points) and
+// its executor.
+std::string fwht_mfma_name();
+bool fwht_mfma_covers(const Request& r);
+std::unique_ptr<Executor> make_fwht_mfma_executor(const Request& r);
 // FFTs (r.log_n points) of the rows of row-major 2^l1 x 2^(r.log_n) blocks
 // (r.batch rows in all), each block's result stored transposed; null where
 // no kernel covers the shape.
