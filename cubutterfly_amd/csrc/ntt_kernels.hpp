@@ -517,11 +517,17 @@ struct Pass {
         }
     }
 
-    template <int FROM, int TO>
-    static __device__ __forceinline__ void exchange(W (&v)[kE], W* lds, std::uint32_t t) {
+    // Register window FROM -> TO through the LDS image. `between` runs
+    // between the writes and the second barrier: the next phase's twiddle
+    // loads go there, so their latency overlaps the barrier wait and their
+    // registers are only live from the phase that uses them (loading every
+    // phase's chunk up front kept them all live and cost occupancy).
+    template <int FROM, int TO, class Between>
+    static __device__ __forceinline__ void exchange(W (&v)[kE], W* lds, std::uint32_t t, Between&& between) {
         lds_barrier();
 #pragma unroll
         for (int r = 0; r < kE; ++r) lds[L::template at<FROM>(t, r)] = v[r];
+        between();
         lds_barrier();
 #pragma unroll
         for (int r = 0; r < kE; ++r) v[r] = lds[L::template at<TO>(t, r)];
@@ -542,22 +548,14 @@ struct Pass {
         }
     }
 
-    struct Chunks {
-        Chunk<0> c0;
-        Chunk<1> c1;
-        Chunk<2> c2;
-    };
-
-    static __device__ __forceinline__ void load_chunks(Chunks& c, const PassArgs<W>& a, const Tile& tl,
-                                                       std::uint32_t t, const DeviceDomain<W>& d) {
-        const __amdgpu_buffer_rsrc_t tw = make_rsrc(a.tw + d.tw, a.tw_bytes);
-        load_chunk<0>(c.c0, a, tl, t, tw);
-        load_chunk<1>(c.c1, a, tl, t, tw);
-        load_chunk<2>(c.c2, a, tl, t, tw);
+    static __device__ __forceinline__ __amdgpu_buffer_rsrc_t twiddles(const PassArgs<W>& a, const DeviceDomain<W>& d) {
+        return make_rsrc(a.tw + d.tw, a.tw_bytes);
     }
 
+    // The tile's butterflies and its store. c0 holds phase 0's twiddle chunk;
+    // later phases load theirs during the preceding exchange.
     static __device__ __forceinline__ void process(const PassArgs<W>& a, const Tile& tl, std::uint32_t t, W (&v)[kE],
-                                                   const Chunks& c, const DeviceDomain<W>& d, W* lds) {
+                                                   const Chunk<0>& c0, const DeviceDomain<W>& d, W* lds) {
         if constexpr (PIN) {  // physical order -> phase-0 layout through LDS
             lds_barrier();
             const Staged b = staged_base(tl, t);
@@ -576,14 +574,18 @@ struct Pass {
             for (int r = 0; r < kE; ++r)
                 if (!CT || LT < kLE || !((r >> top) & 1)) v[r] = shoup(v[r], W(1), d.rwp, d.nq);
         }
-        stages<0>(v, c.c0, d);
+        stages<0>(v, c0, d);
         if constexpr (kPhases > 1) {
-            exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
-            stages<1>(v, c.c1, d);
+            Chunk<1> c1;
+            exchange<tile_window<0>(), tile_window<1>()>(v, lds, t,
+                                                         [&] { load_chunk<1>(c1, a, tl, t, twiddles(a, d)); });
+            stages<1>(v, c1, d);
         }
         if constexpr (kPhases > 2) {
-            exchange<tile_window<1>(), tile_window<2>()>(v, lds, t);
-            stages<2>(v, c.c2, d);
+            Chunk<2> c2;
+            exchange<tile_window<1>(), tile_window<2>()>(v, lds, t,
+                                                         [&] { load_chunk<2>(c2, a, tl, t, twiddles(a, d)); });
+            stages<2>(v, c2, d);
         }
         constexpr int wl = tile_window<kPhases - 1>();
         if constexpr (kLast) {
@@ -640,9 +642,9 @@ struct Pass {
         W v[kE];
         load_tile(a, tl, t, v);
         const DeviceDomain<W> d = domain_of(a, tl);
-        Chunks c;
-        load_chunks(c, a, tl, t, d);
-        process(a, tl, t, v, c, d, lds);
+        Chunk<0> c0;
+        load_chunk<0>(c0, a, tl, t, twiddles(a, d));
+        process(a, tl, t, v, c0, d, lds);
     }
 
     // One tile per workgroup. (Every tile of a 2^16 x 64 pass is resident at
