@@ -89,6 +89,12 @@ __device__ __forceinline__ void exchange(float (&v)[kE], float* lds, unsigned t)
 
 // ---- storage adapters ----------------------------------------------------
 
+// FP32 results stored straight from the last phase (one element per lane,
+// a wave covering 256 consecutive bytes) use nontemporal stores: each output
+// is written once and not read again, and C1 measured 25.7 -> 20.9 us on
+// MI355X. The FP16 and 16-byte vector stores keep the default policy, where
+// the hint measured slower (C5b 50.2 -> 55.3 us) or no faster (C5a).
+
 // 16 bytes at byte offset `off` of a buffer resource.
 __device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t r, unsigned off) {
     const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
@@ -126,7 +132,7 @@ struct F32Io {
         for (int k = 0; k < 4; ++k) q[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
     }
     static __device__ __forceinline__ float load1(const float* p) { return *p; }
-    static __device__ __forceinline__ void store1(float* p, float x) { *p = x; }
+    static __device__ __forceinline__ void store1(float* p, float x) { __builtin_nontemporal_store(x, p); }
 };
 
 struct F16Io {
