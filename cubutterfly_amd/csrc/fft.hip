@@ -382,10 +382,17 @@ struct FftPass {
         if (kLaneOnly || reg_bytes < 4096u) return buffer_load<float2>(src, lane_bytes + reg_bytes);
         return buffer_load<float2>(src, lane_bytes, reg_bytes);
     }
+    // Final-pass stores (the caller's output, written once) are nontemporal
+    // where a wave's stores form segments of at least 512 bytes: one-pass
+    // rows, and transposing row passes with 2^6 or more rows per tile (C3a:
+    // 168.7 -> 156.4 us; on the 32-byte segments of 4096-point transposing
+    // rows the hint measured 2.6x slower). Column passes write the
+    // intermediate the next pass reads (nontemporal there: C3a 183 us).
+    static constexpr int kStoreAux = !COL && (SINGLE || LI >= 6) ? 2 : 0;
     static __device__ __forceinline__ void store_at(float2 x, __amdgpu_buffer_rsrc_t dst, std::uint32_t lane_bytes,
                                                     std::uint32_t reg_bytes) {
-        if (kLaneOnly || reg_bytes < 4096u) buffer_store<float2>(x, dst, lane_bytes + reg_bytes);
-        else buffer_store<float2>(x, dst, lane_bytes, reg_bytes);
+        if (kLaneOnly || reg_bytes < 4096u) buffer_store<float2, kStoreAux>(x, dst, lane_bytes + reg_bytes);
+        else buffer_store<float2, kStoreAux>(x, dst, lane_bytes, reg_bytes);
     }
 
     // `valid` false: an empty buffer range, so every load returns zero

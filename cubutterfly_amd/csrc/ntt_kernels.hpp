@@ -295,6 +295,8 @@ struct Pass {
     // measured 5-6% faster per C2 / C4 step. Forward passes keep write-back
     // stores: write-through made them slower (partial-line segments that
     // the L2 would otherwise merge).
+    // (Nontemporal final stores measured slower for C4, whose bit-reversed
+    // output lands in 8-byte segments: 60.6 -> 71-73 us.)
     static constexpr int kStoreAux = (!CT && !SINGLE) ? 17 : 0;
     static_assert(SINGLE ? (L1 == 0 && L2 == LT) : (COL ? LT == L1 : LT == L2), "pass bits");
     static_assert(LT >= 1 && LB >= kLE && LB <= 13, "tile shape");
