@@ -48,6 +48,8 @@ void ensure_registered() {
         register_u32_strict();
         register_u64_lazy();
         register_u64_strict();
+        register_alt_u32();
+        register_alt_u64();
         return true;
     }();
     (void)once;
@@ -172,8 +174,11 @@ struct EngineImplT {
         } else {
             supported(log_n <= 20, "NTT lengths above 2^20 are not yet lowered for gfx950");
             l1 = std::uint32_t(split_l1(int(log_n)));
+            if (c.split_high && c.split_high != l1) {
+                supported(alt_split(int(log_n), int(c.split_high)), "NTT split has no gfx950 kernels");
+                l1 = c.split_high;
+            }
             l2 = log_n - l1;
-            require(!c.wide_columns || sizeof(W) == 4, "32-column tiles are a u32 lowering");
             const int col_li = c.wide_columns ? kWideColLines : kColLines;
             const int rli = row_lines(int(l1), int(l2));
             const std::uint64_t col_tiles = polys << (l2 - col_li);
@@ -293,9 +298,11 @@ NttEngine::NttEngine(const NttEngineConfig& c) : impl_(new Impl) {
     else
         impl_->u64 = std::make_unique<EngineImplT<std::uint64_t>>(c);
     const bool two = passes() == 2;
+    const bool other_split = two && c.split_high && c.split_high != std::uint32_t(split_l1(int(c.log_n)));
     algorithm_ = std::string("ntt-u") + std::to_string(c.word_bits) + (c.negacyclic ? "-negacyclic" : "-cyclic") +
                  (two ? "-two-pass-r16" : "-resident-r16") + (c.force_strict ? "-strict" : "") +
-                 (two && c.wide_columns ? "-c32" : "");
+                 (two && c.wide_columns ? "-c32" : "") +
+                 (other_split ? "-h" + std::to_string(c.split_high) : "");
     json::Writer w;
     w.begin_object()
         .field("schema_version", 1u)
@@ -317,6 +324,15 @@ NttEngine::NttEngine(const NttEngineConfig& c) : impl_(new Impl) {
 }
 
 NttEngine::~NttEngine() = default;
+
+std::vector<std::uint32_t> ntt_other_splits(std::uint32_t log_n) {
+    std::vector<std::uint32_t> out;
+    if (log_n < 13 || log_n > 20) return out;
+    const int l1 = split_l1(int(log_n));
+    for (const int h : {l1 - 1, l1 + 1})
+        if (alt_split(int(log_n), h)) out.push_back(std::uint32_t(h));
+    return out;
+}
 
 std::size_t NttEngine::workspace_bytes() const {
     return impl_->u32 ? impl_->u32->workspace_bytes() : impl_->u64->workspace_bytes();
@@ -346,6 +362,8 @@ std::string join(const std::vector<std::string>& names) {
 // 32-column tiles are the static choice where they measured faster: u32
 // 2^16-point transforms (C2 step 43.9-44.7 us against 44.9-45.3 us).
 bool wide_columns_default(const Request& r) { return r.word_bits == 32 && r.log_n == 16; }
+
+std::vector<std::uint32_t> other_splits(const Request& r) { return ntt_other_splits(r.log_n); }
 
 // Name of the static model's lowering: resident up to 2^12, then two passes.
 std::string default_name(const Request& r) {
@@ -392,6 +410,8 @@ class NttExecutor final : public Executor {
                   "'" + r.variant + "' is not a lowering of this NTT (available: " + join(names) + ")");
         c.force_strict = r.variant == default_name(r) + "-strict" + suffix;
         c.wide_columns = r.variant.empty() ? wide_columns_default(r) : r.variant == default_name(r) + "-c32" + suffix;
+        for (const std::uint32_t h : other_splits(r))
+            if (r.variant == default_name(r) + "-h" + std::to_string(h) + suffix) c.split_high = h;
         engine_ = std::make_unique<NttEngine>(c);
         algorithm = engine_->algorithm() + (r.pitched ? "-pitched" : "");
         mapping_json = engine_->mapping_json();
@@ -415,16 +435,18 @@ std::unique_ptr<Executor> make_ntt_executor(const Request& r) { return std::make
 
 // Lazy reduction (values in [0, 2q) / [0, 4q) between stages) where the
 // modulus leaves two spare bits, and the fully reduced butterflies.
-// u32 two-pass transforms also offer 32-column tiles in the column pass
-// (`-c32`: 128-byte row segments instead of 64).
+// Two-pass transforms also offer 32-column tiles in the column pass (`-c32`:
+// 128 / 256-byte row segments instead of 64 / 128) and, at 2^15..2^17, the
+// neighbouring splits of the high and low bits (`-h<l1>`).
 std::vector<std::string> ntt_candidates(const Request& r) {
     const std::string suffix = r.pitched ? "-pitched" : "";
     std::vector<std::string> names{default_name(r) + suffix};
     if (r.modulus < (std::uint64_t{1} << (r.word_bits - 2))) names.push_back(default_name(r) + "-strict" + suffix);
-    if (r.word_bits == 32 && r.log_n >= 13 && r.log_n <= 20) {
+    if (r.log_n >= 13 && r.log_n <= 20) {
         names.push_back(default_name(r) + "-c32" + suffix);
         if (wide_columns_default(r)) std::rotate(names.begin(), names.end() - 1, names.end());  // the default first
     }
+    for (const std::uint32_t h : other_splits(r)) names.push_back(default_name(r) + "-h" + std::to_string(h) + suffix);
     return names;
 }
 

@@ -1,0 +1,33 @@
+// Instantiates the NTT pass shapes beyond the planner's static choice for
+// u64 words, lazy and strict: the neighbouring splits of 2^15..2^17 (16- and
+// 32-column tiles) and 32-column tiles at the planner's split of every
+// two-pass length. They are candidates of MEASURE and RNS Prepare.
+#include "ntt_kernels.hpp"
+
+namespace cbw {
+namespace ntt_detail {
+namespace {
+template <bool LAZY>
+void register_alt() {
+    add_split<std::uint64_t, LAZY, 15, 6>();
+    add_split<std::uint64_t, LAZY, 15, 8>();
+    add_split<std::uint64_t, LAZY, 16, 7>();
+    add_split<std::uint64_t, LAZY, 16, 9>();
+    add_split<std::uint64_t, LAZY, 17, 7>();
+    add_split<std::uint64_t, LAZY, 17, 9>();
+    add_wide_columns<std::uint64_t, LAZY, 6, 7>();
+    add_wide_columns<std::uint64_t, LAZY, 7, 7>();
+    add_wide_columns<std::uint64_t, LAZY, 7, 8>();
+    add_wide_columns<std::uint64_t, LAZY, 8, 8>();
+    add_wide_columns<std::uint64_t, LAZY, 8, 9>();
+    add_wide_columns<std::uint64_t, LAZY, 8, 10>();
+    add_wide_columns<std::uint64_t, LAZY, 8, 11>();
+    add_wide_columns<std::uint64_t, LAZY, 8, 12>();
+}
+}  // namespace
+void register_alt_u64() {
+    register_alt<true>();
+    register_alt<false>();
+}
+}  // namespace ntt_detail
+}  // namespace cbw

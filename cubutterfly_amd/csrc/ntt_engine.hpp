@@ -44,7 +44,8 @@ struct NttEngineConfig {
     bool output_bit_reversed = false;
     bool reduce_input = true;  // reduce arbitrary words mod q on load
     bool force_strict = false; // fully reduced butterflies even where lazy ones fit
-    bool wide_columns = false; // u32 two-pass: 32-column tiles in the column pass (`-c32`)
+    bool wide_columns = false; // two-pass: 32-column tiles in the column pass (`-c32`)
+    std::uint32_t split_high = 0;  // two-pass: high (column-pass) bits; 0 = the planner's split (`-h<l1>`)
     std::vector<NttDomain> domains;
     std::vector<NttPolynomial> polynomials;  // empty: `batch` dense rows of domain 0
     std::uint64_t batch = 0;
@@ -68,5 +69,9 @@ class NttEngine {
     std::unique_ptr<Impl> impl_;
     std::string algorithm_, mapping_json_;
 };
+
+// Two-pass high-bit splits other than the planner's that have kernels at
+// 2^log_n (the `-h<l1>` lowerings), empty elsewhere.
+std::vector<std::uint32_t> ntt_other_splits(std::uint32_t log_n);
 
 }  // namespace cbw

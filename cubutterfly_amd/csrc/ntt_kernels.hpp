@@ -731,18 +731,46 @@ constexpr int kColLines = 4;
 constexpr int kWideColLines = 5;
 constexpr int row_lines(int l1, int l2) { return l1 < kTileLog - l2 ? l1 : kTileLog - l2; }
 
+// Column passes of one split with 32-column tiles, where they fit.
+template <class W, bool LAZY, int L1, int L2>
+void add_wide_columns() {
+    if constexpr (L1 + kWideColLines <= 13 && L2 >= kWideColLines) {
+        add_variants<W, LAZY, L1, kWideColLines, true, true, false, L1, L2>();
+        add_variants<W, LAZY, L1, kWideColLines, true, false, false, L1, L2>();
+    }
+}
+
+// Column passes of one split: 16-column tiles, and 32-column tiles (WIDE).
+template <class W, bool LAZY, int L1, int L2, bool WIDE>
+void add_columns() {
+    add_variants<W, LAZY, L1, kColLines, true, true, false, L1, L2>();
+    add_variants<W, LAZY, L1, kColLines, true, false, false, L1, L2>();
+    if constexpr (WIDE) add_wide_columns<W, LAZY, L1, L2>();
+}
+
+template <class W, bool LAZY, int L1, int L2>
+void add_rows() {
+    constexpr int rli = row_lines(L1, L2);
+    add_variants<W, LAZY, L2, rli, false, true, false, L1, L2>();
+    add_variants<W, LAZY, L2, rli, false, false, false, L1, L2>();
+}
+
+// The planner's split (l1 = split_l1): u32 with 16- and 32-column tiles,
+// u64 with 16 (32-column u64 tiles and other splits are instantiated by
+// ntt_alt_shapes.hip).
 template <class W, bool LAZY, int LOG_N>
 void add_two_pass() {
     constexpr int l1 = split_l1(LOG_N), l2 = LOG_N - l1;
-    constexpr int rli = row_lines(l1, l2);
-    add_variants<W, LAZY, l1, kColLines, true, true, false, l1, l2>();
-    add_variants<W, LAZY, l1, kColLines, true, false, false, l1, l2>();
-    if constexpr (sizeof(W) == 4 && l1 + kWideColLines <= 13 && l2 >= kWideColLines) {
-        add_variants<W, LAZY, l1, kWideColLines, true, true, false, l1, l2>();
-        add_variants<W, LAZY, l1, kWideColLines, true, false, false, l1, l2>();
-    }
-    add_variants<W, LAZY, l2, rli, false, true, false, l1, l2>();
-    add_variants<W, LAZY, l2, rli, false, false, false, l1, l2>();
+    add_columns<W, LAZY, l1, l2, sizeof(W) == 4>();
+    add_rows<W, LAZY, l1, l2>();
+}
+
+// Another split of LOG_N (both tile widths), for MEASURE and RNS Prepare.
+template <class W, bool LAZY, int LOG_N, int L1>
+void add_split() {
+    static_assert(L1 >= 4 && LOG_N - L1 >= 4 && LOG_N - L1 <= kTileLog, "split shape");
+    add_columns<W, LAZY, L1, LOG_N - L1, true>();
+    add_rows<W, LAZY, L1, LOG_N - L1>();
 }
 
 // 4 KiWord tiles; columns of 64 B (u32) / 128 B (u64).
@@ -775,6 +803,14 @@ void register_u32_lazy();
 void register_u32_strict();
 void register_u64_lazy();
 void register_u64_strict();
+void register_alt_u32();
+void register_alt_u64();
+
+// Splits l1 of two-pass lengths with kernels: the planner's split_l1 and the
+// neighbouring ones that ntt_alt_shapes.hip instantiates.
+constexpr bool alt_split(int log_n, int l1) {
+    return log_n >= 15 && log_n <= 17 && (l1 == split_l1(log_n) - 1 || l1 == split_l1(log_n) + 1);
+}
 
 }  // namespace ntt_detail
 }  // namespace cbw

@@ -7,8 +7,15 @@
 // exact ring order; disjoint output intervals; Prepare once (outside graph
 // capture) with a prepared-plan cache record; Execute asynchronous and
 // allocation-free with pointer aliasing matching the prepared placement.
-// The gfx950 lowering is the NttEngine (merged-twist CT forward / GS inverse),
-// so Prepare measures the static plan instead of searching mappings.
+// The gfx950 lowering is the NttEngine (merged-twist CT forward / GS inverse).
+// Prepare searches its mappings as the reference's RnsPlan::tune searches
+// its own (src/rns_ntt.cu:538-731): every legal candidate -- lazy or fully
+// reduced arithmetic, 16- or 32-column tiles, the planner's split of the high
+// and low bits or a neighbouring one -- is timed as a HIP graph of
+// `repetitions` calls on private buffers, the three fastest are timed three
+// more times (graphs of 3 x repetitions calls, median kept), and each
+// finalist's output must equal the static plan's on a seeded canonical
+// input before the fastest is selected.
 #include "../../include/cuntt/rns_c_api.h"
 
 #include "common.hpp"
@@ -23,6 +30,7 @@
 #include <fcntl.h>
 #include <fstream>
 #include <iomanip>
+#include <limits>
 #include <sstream>
 #include <string>
 #include <sys/stat.h>
@@ -180,10 +188,85 @@ void atomic_write(const std::string& directory, const std::string& path, const s
 
 }  // namespace
 
+namespace {
+
+// One lowering of an RNS request: the engine options Prepare searches.
+struct RnsMapping {
+    bool strict = false;      // fully reduced butterflies where lazy ones would fit
+    bool wide = false;        // 32-column tiles in the column pass
+    std::uint32_t split = 0;  // high (column-pass) bits; 0 = the planner's split
+    bool operator==(const RnsMapping& o) const { return strict == o.strict && wide == o.wide && split == o.split; }
+};
+
+// A lowering's engines: the transform, and for one-pass in-place plans whose
+// polynomials move, the same transform into dense private scratch.
+struct RnsLowering {
+    RnsMapping mapping;
+    std::unique_ptr<cbw::NttEngine> engine;
+    std::unique_ptr<cbw::NttEngine> to_scratch;
+    std::size_t scratch_bytes = 0;
+};
+
+RnsLowering lower(const RnsConfig& config, const RnsMapping& m, bool same_offsets) {
+    cbw::NttEngineConfig e;
+    e.word_bits = 64;
+    e.log_n = config.log_n;
+    e.negacyclic = config.negacyclic;
+    e.inverse = config.inverse;
+    e.input_bit_reversed = config.input_reversed;
+    e.output_bit_reversed = config.output_reversed;
+    e.reduce_input = false;  // canonical residues are the input contract
+    e.force_strict = m.strict;
+    e.wide_columns = m.wide;
+    e.split_high = m.split;
+    e.domains = config.domains;
+    e.polynomials = config.polynomials;
+    RnsLowering l;
+    l.mapping = m;
+    l.engine = std::make_unique<cbw::NttEngine>(e);
+    const std::uint64_t n = std::uint64_t{1} << config.log_n;
+    l.scratch_bytes = l.engine->workspace_bytes();
+    if (l.engine->passes() == 1 && !same_offsets) {
+        auto dense = e;
+        for (std::size_t p = 0; p < dense.polynomials.size(); ++p) dense.polynomials[p].output_offset = p * n;
+        l.to_scratch = std::make_unique<cbw::NttEngine>(dense);
+        l.scratch_bytes = config.polynomials.size() * n * sizeof(std::uint64_t);
+    }
+    return l;
+}
+
+// Mappings Prepare may choose for a request, the static plan first.
+std::vector<RnsMapping> candidates(const RnsConfig& c) {
+    std::uint64_t max_q = 0;
+    for (const auto& d : c.domains) max_q = std::max(max_q, d.modulus);
+    std::vector<bool> arithmetic{false};
+    if (max_q < (std::uint64_t{1} << 62)) arithmetic.push_back(true);  // lazy fits: strict is a second choice
+    std::vector<RnsMapping> out;
+    for (const bool strict : arithmetic) {
+        out.push_back({strict, false, 0});
+        if (c.log_n <= 12) continue;  // one pass: no columns, no split
+        out.push_back({strict, true, 0});
+        for (const std::uint32_t split : cbw::ntt_other_splits(c.log_n)) out.push_back({strict, false, split});
+    }
+    return out;
+}
+
+std::string mapping_name(const RnsMapping& m) {
+    return std::string(m.strict ? "strict" : "lazy") + (m.wide ? "-c32" : "-c16") +
+           (m.split ? "-h" + std::to_string(m.split) : "");
+}
+
+struct RnsMeasurement {
+    std::string mapping;    // mapping_name()
+    std::string algorithm;  // the engine's lowering name
+    double kernel_ms;
+};
+
+}  // namespace
+
 struct cubutterflyRnsPlanOpaque {
     RnsConfig config;
-    std::unique_ptr<cbw::NttEngine> engine;
-    std::unique_ptr<cbw::NttEngine> to_scratch;  // one-pass in-place with moved offsets
+    RnsLowering lowering;  // the selected mapping (the static plan until Prepare)
     cbw::DeviceBuffer scratch;
     std::uint64_t input_extent = 0, output_extent = 0;
     bool prepared = false, in_place = false, same_offsets = false;
@@ -192,21 +275,31 @@ struct cubutterflyRnsPlanOpaque {
     bool cache_hit = false;
     std::string cache_key, source;
     double kernel_ms = 0;
+    std::vector<RnsMeasurement> measurements;
 
-    void run(const std::uint64_t* in, std::uint64_t* out, hipStream_t stream) {
-        if (engine->passes() == 1 && in == out && !same_offsets) {
+    static void run(const RnsLowering& l, const RnsConfig& config, bool same_offsets, const std::uint64_t* in,
+                    std::uint64_t* out, void* scratch, hipStream_t stream) {
+        if (l.engine->passes() == 1 && in == out && !same_offsets) {
             // A one-pass tile would overwrite words another tile has not read:
             // transform into the private scratch, then move each polynomial.
-            to_scratch->execute(in, scratch.as<std::uint64_t>(), nullptr, stream);
+            auto* dense = static_cast<std::uint64_t*>(scratch);
+            l.to_scratch->execute(in, dense, nullptr, stream);
             const std::uint64_t n = std::uint64_t{1} << config.log_n;
             for (std::size_t p = 0; p < config.polynomials.size(); ++p)
-                cbw::hip_check(hipMemcpyAsync(out + config.polynomials[p].output_offset,
-                                              scratch.as<std::uint64_t>() + p * n, n * sizeof(std::uint64_t),
-                                              hipMemcpyDeviceToDevice, stream),
+                cbw::hip_check(hipMemcpyAsync(out + config.polynomials[p].output_offset, dense + p * n,
+                                              n * sizeof(std::uint64_t), hipMemcpyDeviceToDevice, stream),
                                "RNS scratch move");
             return;
         }
-        engine->execute(in, out, scratch.as<void>(), stream);
+        l.engine->execute(in, out, scratch, stream);
+    }
+    void run(const std::uint64_t* in, std::uint64_t* out, hipStream_t stream) {
+        run(lowering, config, same_offsets, in, out, scratch.as<void>(), stream);
+    }
+    // Makes `l` the plan's lowering, growing the private scratch if it needs more.
+    void select(RnsLowering l) {
+        if (l.scratch_bytes > scratch.bytes()) scratch.allocate(l.scratch_bytes);
+        lowering = std::move(l);
     }
 };
 
@@ -248,8 +341,165 @@ std::string identity_json(const cubutterflyRnsPlanOpaque& plan, int placement, u
         .field("multiprocessor_count", props.multiProcessorCount)
         .end_object();
     w.key("runtime").begin_object().field("hip_runtime_version", runtime).end_object();
-    w.key("protocol").begin_object().field("name", "mi355x_static_plan_timing_v1").field("repetitions", repetitions).end_object();
+    w.key("protocol").begin_object().field("name", "mi355x_candidate_sweep_v1").field("repetitions", repetitions).end_object();
     w.end_object();
+    return w.str();
+}
+
+// Time of one call of lowering `l`: a HIP graph of `repeat` calls captured on
+// a private stream, launched once untimed (its upload belongs to
+// preparation), then once between two events on `stream`
+// (reference src/rns_ntt.cu:566-622).
+double time_lowering(const cubutterflyRnsPlanOpaque& plan, const RnsLowering& l, const std::uint64_t* in,
+                     std::uint64_t* out, void* scratch, unsigned repeat, hipStream_t stream) {
+    cubutterflyRnsPlanOpaque::run(l, plan.config, plan.same_offsets, in, out, scratch, stream);
+    cbw::hip_check(hipStreamSynchronize(stream), "RNS candidate warm-up");
+    hipStream_t capture = nullptr;
+    cbw::hip_check(hipStreamCreateWithFlags(&capture, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    hipEvent_t start = nullptr, stop = nullptr;
+    auto release = [&] {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (start) (void)hipEventDestroy(start);
+        if (stop) (void)hipEventDestroy(stop);
+        if (capture) (void)hipStreamDestroy(capture);
+    };
+    try {
+        cbw::hip_check(hipStreamBeginCapture(capture, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            for (unsigned i = 0; i < repeat; ++i)
+                cubutterflyRnsPlanOpaque::run(l, plan.config, plan.same_offsets, in, out, scratch, capture);
+        } catch (...) {
+            hipGraph_t abandoned = nullptr;
+            (void)hipStreamEndCapture(capture, &abandoned);
+            if (abandoned) (void)hipGraphDestroy(abandoned);
+            throw;
+        }
+        cbw::hip_check(hipStreamEndCapture(capture, &graph), "hipStreamEndCapture");
+        cbw::hip_check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+        cbw::hip_check(hipEventCreate(&start), "hipEventCreate");
+        cbw::hip_check(hipEventCreate(&stop), "hipEventCreate");
+        cbw::hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+        cbw::hip_check(hipEventRecord(start, stream), "hipEventRecord");
+        cbw::hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+        cbw::hip_check(hipEventRecord(stop, stream), "hipEventRecord");
+        cbw::hip_check(hipEventSynchronize(stop), "hipEventSynchronize");
+        float ms = 0;
+        cbw::hip_check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+        if (!(ms > 0)) throw std::runtime_error("invalid RNS candidate timing");
+        release();
+        return double(ms) / repeat;
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+// Seeded canonical input words (each polynomial's residues below its
+// modulus; words outside every polynomial zero).
+std::vector<std::uint64_t> canonical_input(const RnsConfig& c, std::uint64_t extent) {
+    std::vector<std::uint64_t> words(extent, 0);
+    const std::uint64_t n = std::uint64_t{1} << c.log_n;
+    std::uint64_t state = 0x5eed5eedull;
+    for (const auto& p : c.polynomials) {
+        const std::uint64_t q = c.domains[p.domain].modulus;
+        for (std::uint64_t i = 0; i < n; ++i) {
+            state += 0x9e3779b97f4a7c15ull;  // splitmix64
+            std::uint64_t z = state;
+            z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+            z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+            words[p.input_offset + i] = (z ^ (z >> 31)) % q;
+        }
+    }
+    return words;
+}
+
+// The candidate sweep of Prepare: returns the selected lowering and every
+// measurement (the static plan's included).
+RnsLowering sweep(cubutterflyRnsPlanOpaque& plan, bool in_place, unsigned repetitions, hipStream_t stream,
+                  std::vector<RnsMeasurement>& tested) {
+    const std::uint64_t in_words = in_place ? std::max(plan.input_extent, plan.output_extent) : plan.input_extent;
+    cbw::DeviceBuffer in(in_words * 8), out(in_place ? 0 : plan.output_extent * 8);
+    std::uint64_t* destination = in_place ? in.as<std::uint64_t>() : out.as<std::uint64_t>();
+    cbw::hip_check(hipMemsetAsync(in.as<void>(), 0, in_words * 8, stream), "RNS prepare fill");
+    std::vector<RnsLowering> lowerings;
+    for (const RnsMapping& m : candidates(plan.config)) {
+        try {
+            lowerings.push_back(lower(plan.config, m, plan.same_offsets));
+        } catch (const cbw::NotSupported&) {
+            continue;  // a shape without kernels is no candidate
+        }
+    }
+    std::size_t scratch_bytes = 0;
+    for (const auto& l : lowerings) scratch_bytes = std::max(scratch_bytes, l.scratch_bytes);
+    cbw::DeviceBuffer scratch(scratch_bytes);
+    for (std::size_t i = 0; i < lowerings.size(); ++i)
+        tested.push_back({mapping_name(lowerings[i].mapping), lowerings[i].engine->algorithm(),
+                          time_lowering(plan, lowerings[i], in.as<std::uint64_t>(), destination, scratch.as<void>(),
+                                        repetitions, stream)});
+    // Finalists: the three fastest, each timed three more times with graphs
+    // of 3 x repetitions calls; the median decides.
+    std::vector<std::size_t> order(tested.size());
+    for (std::size_t i = 0; i < order.size(); ++i) order[i] = i;
+    std::sort(order.begin(), order.end(), [&](std::size_t a, std::size_t b) { return tested[a].kernel_ms < tested[b].kernel_ms; });
+    const std::size_t finalists = std::min<std::size_t>(3, order.size());
+    std::size_t best = order.front();
+    double best_ms = std::numeric_limits<double>::infinity();
+    for (std::size_t f = 0; f < finalists; ++f) {
+        std::vector<double> again;
+        for (int k = 0; k < 3; ++k)
+            again.push_back(time_lowering(plan, lowerings[order[f]], in.as<std::uint64_t>(), destination,
+                                          scratch.as<void>(), 3 * repetitions, stream));
+        std::sort(again.begin(), again.end());
+        if (again[1] < best_ms) {
+            best_ms = again[1];
+            best = order[f];
+        }
+    }
+    // Every finalist must reproduce the static plan's words on a seeded
+    // canonical input (separate buffers, so each sees the same input).
+    const auto host = canonical_input(plan.config, plan.input_extent);
+    cbw::DeviceBuffer check_in(plan.input_extent * 8), check_out(plan.output_extent * 8);
+    cbw::hip_check(hipMemcpy(check_in.as<void>(), host.data(), plan.input_extent * 8, hipMemcpyHostToDevice),
+                   "RNS validation input");
+    auto output_of = [&](const RnsLowering& l) {
+        cbw::hip_check(hipMemsetAsync(check_out.as<void>(), 0, plan.output_extent * 8, stream), "RNS validation fill");
+        cubutterflyRnsPlanOpaque::run(l, plan.config, plan.same_offsets, check_in.as<std::uint64_t>(),
+                                      check_out.as<std::uint64_t>(), scratch.as<void>(), stream);
+        std::vector<std::uint64_t> words(plan.output_extent);
+        cbw::hip_check(hipMemcpyAsync(words.data(), check_out.as<void>(), plan.output_extent * 8,
+                                      hipMemcpyDeviceToHost, stream),
+                       "RNS validation output");
+        cbw::hip_check(hipStreamSynchronize(stream), "RNS validation");
+        return words;
+    };
+    const auto expected = output_of(lowerings.front());  // the static plan
+    const std::uint64_t n = std::uint64_t{1} << plan.config.log_n;
+    for (std::size_t f = 0; f < finalists; ++f) {
+        if (order[f] == 0) continue;
+        const auto got = output_of(lowerings[order[f]]);
+        for (const auto& p : plan.config.polynomials)
+            if (!std::equal(got.begin() + p.output_offset, got.begin() + p.output_offset + n,
+                            expected.begin() + p.output_offset))
+                throw std::runtime_error("RNS candidate " + lowerings[order[f]].engine->algorithm() +
+                                         " disagrees with the static plan");
+    }
+    plan.kernel_ms = best_ms;
+    return std::move(lowerings[best]);
+}
+
+std::string measurements_json(const std::vector<RnsMeasurement>& tested) {
+    cbw::json::Writer w;
+    w.begin_array();
+    for (const auto& t : tested)
+        w.begin_object()
+            .field("mapping", t.mapping)
+            .field("algorithm", t.algorithm)
+            .field("kernel_ms", t.kernel_ms)
+            .end_object();
+    w.end_array();
     return w.str();
 }
 
@@ -268,28 +518,11 @@ int cubutterflyRnsCreate(const char* config_json_text, cubutterflyRnsPlan* resul
         plan->config = parse_config(config_json_text);
         validate(plan->config, plan->input_extent, plan->output_extent);
         cbw::hip_check(hipGetDevice(&plan->device), "hipGetDevice");
-        cbw::NttEngineConfig e;
-        e.word_bits = 64;
-        e.log_n = plan->config.log_n;
-        e.negacyclic = plan->config.negacyclic;
-        e.inverse = plan->config.inverse;
-        e.input_bit_reversed = plan->config.input_reversed;
-        e.output_bit_reversed = plan->config.output_reversed;
-        e.reduce_input = false;  // canonical residues are the input contract
-        e.domains = plan->config.domains;
-        e.polynomials = plan->config.polynomials;
-        plan->engine = std::make_unique<cbw::NttEngine>(e);
         plan->same_offsets = std::all_of(plan->config.polynomials.begin(), plan->config.polynomials.end(),
                                          [](const cbw::NttPolynomial& p) { return p.input_offset == p.output_offset; });
-        const std::uint64_t n = std::uint64_t{1} << plan->config.log_n;
-        std::size_t scratch_bytes = plan->engine->workspace_bytes();
-        if (plan->engine->passes() == 1 && !plan->same_offsets) {
-            auto dense = e;
-            for (std::size_t p = 0; p < dense.polynomials.size(); ++p) dense.polynomials[p].output_offset = p * n;
-            plan->to_scratch = std::make_unique<cbw::NttEngine>(dense);
-            scratch_bytes = plan->config.polynomials.size() * n * sizeof(std::uint64_t);
-        }
-        plan->scratch.allocate(scratch_bytes);  // private, outside timing (reference :286-366)
+        // The static plan until Prepare selects (private scratch allocated
+        // here, outside execution; reference :286-366).
+        plan->select(lower(plan->config, RnsMapping{}, plan->same_offsets));
         *result = plan.release();
     });
 }
@@ -301,7 +534,7 @@ int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* ca
         require(!plan->prepared, "plan is already prepared; create another plan to retune");
         require(placement == 0 || placement == 1, "invalid placement");
         require(policy >= 0 && policy <= 2, "invalid cache policy");
-        require(repetitions > 0, "repetitions must be positive");
+        require(repetitions > 0 && repetitions <= 1000, "RNS tuning repetitions must be in [1,1000]");
         const auto stream = static_cast<hipStream_t>(stream_handle);
         hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
         cbw::hip_check(hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
@@ -347,44 +580,46 @@ int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* ca
             };
             if (!same(stored, reparsed, same))
                 throw std::runtime_error("RNS cache identity mismatch (incompatible record or hash collision): " + path);
-            require(record.at("source").as_string("source") == "static_plan_timing",
+            require(record.at("source").as_string("source") == "candidate_sweep",
                     "unsupported RNS cache measurement provenance");
+            // The record names one of this request's candidates; it is rebuilt,
+            // never trusted beyond that.
+            const std::string selected = record.at("selected").as_string("selected");
+            const auto options = candidates(plan->config);
+            const auto it = std::find_if(options.begin(), options.end(),
+                                         [&](const RnsMapping& m) { return mapping_name(m) == selected; });
+            require(it != options.end(), "RNS cache record selects no mapping of this request: " + selected);
             plan->kernel_ms = record.at("kernel_ms").as_double("kernel_ms");
             require(plan->kernel_ms > 0, "invalid RNS cache kernel_ms");
+            plan->select(lower(plan->config, *it, plan->same_offsets));
+            for (const auto& m : record.at("candidates").items)
+                plan->measurements.push_back({m.at("mapping").as_string("mapping"),
+                                              m.at("algorithm").as_string("algorithm"),
+                                              m.at("kernel_ms").as_double("kernel_ms")});
             plan->cache_hit = true;
-            plan->source = "prepared_cache_timing_only";
+            plan->source = "prepared_cache";
         } else {
             if (policy == 1) throw std::runtime_error("required RNS prepared cache record is missing: " + path);
-            // Time the static plan on private zero-filled buffers.
-            const std::uint64_t words = std::max(plan->input_extent, plan->output_extent);
-            cbw::DeviceBuffer in(words * 8), out(words * 8);
-            cbw::hip_check(hipMemsetAsync(in.as<void>(), 0, words * 8, stream), "RNS prepare fill");
-            std::uint64_t* target = placement ? in.as<std::uint64_t>() : out.as<std::uint64_t>();
-            hipEvent_t start, stop;
-            cbw::hip_check(hipEventCreate(&start), "hipEventCreate");
-            cbw::hip_check(hipEventCreate(&stop), "hipEventCreate");
-            plan->run(in.as<std::uint64_t>(), target, stream);  // warm
-            cbw::hip_check(hipEventRecord(start, stream), "hipEventRecord");
-            for (unsigned r = 0; r < repetitions; ++r) plan->run(in.as<std::uint64_t>(), target, stream);
-            cbw::hip_check(hipEventRecord(stop, stream), "hipEventRecord");
-            cbw::hip_check(hipEventSynchronize(stop), "hipEventSynchronize");
-            float ms = 0;
-            cbw::hip_check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
-            (void)hipEventDestroy(start);
-            (void)hipEventDestroy(stop);
-            plan->kernel_ms = std::max(1e-6, double(ms) / repetitions);
-            plan->source = directory.empty() ? "uncached_static_plan_timing" : "static_plan_timing";
+            std::vector<RnsMeasurement> tested;
+            RnsLowering chosen = sweep(*plan, placement == 1, repetitions, stream, tested);
+            const std::string selected = mapping_name(chosen.mapping);
+            plan->select(std::move(chosen));
+            plan->measurements = std::move(tested);
+            plan->source = directory.empty() ? "uncached_candidate_sweep" : "candidate_sweep";
             if (!directory.empty()) {
                 cbw::json::Writer w;
                 w.begin_object()
                     .field("schema_version", 1u)
                     .key("identity")
                     .value_raw(identity)
+                    .field("selected", selected)
                     .key("mapping")
-                    .value_raw(plan->engine->mapping_json())
+                    .value_raw(plan->lowering.engine->mapping_json())
                     .field("kernel_ms", plan->kernel_ms)
-                    .field("source", "static_plan_timing")
-                    .field("validation", "timing_only_not_mathematically_validated")
+                    .field("source", "candidate_sweep")
+                    .key("candidates")
+                    .value_raw(measurements_json(plan->measurements))
+                    .field("validation", "finalists_bit_exact_against_static_plan")
                     .end_object();
                 atomic_write(directory, path, w.str() + "\n");
             }
@@ -419,7 +654,10 @@ int cubutterflyRnsInfoJson(cubutterflyRnsPlan plan, char* buffer, size_t* bytes)
             .key("request")
             .value_raw(config_json(plan->config))
             .key("mapping")
-            .value_raw(plan->engine->mapping_json())
+            .value_raw(plan->lowering.engine->mapping_json())
+            .field("selected", mapping_name(plan->lowering.mapping))
+            .key("candidates")
+            .value_raw(measurements_json(plan->measurements))
             .field("placement", plan->in_place ? "in_place" : "separate")
             .field("cache_hit", plan->cache_hit)
             .field("cache_key", plan->cache_key)

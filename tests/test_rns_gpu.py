@@ -66,6 +66,37 @@ def test_c4_full_size_round_trip(torch_gpu, rlib):
     np.testing.assert_array_equal(back.reshape(32, n), x)
 
 
+@pytest.mark.parametrize("inverse", [False, True])
+def test_prepare_sweeps_the_candidates(torch_gpu, rlib, inverse):
+    # Prepare times every mapping the gfx950 engine offers this request --
+    # lazy and strict arithmetic (the 60-bit primes leave two spare bits),
+    # 16- and 32-column tiles, the neighbouring splits 7 / 9 of the 16 index
+    # bits -- and executes the fastest; the result stays bit-exact.
+    print(f"case rns prepare sweep inverse={inverse}", flush=True)
+    log_n, n, limbs = 16, 1 << 16, 4
+    moduli = workloads.c4_moduli()[:limbs]
+    roots = [oracle.find_primitive_root(log_n + 1, q) for q in moduli]
+    x = np.stack([workloads.ntt_input(log_n, 1, q, seed=2, channel=i)[0] for i, q in enumerate(moduli)])
+    cfg = rns.request(log_n, list(zip(moduli, roots)), inverse=inverse)
+    stream = torch_gpu.cuda.Stream()
+    xd = to_device(torch_gpu, x.ravel())
+    yd = torch_gpu.empty_like(xd)
+    with rns.RnsPlan(rlib, cfg) as plan:
+        plan.prepare(stream.cuda_stream, repetitions=2)
+        plan.execute(xd, yd, stream.cuda_stream)
+        torch_gpu.cuda.synchronize()
+        info = plan.info()
+    mappings = [c["mapping"] for c in info["candidates"]]
+    assert mappings == ["lazy-c16", "lazy-c32", "lazy-c16-h7", "lazy-c16-h9",
+                        "strict-c16", "strict-c32", "strict-c16-h7", "strict-c16-h9"]
+    assert all(c["kernel_ms"] > 0 for c in info["candidates"])
+    assert info["selected"] in mappings and info["source"] == "uncached_candidate_sweep"
+    assert info["kernel_ms"] > 0 and info["mapping"]["algorithm"] in [c["algorithm"] for c in info["candidates"]]
+    expected = oracle.rns(x, moduli, roots, inverse=inverse, input_bit_reversed=inverse,
+                          output_bit_reversed=not inverse, threads=oracle.default_threads())
+    np.testing.assert_array_equal(to_host(torch_gpu, yd, np.uint64).reshape(limbs, n), expected)
+
+
 def reference_layout(log_n, negacyclic, inverse, in_rev, out_rev):
     """Config and input of tests/test_rns_ntt.cu:113-162."""
     n = 1 << log_n
@@ -155,12 +186,23 @@ def test_prepare_cache_contract(torch_gpu, rlib, tmp_path):
             plan.prepare(stream)  # already prepared
     records = list(tmp_path.glob("rns-v1-*.json"))
     assert len(records) == 1 and records[0].stem == first["cache_key"]
+    record = json.loads(records[0].read_text())
+    assert record["selected"] == first["selected"] and record["source"] == "candidate_sweep"
+    assert [c["mapping"] for c in record["candidates"]] == ["lazy-c16", "strict-c16"]  # one pass: arithmetic only
+    assert record["validation"] == "finalists_bit_exact_against_static_plan"
     with rns.RnsPlan(rlib, cfg) as plan:
         plan.prepare(stream, cache_dir=tmp_path, cache="require")
         hit = plan.info()
         assert hit["cache_hit"] and hit["kernel_ms"] == first["kernel_ms"]
+        assert hit["selected"] == first["selected"] and hit["candidates"] == first["candidates"]
+    # A record that selects no mapping of the request is refused.
+    tampered = dict(record, selected="lazy-c64")
+    records[0].write_text(json.dumps(tampered))
+    with rns.RnsPlan(rlib, cfg) as plan:
+        with pytest.raises(cb.AbiError) as info:
+            plan.prepare(stream, cache_dir=tmp_path, cache="require")
+        assert "selects no mapping" in str(info.value)
     # A record whose identity differs is refused, not replayed.
-    record = json.loads(records[0].read_text())
     record["identity"]["placement"] = "in_place"
     records[0].write_text(json.dumps(record))
     with rns.RnsPlan(rlib, cfg) as plan:

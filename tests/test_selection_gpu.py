@@ -104,27 +104,44 @@ def test_every_fft_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path
         fft_ok(torch_gpu, lib, t, stream, log_n, batch, inverse, **opts)
 
 
-@pytest.mark.parametrize("log_n", [10, 13, 14, 16, 17])
+QDEF = 1152921504606584833  # include/cuntt/ntt.hpp:17
+
+
+def ntt_words(log_n, batch, bits, inverse):
+    if bits == 32:
+        return ntt(log_n, batch, inverse)
+    return cb.describe(cb.Operator.NTT, cb.DataType.UINT64, [1 << log_n], compute=cb.ComputeType.UINT64, batch=batch,
+                       modulus=QDEF, word_bits=64, ntt_ring=cb.NttRing.NEGACYCLIC, inverse=inverse)
+
+
+@pytest.mark.parametrize("bits", [32, 64])
+@pytest.mark.parametrize("log_n", [10, 13, 14, 15, 16, 17])
 @pytest.mark.parametrize("inverse", [False, True])
-def test_ntt_strict_candidate(torch_gpu, lib, stream, tmp_path, log_n, inverse):
+def test_every_ntt_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path, bits, log_n, inverse):
+    print(f"case ntt candidates u{bits} log_n={log_n} inverse={inverse}", flush=True)
     batch = 4
-    t = ntt(log_n, batch, inverse)
+    t = ntt_words(log_n, batch, bits, inverse)
     with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream,
                  cache_path=tmp_path / "c.tsv") as plan:
         names = measured(plan)
-    # Lazy and strict; u32 two-pass lengths add 32-column tiles, the static
-    # choice (listed first) at 2^16.
-    base = "ntt-u32-negacyclic-" + ("two-pass-r16" if log_n > 12 else "resident-r16")
+    # Lazy and strict; two-pass lengths add 32-column tiles (the static choice,
+    # listed first, for u32 at 2^16) and at 2^15..2^17 the neighbouring
+    # splits of the high and low bits.
+    base = f"ntt-u{bits}-negacyclic-" + ("two-pass-r16" if log_n > 12 else "resident-r16")
     expected = [base, base + "-strict"] + ([base + "-c32"] if log_n >= 13 else [])
-    if log_n == 16:
+    if log_n == 16 and bits == 32:
         expected = expected[-1:] + expected[:-1]
+    l1 = min(8, log_n // 2)
+    if 15 <= log_n <= 17:
+        expected += [f"{base}-h{l1 - 1}", f"{base}-h{l1 + 1}"]
     assert names == expected
+    q = Q30 if bits == 32 else QDEF
     rng = np.random.default_rng(log_n)
-    x = rng.integers(0, 1 << 32, (batch, 1 << log_n), dtype=np.uint64).astype(np.uint32)
-    expected = oracle.ntt_negacyclic(x.astype(np.uint64) % Q30, Q30, inverse=inverse).astype(np.uint32)
+    words = np.uint32 if bits == 32 else np.uint64
+    x = rng.integers(0, np.iinfo(words).max, (batch, 1 << log_n), dtype=np.uint64, endpoint=True).astype(words)
+    expected = oracle.ntt_negacyclic(x.astype(np.uint64) % np.uint64(q), q, inverse=inverse).astype(words)
     for name in names:
-        opts = {"algorithm": name}
-        got = run_plan(torch_gpu, lib, t, x, stream, **opts)
+        got = run_plan(torch_gpu, lib, t, x, stream, algorithm=name)
         np.testing.assert_array_equal(got, expected, err_msg=name)
 
 
