@@ -257,6 +257,25 @@ struct PitchedOut {
     }
 };
 
+// y = (x * norm) * scale, each product rounded to fp32, as the reference's
+// finalize and narrowing kernels apply them; a factor of exactly 1 is
+// skipped (x * 1 = x), by a uniform branch on the kernel arguments. The
+// results are then hidden from the optimiser, so a product is not fused
+// with the FP16 narrowing into one rounding.
+template <int N>
+__device__ __forceinline__ void finalize(float (&v)[N], float norm, float scale) {
+    if (norm != 1.0f) {
+#pragma unroll
+        for (int r = 0; r < N; ++r) v[r] = v[r] * norm;
+    }
+    if (scale != 1.0f) {
+#pragma unroll
+        for (int r = 0; r < N; ++r) v[r] = v[r] * scale;
+    }
+#pragma unroll
+    for (int r = 0; r < N; ++r) opaque(v[r]);
+}
+
 // The butterflies of one tile and its store through `out`.
 template <int LOG_N, int LB, class Io, class Out>
 __device__ __forceinline__ void transform_store(float (&v)[kE], float* lds, unsigned t, const Out& out, float norm,
@@ -282,20 +301,18 @@ __device__ __forceinline__ void transform_store(float (&v)[kE], float* lds, unsi
     // The products land in new registers (not in `v`), so the caller can keep
     // `v` free of pending store data (see the tile loop).
     if constexpr (kDirectStore) {
+        float y[kE];
 #pragma unroll
-        for (int r = 0; r < kE; ++r) {
-            float y = (v[r] * norm) * scale;
-            opaque(y);
-            out.one(phase_index<kLast, LB>(t, r), y);
-        }
+        for (int r = 0; r < kE; ++r) y[r] = v[r];
+        finalize<kE>(y, norm, scale);
+#pragma unroll
+        for (int r = 0; r < kE; ++r) out.one(phase_index<kLast, LB>(t, r), y[r]);
     } else {
         if constexpr (kPhases > 1) exchange<kLast, 0, LB>(v, lds, t);
         float x[kE];
 #pragma unroll
-        for (int r = 0; r < kE; ++r) {
-            x[r] = (v[r] * norm) * scale;
-            opaque(x[r]);
-        }
+        for (int r = 0; r < kE; ++r) x[r] = v[r];
+        finalize<kE>(x, norm, scale);
         out.sixteen(t, x);
     }
 }
@@ -428,17 +445,25 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_pitched_kernel(const typ
 constexpr int kLW = 5;
 constexpr int kW = 1 << kLW;
 
-__device__ __forceinline__ unsigned wide_lds_addr(unsigned i) { return i + (i >> kLW); }
+__device__ __forceinline__ constexpr unsigned wide_lds_addr(unsigned i) { return i + (i >> kLW); }
 
 template <int LOG_N>
 struct WideMap {
     static constexpr int kP = kLW - (LOG_N - 10);  // passenger bits of phase 2
-    static __device__ __forceinline__ unsigned i0(unsigned t, unsigned r) { return (t << kLW) | r; }
-    static __device__ __forceinline__ unsigned i1(unsigned t, unsigned r) {
+    static __device__ __forceinline__ constexpr unsigned i0(unsigned t, unsigned r) { return (t << kLW) | r; }
+    static __device__ __forceinline__ constexpr unsigned i1(unsigned t, unsigned r) {
         return (t & 31u) | (r << 5) | ((t >> 5) << 10);
     }
-    static __device__ __forceinline__ unsigned i2(unsigned t, unsigned r) {
+    static __device__ __forceinline__ constexpr unsigned i2(unsigned t, unsigned r) {
         return (r & ((1u << kP) - 1u)) | (t << kP) | ((r >> kP) << 10);
+    }
+    // LDS word of element I(t, r): each map is a sum over disjoint bit
+    // fields of t and r, and so is wide_lds_addr (i / 32 of disjoint fields is
+    // the sum of their parts), so the word is a per-thread base plus a
+    // compile-time register offset that folds into the LDS instruction.
+    template <unsigned (*I)(unsigned, unsigned)>
+    static __device__ __forceinline__ unsigned lds_word(unsigned t, int r) {
+        return wide_lds_addr(I(t, 0u)) + wide_lds_addr(I(0u, unsigned(r)));
     }
 };
 
@@ -549,23 +574,19 @@ __global__ __launch_bounds__(1 << (LOG_N - kLW), 4) void fwht_wide_kernel(const 
         wide_stages<0, kLW>(v);
         lds_barrier();  // readers of the previous tile's image are done
 #pragma unroll
-        for (int r = 0; r < kW; ++r) lds[wide_lds_addr(M::i0(t, r))] = v[r];
+        for (int r = 0; r < kW; ++r) lds[M::template lds_word<M::i0>(t, r)] = v[r];
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kW; ++r) v[r] = lds[wide_lds_addr(M::i1(t, r))];
+        for (int r = 0; r < kW; ++r) v[r] = lds[M::template lds_word<M::i1>(t, r)];
         wide_stages<0, kLW>(v);
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kW; ++r) lds[wide_lds_addr(M::i1(t, r))] = v[r];
+        for (int r = 0; r < kW; ++r) lds[M::template lds_word<M::i1>(t, r)] = v[r];
         lds_barrier();
 #pragma unroll
-        for (int r = 0; r < kW; ++r) v[r] = lds[wide_lds_addr(M::i2(t, r))];
+        for (int r = 0; r < kW; ++r) v[r] = lds[M::template lds_word<M::i2>(t, r)];
         wide_stages<M::kP, kLW>(v);
-#pragma unroll
-        for (int r = 0; r < kW; ++r) {
-            v[r] = (v[r] * norm) * scale;
-            opaque(v[r]);
-        }
+        finalize<kW>(v, norm, scale);
         const __amdgpu_buffer_rsrc_t dst = make_rsrc(output + std::uint64_t(row) * out_pitch, kBytes);
 #pragma unroll
         for (int g = 0; g < kW / kRun; ++g)

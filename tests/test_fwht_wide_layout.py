@@ -8,6 +8,7 @@ WideMap and wide_lds_addr), restated here:
   order (the reference's stage order, src/butterfly_reference.cpp:349-369);
 * the registers of phase 2 below bit P (P = 15 - log n) are element bits
   0..P-1, so each thread's results form runs of 2^P consecutive elements;
+* each LDS word splits into a per-thread base plus a register offset;
 * every 32-lane group of the four exchange accesses (phase-0 write, phase-1
   read and write, phase-2 read) lands on 32 distinct banks of the padded image
   addr = i + i/32.
@@ -69,3 +70,16 @@ def test_the_padded_image_fits_the_kernel_array():
     for log_n in (11, 12, 13):
         n = 1 << log_n
         assert max(lds_addr(i) for i in range(n)) < n + (n >> 5)
+
+
+@pytest.mark.parametrize("log_n", [11, 12, 13])
+def test_lds_words_split_into_thread_and_register_parts(log_n):
+    # The kernel addresses element I(t, r) at lds_addr(I(t, 0)) +
+    # lds_addr(I(0, r)) (WideMap::lds_word): a per-thread base plus a
+    # compile-time register offset. That equals lds_addr(I(t, r)) for every
+    # map, thread and register.
+    _, threads, (i0, i1, i2) = maps(log_n)
+    for f in (i0, i1, i2):
+        for t in range(threads):
+            for r in range(32):
+                assert lds_addr(f(t, 0)) + lds_addr(f(0, r)) == lds_addr(f(t, r))
