@@ -101,6 +101,22 @@ __device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t r, unsigned of
     return make_uint4(x[0], x[1], x[2], x[3]);
 }
 
+// The first radix-2 stage straight from one packed fp16 pair (lo = the even
+// element, hi = the odd one): s = lo + hi, d = lo - hi in fp32. Both halves
+// widen to fp32 exactly and v_fma_mix_f32 computes lo * 1.0 + (+-hi) with a
+// single fp32 rounding, so s and d equal the fp32 sum and difference of the
+// widened values bit for bit, in one instruction each instead of three.
+__device__ __forceinline__ void f16x2_sum_diff(unsigned w, float& s, float& d) {
+    asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(s) : "v"(w));
+    asm("v_fma_mix_f32 %0, %1, 1.0, -%1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(d) : "v"(w));
+}
+
+// Two fp32 values narrowed to one packed fp16 pair, round to nearest even
+// (v_cvt_pk_f16_f32: the same rounding as two __float2half_rn).
+__device__ __forceinline__ unsigned pack_f16x2(float lo, float hi) {
+    return __builtin_bit_cast(unsigned, __floats2half2_rn(lo, hi));
+}
+
 struct F32Io {
     using T = float;
     // 16 consecutive floats at byte offset `off` of a tile's buffer.
@@ -168,11 +184,7 @@ struct F16Io {
         for (int k = 0; k < 2; ++k) {
             unsigned w[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const unsigned lo = __half_as_ushort(__float2half_rn(v[8 * k + 2 * j + 0]));
-                const unsigned hi = __half_as_ushort(__float2half_rn(v[8 * k + 2 * j + 1]));
-                w[j] = lo | (hi << 16);
-            }
+            for (int j = 0; j < 4; ++j) w[j] = pack_f16x2(v[8 * k + 2 * j], v[8 * k + 2 * j + 1]);
             q[k] = make_uint4(w[0], w[1], w[2], w[3]);
         }
     }
@@ -504,15 +516,17 @@ __device__ __forceinline__ void wide_load(__amdgpu_buffer_rsrc_t r, unsigned off
     }
 }
 
+// The raw words as 32 fp32 elements with the first stage (register bit 0)
+// already applied; for fp16 each word is that stage's pair.
 template <class Io>
-__device__ __forceinline__ void wide_unpack(const unsigned (&w)[wide_words<Io>()], float (&v)[kW]) {
+__device__ __forceinline__ void wide_unpack_first_stage(const unsigned (&w)[wide_words<Io>()], float (&v)[kW]) {
+    if constexpr (sizeof(typename Io::T) == 4) {
 #pragma unroll
-    for (int r = 0; r < kW; ++r) {
-        if constexpr (sizeof(typename Io::T) == 4) {
-            v[r] = __uint_as_float(w[r]);
-        } else {
-            v[r] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[r >> 1] >> (16 * (r & 1)))));
-        }
+        for (int r = 0; r < kW; ++r) v[r] = __uint_as_float(w[r]);
+        wide_stages<0, 1>(v);
+    } else {
+#pragma unroll
+        for (int k = 0; k < kW / 2; ++k) f16x2_sum_diff(w[k], v[2 * k], v[2 * k + 1]);
     }
 }
 
@@ -527,9 +541,7 @@ __device__ __forceinline__ void wide_store_run(__amdgpu_buffer_rsrc_t r, unsigne
         if constexpr (sizeof(typename Io::T) == 4) {
             w[k] = __float_as_uint(x[k]);
         } else {
-            const unsigned lo = __half_as_ushort(__float2half_rn(x[2 * k]));
-            const unsigned hi = __half_as_ushort(__float2half_rn(x[2 * k + 1]));
-            w[k] = lo | (hi << 16);
+            w[k] = pack_f16x2(x[2 * k], x[2 * k + 1]);
         }
     }
     using V4 = __attribute__((ext_vector_type(4))) unsigned;
@@ -570,8 +582,9 @@ __global__ __launch_bounds__(1 << (LOG_N - kLW), 4) void fwht_wide_kernel(const 
     const unsigned out_off = (t << M::kP) * unsigned(sizeof(T));
     unsigned tile = blockIdx.x;
 
+    // `v` arrives with register bit 0 butterflied (wide_unpack_first_stage).
     auto transform = [&](float (&v)[kW], unsigned row) {
-        wide_stages<0, kLW>(v);
+        wide_stages<1, kLW>(v);
         lds_barrier();  // readers of the previous tile's image are done
 #pragma unroll
         for (int r = 0; r < kW; ++r) lds[M::template lds_word<M::i0>(t, r)] = v[r];
@@ -603,7 +616,7 @@ __global__ __launch_bounds__(1 << (LOG_N - kLW), 4) void fwht_wide_kernel(const 
         load(following, more, nxt);
         __builtin_amdgcn_sched_barrier(0);
         float v[kW];
-        wide_unpack<Io>(cur, v);
+        wide_unpack_first_stage<Io>(cur, v);
         transform(v, tile);
         // `cur` stays allocated through the stores (see the 16-register kernel).
 #pragma unroll
@@ -625,7 +638,7 @@ __global__ __launch_bounds__(1 << (LOG_N - kLW), 4) void fwht_wide_kernel(const 
             unsigned w[wide_words<Io>()];
             load(tile, true, w);
             float v[kW];
-            wide_unpack<Io>(w, v);
+            wide_unpack_first_stage<Io>(w, v);
             transform(v, tile);
         }
     }
