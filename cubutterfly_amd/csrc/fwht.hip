@@ -480,13 +480,13 @@ struct WideMap {
 };
 
 // Radix-2 stages on register bits [LO, HI), lowest first.
-template <int LO, int HI>
-__device__ __forceinline__ void wide_stages(float (&v)[kW]) {
+template <int LO, int HI, int N>
+__device__ __forceinline__ void wide_stages(float (&v)[N]) {
 #pragma unroll
     for (int j = LO; j < HI; ++j) {
         const int d = 1 << j;
 #pragma unroll
-        for (int r = 0; r < kW; ++r) {
+        for (int r = 0; r < N; ++r) {
             if ((r & d) == 0) {
                 const float a = v[r];
                 const float b = v[r + d];
@@ -652,6 +652,152 @@ void launch_wide(const void* in, void* out, std::uint64_t rows, std::uint64_t in
                        static_cast<unsigned>(rows), in_pitch, out_pitch, norm, scale);
 }
 
+// ---- 64 elements per lane, no LDS (rows of 2^5 .. 2^8 points) --------------
+//
+// A wave owns 4096 consecutive elements (4096 / n rows) and each lane 64 of
+// them: four runs of 16 consecutive elements. Element index bits:
+//   0-3   register bits 0-3 (position in the run),
+//   4, 5  lane bits 4, 5 (the run's quarter of a 64-element line),
+//   6, 7  register bits 4, 5 (which of the lane's four lines),
+//   8-11  lane bits 0-3.
+// So each 16-byte load or store instruction touches 16 lines of 128 bytes
+// (as many as the 16-register kernel's), and the bits a row of <= 256 points
+// butterflies are register bits or lane bits 4 and 5. gfx950's lane-swap
+// instructions exchange those two lane bits with register bits
+// (v_permlane16_swap: lane bit 4, v_permlane32_swap: lane bit 5; each swaps a
+// register pair's values between lane halves, a 2 x 2 transpose): after
+// register bits 0-3 are butterflied, bit 4 is swapped into register bit 0 and
+// bit 5 into register bit 1, each butterflied there, then bits 6 and 7 in
+// register bits 4 and 5, and the two swaps are undone for the stores. No
+// LDS, no barrier, the waves are independent. Same stages in the same order
+// (bits 0, 1, ..., log n - 1) as the other kernels, so results are
+// bit-identical.
+constexpr int kLaneLog = 6;
+constexpr int kLaneRegs = 1 << kLaneLog;
+constexpr int kLaneTileLog = kLaneLog + 6;  // elements per wave
+constexpr int kLaneWaves = 4;               // waves per workgroup
+
+// Element (within the wave's 4096) of lane l's register 0, and of register r
+// of lane 0: the index is their sum (disjoint bit fields).
+__device__ __forceinline__ unsigned lane_element(unsigned l) {
+    return (((l >> 4) & 3u) << 4) | ((l & 15u) << 8);
+}
+constexpr unsigned register_element(unsigned r) { return (r & 15u) | ((r >> 4) << 6); }
+
+// Exchanges register bit RB with lane bit LANE_BIT (4 or 5) in every register
+// pair that differs in bit RB: afterwards the pair is indexed by the old lane
+// bit and the lane bit by the old register bit.
+template <int LANE_BIT, int RB, int N>
+__device__ __forceinline__ void swap_lane_bit(float (&v)[N]) {
+    static_assert(LANE_BIT == 4 || LANE_BIT == 5, "gfx950 swaps lane bits 4 and 5");
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        if ((r >> RB) & 1) continue;
+        const int p = r | (1 << RB);
+        const auto s = LANE_BIT == 5 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v[r]), __float_as_uint(v[p]),
+                                                                        false, false)
+                                     : __builtin_amdgcn_permlane16_swap(__float_as_uint(v[r]), __float_as_uint(v[p]),
+                                                                        false, false);
+        v[r] = __uint_as_float(s[0]);
+        v[p] = __uint_as_float(s[1]);
+    }
+}
+
+// Byte offset of element e of the wave's rows at pitch `pitch` (elements):
+// row e >> log n, column e mod n. Additive over disjoint bit fields of e.
+template <int LOG_N, int B>
+__device__ __forceinline__ unsigned lane_offset(unsigned e, std::uint64_t pitch) {
+    return unsigned(((e >> LOG_N) * pitch + (e & ((1u << LOG_N) - 1u))) * B);
+}
+
+// Rows of a tile (4096 / n rows, one wave) at input + row * pitch (elements;
+// packed rows have pitch n); rows past `rows` are absent (the buffer range
+// drops their accesses, and every 16-byte access lies in one row). Wave w of
+// the grid takes tile w. (A persistent grid, each wave walking tiles with the
+// next tile's loads in flight, measured slower: C5b 57.4-58.8 us against
+// 54.2 us.)
+template <int LOG_N, class Io>
+__global__ __launch_bounds__(64 * kLaneWaves) void fwht_lane_kernel(const typename Io::T* __restrict__ input,
+                                                                    typename Io::T* output, unsigned rows,
+                                                                    std::uint64_t in_pitch,
+                                                                    std::uint64_t out_pitch, float norm,
+                                                                    float scale) {
+    static_assert(LOG_N >= 5 && LOG_N <= 8, "bits 4 and 5 are the lane bits swapped in");
+    using T = typename Io::T;
+    constexpr unsigned kN = 1u << LOG_N;
+    constexpr unsigned kRowsPerWave = 1u << (kLaneTileLog - LOG_N);
+    constexpr unsigned kB = sizeof(T);
+    constexpr int kPerAccess = 16 / int(kB);  // elements per 16-byte access
+    constexpr int kWords = kLaneRegs * int(kB) / 4;
+    const unsigned lane = threadIdx.x & 63u;
+    const unsigned tiles = (rows + kRowsPerWave - 1u) / kRowsPerWave;
+    const unsigned tile = uniform(blockIdx.x * unsigned(kLaneWaves) + (threadIdx.x >> 6));
+    if (tile >= tiles) return;
+    const unsigned le = lane_element(lane);
+    const unsigned in_base = lane_offset<LOG_N, kB>(le, in_pitch);
+    const unsigned out_base = lane_offset<LOG_N, kB>(le, out_pitch);
+    // Buffer over the tile's existing rows.
+    const std::uint64_t row0 = std::uint64_t(tile) * kRowsPerWave;
+    const unsigned present = unsigned(min(std::uint64_t(kRowsPerWave), rows - row0));
+    auto span = [&](const T* base, std::uint64_t pitch) {
+        return make_rsrc(base + row0 * pitch, unsigned(((present - 1u) * pitch + kN) * kB));
+    };
+    // Raw words of the lane's 64 elements, 16 bytes per access, registers in order.
+    unsigned w[kWords];
+    const __amdgpu_buffer_rsrc_t src = span(input, in_pitch);
+#pragma unroll
+    for (int a = 0; a < kLaneRegs / kPerAccess; ++a) {
+        const unsigned off = in_base + lane_offset<LOG_N, kB>(register_element(unsigned(a * kPerAccess)), in_pitch);
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(src, static_cast<int>(off), 0, 0);
+        w[4 * a + 0] = x[0];
+        w[4 * a + 1] = x[1];
+        w[4 * a + 2] = x[2];
+        w[4 * a + 3] = x[3];
+    }
+    float v[kLaneRegs];
+    if constexpr (kB == 4) {
+#pragma unroll
+        for (int r = 0; r < kLaneRegs; ++r) v[r] = __uint_as_float(w[r]);
+        wide_stages<0, 1>(v);
+    } else {
+#pragma unroll
+        for (int k = 0; k < kLaneRegs / 2; ++k) f16x2_sum_diff(w[k], v[2 * k], v[2 * k + 1]);
+    }
+    wide_stages<1, 4>(v);    // element bits 1-3
+    swap_lane_bit<4, 0>(v);  // register bit 0 <- element bit 4
+    wide_stages<0, 1>(v);
+    if constexpr (LOG_N >= 6) {
+        swap_lane_bit<5, 1>(v);  // register bit 1 <- element bit 5
+        wide_stages<1, 2>(v);
+    }
+    if constexpr (LOG_N >= 7) wide_stages<4, LOG_N - 2>(v);  // element bits 6, 7 in register bits 4, 5
+    if constexpr (LOG_N >= 6) swap_lane_bit<5, 1>(v);
+    swap_lane_bit<4, 0>(v);
+    finalize<kLaneRegs>(v, norm, scale);
+    const __amdgpu_buffer_rsrc_t dst = span(output, out_pitch);
+    using V4 = __attribute__((ext_vector_type(4))) unsigned;
+#pragma unroll
+    for (int a = 0; a < kLaneRegs / kPerAccess; ++a) {
+        unsigned o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * a + j;
+            if constexpr (kB == 4) o[j] = __float_as_uint(v[e]);
+            else o[j] = pack_f16x2(v[2 * e], v[2 * e + 1]);
+        }
+        const unsigned off = out_base + lane_offset<LOG_N, kB>(register_element(unsigned(a * kPerAccess)), out_pitch);
+        __builtin_amdgcn_raw_buffer_store_b128(V4{o[0], o[1], o[2], o[3]}, dst, static_cast<int>(off), 0, 0);
+    }
+}
+
+template <int LOG_N, class Io>
+void launch_lanes(const void* in, void* out, std::uint64_t rows, std::uint64_t in_pitch, std::uint64_t out_pitch,
+                  float norm, float scale, unsigned grid, hipStream_t stream) {
+    hipLaunchKernelGGL((fwht_lane_kernel<LOG_N, Io>), dim3(grid), dim3(64 * kLaneWaves), 0, stream,
+                       static_cast<const typename Io::T*>(in), static_cast<typename Io::T*>(out),
+                       static_cast<unsigned>(rows), in_pitch, out_pitch, norm, scale);
+}
+
 using Launch = void (*)(const void*, void*, std::uint64_t, float, float, unsigned, hipStream_t);
 
 template <int LOG_N, class Io>
@@ -743,38 +889,87 @@ WideLaunch wide_launcher(const Request& r) {
     return wide_table_entry(int(r.log_n), std::make_integer_sequence<int, 3>{});
 }
 
+template <class Io, int... L>
+PitchedLaunch lane_table_entry(int log_n, std::integer_sequence<int, L...>) {
+    PitchedLaunch table[] = {launch_lanes<L + 5, Io>...};
+    return table[log_n - 5];
+}
+
+// The 64-elements-per-lane kernel: rows of 2^5 .. 2^8 points, row count
+// within 32 bits, a wave's pitched span within 31-bit byte offsets.
+PitchedLaunch lane_launcher(const Request& r) {
+    if (r.log_n < 5 || r.log_n > 8 || r.batch > 0xffffffffull) return nullptr;
+    if (r.pitched) {
+        const std::uint64_t rows_per_wave = std::uint64_t{1} << (kLaneTileLog - r.log_n);
+        const std::uint64_t pitch = std::max(r.in_batch_stride, r.out_batch_stride);
+        const std::uint64_t bytes = r.fp16_final ? 2 : 4;
+        if (rows_per_wave * pitch * bytes >= (std::uint64_t{1} << 31)) return nullptr;
+    }
+    return r.fp16_final ? lane_table_entry<F16Io>(int(r.log_n), std::make_integer_sequence<int, 4>{})
+                        : lane_table_entry<F32Io>(int(r.log_n), std::make_integer_sequence<int, 4>{});
+}
+
+// Kernel families of the FWHT lowerings.
+enum class FwhtKind { Resident, Wide, WidePersistent, Lanes };
+
 class FwhtExecutor final : public Executor {
   public:
-    // `wide`: the 32-register kernel (packed or pitched rows) in place of
-    // the 16-register ones; `persistent`: its grid sized to the resident
-    // workgroups, each walking rows with next-row prefetch.
-    FwhtExecutor(const Request& r, Launch launch, PitchedLaunch pitched, WideLaunch wide, bool persistent)
-        : r_(r), launch_(launch), pitched_(pitched), wide_(persistent ? wide.walk : wide.launch) {
+    // Resident: the 16-register kernels (`launch` packed, `pitched` pitched
+    // rows); Wide: the 32-register kernel, one tile per workgroup's turn;
+    // WidePersistent: its grid sized to the resident workgroups, each walking
+    // rows with next-row prefetch; Lanes: 64 elements per lane, no LDS, one
+    // tile per wave.
+    FwhtExecutor(const Request& r, FwhtKind kind, Launch launch, PitchedLaunch pitched, PitchedLaunch rows_kernel,
+                 unsigned resident)
+        : r_(r), kind_(kind), launch_(launch), pitched_(pitched), rows_kernel_(rows_kernel) {
         norm_ = r.normalize ? 1.0f / static_cast<float>(r.n) : 1.0f;
         scale_ = r.fp16_final ? r.output_scale : 1.0f;
-        const int lb = wide_ ? static_cast<int>(r.log_n) : r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
         const std::uint64_t total = r.n * r.batch;
-        const std::uint64_t rows_per_tile = std::uint64_t{1} << (lb - int(r.log_n));
-        const std::uint64_t tiles =
-            pitched_ || wide_ ? (r.batch + rows_per_tile - 1) / rows_per_tile : (total + (1ull << lb) - 1) >> lb;
+        std::uint64_t tiles = 0, tile_elements = 0, lds = 0;
+        unsigned threads = 0, regs = 0, phases = 0;
+        if (kind == FwhtKind::Lanes) {
+            const std::uint64_t rows_per_wave = std::uint64_t{1} << (kLaneTileLog - int(r.log_n));
+            tiles = (r.batch + rows_per_wave - 1) / rows_per_wave;  // one per wave
+            tile_elements = std::uint64_t{1} << kLaneTileLog;
+            threads = 64u * kLaneWaves;
+            regs = kLaneRegs;
+            phases = 1;
+            grid_ = static_cast<unsigned>(std::min<std::uint64_t>((tiles + kLaneWaves - 1) / kLaneWaves,
+                                                                  0x7fffffffull));
+            reason = "64 elements per lane (" + std::to_string(threads) +
+                     " threads, each wave on its own 4096 elements): bits 0-3 in registers, bit 4 through "
+                     "v_permlane16_swap" +
+                     std::string(r.log_n >= 6 ? ", bit 5 through v_permlane32_swap" : "") +
+                     std::string(r.log_n >= 7 ? ", bits 6+ in registers" : "") + ", no LDS";
+        } else {
+            const bool wide = kind != FwhtKind::Resident;
+            const int lb = wide ? static_cast<int>(r.log_n) : r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
+            const std::uint64_t rows_per_tile = std::uint64_t{1} << (lb - int(r.log_n));
+            tiles = pitched_ || wide ? (r.batch + rows_per_tile - 1) / rows_per_tile
+                                     : (total + (1ull << lb) - 1) >> lb;
+            tile_elements = std::uint64_t{1} << lb;
+            const int regs_log = wide ? kLW : kLE;
+            threads = 1u << (lb - regs_log);
+            regs = 1u << regs_log;
+            phases = wide ? 3u : unsigned((r.log_n + kLE - 1) / kLE);
+            lds = ((1u << lb) + ((1u << lb) >> regs_log)) * 4ull;
+            // Grid: one workgroup per tile (measured at least as fast as a
+            // persistent, occupancy-sized grid for every BASELINE shape once
+            // the kernel's prefetch overlapped), capped at the launch limit;
+            // the kernel walks any tiles beyond the grid with next-tile
+            // prefetch.
+            grid_ = static_cast<unsigned>(std::min<std::uint64_t>(tiles, 0x7fffffffull));
+            if (kind == FwhtKind::WidePersistent) grid_ = std::min(grid_, resident);
+            reason = wide ? "one row per workgroup (" + std::to_string(threads) +
+                                " threads x 32 registers, phases of bits 0-4, 5-9 and 10+, the last carrying the low "
+                                "element bits so results leave as 8- to 64-byte vectors)"
+                          : "whole rows resident in one workgroup (" + std::to_string(threads) +
+                                " threads x 16 registers, padded LDS exchange)";
+            reason += std::string(grid_ < tiles ? ", persistent grid with next-tile prefetch" : "");
+        }
         require(tiles <= 0xffffffffull, "FWHT batch exceeds the tile index range");
-        // Grid: one workgroup per tile (measured at least as fast as a
-        // persistent, occupancy-sized grid for every BASELINE shape once the
-        // kernel's prefetch overlapped), capped at the launch limit; the
-        // kernel walks any tiles beyond the grid with next-tile prefetch.
-        const int regs_log = wide_ ? kLW : kLE;
-        const unsigned threads = 1u << (lb - regs_log);
-        const std::uint64_t lds = ((1u << lb) + ((1u << lb) >> regs_log)) * 4ull;
-        grid_ = static_cast<unsigned>(std::min<std::uint64_t>(tiles, 0x7fffffffull));
-        if (wide_ && persistent) grid_ = std::min(grid_, wide.resident());
-        algorithm = name(r, wide_ != nullptr, wide_ && persistent);
-        reason = wide_ ? "one row per workgroup (" + std::to_string(threads) +
-                             " threads x 32 registers, phases of bits 0-4, 5-9 and 10+, the last carrying the low "
-                             "element bits so results leave as 8- to 64-byte vectors)"
-                       : "whole rows resident in one workgroup (" + std::to_string(threads) +
-                             " threads x 16 registers, padded LDS exchange)";
-        reason += std::string(grid_ < tiles ? ", persistent grid with next-tile prefetch" : "") +
-                  "; stage order bits 0..log n-1";
+        reason += "; stage order bits 0..log n-1";
+        algorithm = name(r, kind);
         json::Writer w;
         w.begin_object()
             .field("schema_version", 1u)
@@ -782,26 +977,29 @@ class FwhtExecutor final : public Executor {
             .field("algorithm", algorithm)
             .field("log_n", r.log_n)
             .field("batch", r.batch)
-            .field("tile_elements", std::uint64_t{1} << lb)
+            .field("tile_elements", tile_elements)
             .field("tiles", tiles)
             .field("grid", grid_)
             .field("threads_per_block", threads)
-            .field("registers_per_thread", 1u << regs_log)
-            .field("phases", wide_ ? 3u : unsigned((r.log_n + kLE - 1) / kLE))
+            .field("registers_per_thread", regs)
+            .field("phases", phases)
             .field("lds_bytes", lds)
-            .field("input_pitch", pitched_ ? r.in_batch_stride : r.n)
-            .field("output_pitch", pitched_ ? r.out_batch_stride : r.n)
+            .field("input_pitch", r.pitched ? r.in_batch_stride : r.n)
+            .field("output_pitch", r.pitched ? r.out_batch_stride : r.n)
             .end_object();
         mapping_json = w.str();
     }
-    static std::string name(const Request& r, bool wide, bool persistent = false) {
-        return std::string(r.fp16_final ? "fwht-fp16-fp32-resident-r" : "fwht-fp32-resident-r") +
-               (wide ? "32" : "16") + (persistent ? "-persistent" : "") + (r.pitched ? "-pitched" : "");
+    static std::string name(const Request& r, FwhtKind kind) {
+        const char* family = kind == FwhtKind::Lanes      ? "lanes-r64"
+                             : kind == FwhtKind::Resident ? "resident-r16"
+                             : kind == FwhtKind::Wide     ? "resident-r32"
+                                                          : "resident-r32-persistent";
+        return std::string(r.fp16_final ? "fwht-fp16-fp32-" : "fwht-fp32-") + family + (r.pitched ? "-pitched" : "");
     }
     void execute(const void* in, void* out, void*, hipStream_t stream) override {
-        if (wide_)
-            wide_(in, out, r_.batch, pitched_ ? r_.in_batch_stride : r_.n, pitched_ ? r_.out_batch_stride : r_.n,
-                  norm_, scale_, grid_, stream);
+        if (rows_kernel_)
+            rows_kernel_(in, out, r_.batch, r_.pitched ? r_.in_batch_stride : r_.n,
+                         r_.pitched ? r_.out_batch_stride : r_.n, norm_, scale_, grid_, stream);
         else if (pitched_)
             pitched_(in, out, r_.batch, r_.in_batch_stride, r_.out_batch_stride, norm_, scale_, grid_, stream);
         else
@@ -811,12 +1009,28 @@ class FwhtExecutor final : public Executor {
 
   private:
     Request r_;
+    FwhtKind kind_;
     Launch launch_;
     PitchedLaunch pitched_;
-    PitchedLaunch wide_;
+    PitchedLaunch rows_kernel_;  // the 32-register or the lane kernel (packed or pitched rows)
     float norm_ = 1.0f, scale_ = 1.0f;
     unsigned grid_ = 1;
 };
+
+// The lowerings of a request, default first. Default: the 32-register kernel
+// for FP16 rows of 2^12 points (55.7-56.6 us against 56.4-58.5 us for 16384
+// rows); the 16-register kernel elsewhere. The others are MEASURE candidates
+// and explicit choices.
+std::vector<FwhtKind> fwht_kinds(const Request& r) {
+    std::vector<FwhtKind> kinds = {FwhtKind::Resident};
+    if (wide_launcher(r)) {
+        kinds.push_back(FwhtKind::Wide);
+        kinds.push_back(FwhtKind::WidePersistent);
+        if (r.log_n == 12) std::swap(kinds[0], kinds[1]);
+    }
+    if (lane_launcher(r)) kinds.push_back(FwhtKind::Lanes);
+    return kinds;
+}
 
 }  // namespace
 
@@ -839,20 +1053,31 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
         pitched = r.fp16_final ? pitched_launcher<F16Io>(r.log_n) : pitched_launcher<F32Io>(r.log_n);
         require(pitched != nullptr, "pitched FWHT rows need n >= 16");
     }
+    const std::vector<FwhtKind> kinds = fwht_kinds(r);
+    FwhtKind kind = kinds.front();
+    if (!r.variant.empty()) {
+        std::string available;
+        bool found = false;
+        for (FwhtKind k : kinds) {
+            available += (available.empty() ? "" : ", ") + FwhtExecutor::name(r, k);
+            if (FwhtExecutor::name(r, k) == r.variant) {
+                kind = k;
+                found = true;
+            }
+        }
+        supported(found, "'" + r.variant + "' is not a lowering of this FWHT (available: " + available + ")");
+    }
     const WideLaunch wide = wide_launcher(r);
-    // Default: the 32-register kernel where it measured faster (FP16 rows of
-    // 2^12 points: 55.7-56.6 us against 56.4-58.5 us for 16384 rows); other
-    // lengths keep the 16-register kernel unless MEASURE picks it.
-    const bool wide_default = wide && r.log_n == 12;
-    const bool one_per_row =
-        wide && (r.variant.empty() ? wide_default : r.variant == FwhtExecutor::name(r, true));
-    const bool persistent = wide && r.variant == FwhtExecutor::name(r, true, true);
-    std::string available = FwhtExecutor::name(r, false);
-    if (wide) available += ", " + FwhtExecutor::name(r, true) + ", " + FwhtExecutor::name(r, true, true);
-    supported(r.variant.empty() || one_per_row || persistent || r.variant == FwhtExecutor::name(r, false),
-              "'" + r.variant + "' is not a lowering of this FWHT (available: " + available + ")");
-    auto e = std::make_unique<FwhtExecutor>(r, launch, pitched, one_per_row || persistent ? wide : WideLaunch{},
-                                            persistent);
+    PitchedLaunch rows_kernel = nullptr;
+    unsigned resident = 0;
+    if (kind == FwhtKind::Wide) rows_kernel = wide.launch;
+    if (kind == FwhtKind::WidePersistent) {
+        rows_kernel = wide.walk;
+        resident = wide.resident();
+    }
+    if (kind == FwhtKind::Lanes) rows_kernel = lane_launcher(r);
+    auto e = std::make_unique<FwhtExecutor>(r, kind, launch, kind == FwhtKind::Resident ? pitched : nullptr,
+                                            rows_kernel, resident);
     if (r.allow_mma && !mfma)
         e->reason += "; ALLOW_FP16_MMA requested, but the MFMA Hadamard-block kernel covers packed rows of 2 to 4096 "
                      "points only: stage-ordered VALU kernel used";
@@ -863,12 +1088,8 @@ std::vector<std::string> fwht_candidates(const Request& r) {
     Request v = r;
     v.variant.clear();
     make_fwht_executor(v);  // the default lowering exists (throws NotSupported otherwise)
-    std::vector<std::string> names = {FwhtExecutor::name(r, false)};
-    if (wide_launcher(r)) {
-        names.push_back(FwhtExecutor::name(r, true));
-        names.push_back(FwhtExecutor::name(r, true, true));
-        if (r.log_n == 12) std::swap(names[0], names[1]);  // the default first
-    }
+    std::vector<std::string> names;
+    for (FwhtKind k : fwht_kinds(r)) names.push_back(FwhtExecutor::name(r, k));
     if (r.allow_mma && fwht_mfma_covers(r)) names.insert(names.begin(), fwht_mfma_name());
     return names;
 }

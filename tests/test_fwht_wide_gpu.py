@@ -105,7 +105,8 @@ def test_measure_lists_both_lowerings(torch_gpu, lib, stream, tmp_path):
         reason = plan.selection_reason()
         name = plan.algorithm_name()
     assert "fwht-fp16-fp32-resident-r16=" in reason and "fwht-fp16-fp32-resident-r32=" in reason, reason
-    assert name in ("fwht-fp16-fp32-resident-r16", "fwht-fp16-fp32-resident-r32")
+    assert name in ("fwht-fp16-fp32-resident-r16", "fwht-fp16-fp32-resident-r32",
+                    "fwht-fp16-fp32-resident-r32-persistent")
 
 
 @pytest.mark.parametrize("log_n,fp16", [(10, True), (14, True), (12, False)])
