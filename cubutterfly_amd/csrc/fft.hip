@@ -27,6 +27,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 
 // Complex products may fuse into FMAs here: FFT accuracy is specified as a
 // relative L2 bound, and fused products are the more accurate ones.
@@ -395,8 +396,10 @@ struct FftPass {
         else buffer_store<float2, kStoreAux>(x, dst, lane_bytes, reg_bytes);
     }
 
-    // `valid` false: an empty buffer range, so every load returns zero
-    // without touching memory (keeps a prefetch unconditional, see step()).
+    // Registers [R0, R1) of a tile. `valid` false: an empty buffer range, so
+    // every load returns zero without touching memory (keeps a prefetch
+    // unconditional, see step()).
+    template <int R0 = 0, int R1 = kE>
     static __device__ __forceinline__ void load(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
                                                 float2 (&v)[kE], bool valid = true) {
         constexpr int w0 = tile_window<0>();
@@ -404,7 +407,7 @@ struct FftPass {
             make_rsrc(a.in + span_base(a, tl, a.in_pitch), valid ? span_bytes(a, tl, m) : 0u);
         const std::uint32_t tb = natural_offset(a, tl, index<w0>(t, 0)) * 8u;
 #pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = load_at(src, tb, natural_offset(a, Tile{}, index<w0>(0, r)) * 8u);
+        for (int r = R0; r < R1; ++r) v[r] = load_at(src, tb, natural_offset(a, Tile{}, index<w0>(0, r)) * 8u);
     }
 
     static __device__ __forceinline__ void bases_of(float2 (&bs)[3], const FftArgs& a, std::uint32_t t,
@@ -415,22 +418,31 @@ struct FftPass {
     }
     static_assert(kPhases <= 4, "at most four digits per pass");
 
+    // `after(P)` runs after digit P (an std::integral_constant), before the
+    // next exchange or the store: the persistent walk issues a slice of the
+    // next tile's loads there.
+    template <class After>
     static __device__ __forceinline__ void process(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
-                                                   float2 (&v)[kE], const float2 (&bs)[3], float2* lds) {
+                                                   float2 (&v)[kE], const float2 (&bs)[3], float2* lds,
+                                                   After&& after) {
         digit<0>(v, bs[0]);
+        after(std::integral_constant<int, 0>{});
         if constexpr (kPhases > 1) {
             exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
             digit<1>(v, bs[1]);
+            after(std::integral_constant<int, 1>{});
         }
         if constexpr (kPhases > 2) {
             exchange<tile_window<1>(), tile_window<2>()>(v, lds, t);
             digit<2>(v, bs[2]);
+            after(std::integral_constant<int, 2>{});
         }
         if constexpr (kPhases > 3) {
             // A fourth digit (4-bit digits over 13 or 14 bits) fetches its
             // base here, keeping the bases held across the tile to three.
             exchange<tile_window<2>(), tile_window<3>()>(v, lds, t);
             digit<3>(v, level_base<3>(a, t, tl.c0, m));
+            after(std::integral_constant<int, 3>{});
         }
         constexpr int wl = tile_window<kPhases - 1>();
         const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.out + span_base(a, tl, a.out_pitch), span_bytes(a, tl, m));
@@ -516,7 +528,7 @@ struct FftPass {
         load(a, tl, t, m, v);
         if constexpr (!kPrefetch) {  // one tile per workgroup (the grid covers every tile)
             if constexpr (COL) bases_of(bs, a, t, tl.c0, m);
-            process(a, tl, t, m, v, bs, lds);
+            process(a, tl, t, m, v, bs, lds, [](auto) {});
             return;
         }
         // Two register buffers in turn (unrolled by two), so no tile is
@@ -528,6 +540,9 @@ struct FftPass {
             if (!step(a, t, m, pos, stride, range_base, range_end, tl, bs, w, v, lds)) break;
         }
     }
+
+    // End of prefetch slice S: registers [slice_end(S - 1), slice_end(S)).
+    static constexpr int slice_end(int s) { return (s + 1) * kE / kPhases; }
 
     // One tile of the persistent walk: prefetch the next tile into `next`,
     // process the current one from `cur`. Returns whether a next tile exists.
@@ -548,13 +563,22 @@ struct FftPass {
         // `cur` merging a path without the prefetch, and it would then wait
         // for the prefetch too.
         const Tile tn = decode(a, range_base + following, m);
-        load(a, tn, tt, m, next, more);
-        // No instruction moves across this point, so every use of `cur` comes
-        // after the prefetch is issued: the wait for `cur` then counts the
-        // prefetch as younger and does not wait for it (or for the previous
-        // tile's stores).
+        // The prefetch goes out in kPhases slices: the first before digit 0,
+        // each further one after a digit, so a tile's loads do not all queue
+        // in the address unit at once. No instruction moves across the slice
+        // boundaries, so every use of `cur` comes after the first slice is
+        // issued: the wait for `cur` then counts the prefetch as younger and
+        // does not wait for it (or for the previous tile's stores).
+        load<0, slice_end(0)>(a, tn, tt, m, next, more);
         __builtin_amdgcn_sched_barrier(0);
-        process(a, tl, tt, m, cur, bs, lds);
+        process(a, tl, tt, m, cur, bs, lds, [&](auto digit_done) {
+            constexpr int S = decltype(digit_done)::value + 1;
+            if constexpr (S < kPhases) {
+                __builtin_amdgcn_sched_barrier(0);
+                load<slice_end(S - 1), slice_end(S)>(a, tn, tt, m, next, more);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        });
         // Keep `cur`'s registers allocated through the stores: otherwise the
         // stores take their data from them, and the next prefetch into them
         // would first wait for those stores.
