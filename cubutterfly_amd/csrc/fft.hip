@@ -308,11 +308,14 @@ struct FftPass {
         if constexpr (R + 1 < kE) apply_powers<R + 1, DS>(v, p1, p2, p3, p4, p8, p16);
     }
 
-    template <int FROM, int TO>
-    static __device__ __forceinline__ void exchange(float2 (&v)[kE], float2* lds, std::uint32_t t) {
+    // `between` runs after this wave's LDS writes, before the barrier.
+    template <int FROM, int TO, class Between>
+    static __device__ __forceinline__ void exchange(float2 (&v)[kE], float2* lds, std::uint32_t t,
+                                                    Between&& between) {
         lds_barrier();
 #pragma unroll
         for (int r = 0; r < kE; ++r) lds[L::split(index<FROM>(t, 0), index<FROM>(0, r))] = v[r];
+        between();
         lds_barrier();
 #pragma unroll
         for (int r = 0; r < kE; ++r) v[r] = lds[L::split(index<TO>(t, 0), index<TO>(0, r))];
@@ -418,35 +421,39 @@ struct FftPass {
     }
     static_assert(kPhases <= 4, "at most four digits per pass");
 
-    // `after(P)` runs after digit P (an std::integral_constant), before the
-    // next exchange or the store: the persistent walk issues a slice of the
-    // next tile's loads there.
-    template <class After>
+    // `at(K)` (K an std::integral_constant) runs at hook point K: 2P right
+    // after digit P, 2P + 1 between this wave's LDS writes and the barrier of
+    // the exchange that follows digit P (for the last digit, the final
+    // store's; a column pass has none and runs it before its stores). Every
+    // point 0 .. 2 kPhases - 1 runs once per tile. The persistent walk issues
+    // slices of the next tile's loads there.
+    template <class At>
     static __device__ __forceinline__ void process(const FftArgs& a, const Tile& tl, std::uint32_t t, std::uint32_t m,
-                                                   float2 (&v)[kE], const float2 (&bs)[3], float2* lds,
-                                                   After&& after) {
+                                                   float2 (&v)[kE], const float2 (&bs)[3], float2* lds, At&& at) {
+        using std::integral_constant;
         digit<0>(v, bs[0]);
-        after(std::integral_constant<int, 0>{});
+        at(integral_constant<int, 0>{});
         if constexpr (kPhases > 1) {
-            exchange<tile_window<0>(), tile_window<1>()>(v, lds, t);
+            exchange<tile_window<0>(), tile_window<1>()>(v, lds, t, [&] { at(integral_constant<int, 1>{}); });
             digit<1>(v, bs[1]);
-            after(std::integral_constant<int, 1>{});
+            at(integral_constant<int, 2>{});
         }
         if constexpr (kPhases > 2) {
-            exchange<tile_window<1>(), tile_window<2>()>(v, lds, t);
+            exchange<tile_window<1>(), tile_window<2>()>(v, lds, t, [&] { at(integral_constant<int, 3>{}); });
             digit<2>(v, bs[2]);
-            after(std::integral_constant<int, 2>{});
+            at(integral_constant<int, 4>{});
         }
         if constexpr (kPhases > 3) {
             // A fourth digit (4-bit digits over 13 or 14 bits) fetches its
             // base here, keeping the bases held across the tile to three.
-            exchange<tile_window<2>(), tile_window<3>()>(v, lds, t);
+            exchange<tile_window<2>(), tile_window<3>()>(v, lds, t, [&] { at(integral_constant<int, 5>{}); });
             digit<3>(v, level_base<3>(a, t, tl.c0, m));
-            after(std::integral_constant<int, 3>{});
+            at(integral_constant<int, 6>{});
         }
         constexpr int wl = tile_window<kPhases - 1>();
         const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.out + span_base(a, tl, a.out_pitch), span_bytes(a, tl, m));
         if constexpr (COL) {  // intermediate: same positions
+            at(integral_constant<int, 2 * kPhases - 1>{});
             const std::uint32_t tb = natural_offset(a, tl, index<wl>(t, 0)) * 8u;
 #pragma unroll
             for (int r = 0; r < kE; ++r) store_at(v[r], dst, tb, natural_offset(a, Tile{}, index<wl>(0, r)) * 8u);
@@ -456,6 +463,7 @@ struct FftPass {
         lds_barrier();
 #pragma unroll
         for (int r = 0; r < kE; ++r) lds[L::split(index<wl>(t, 0), index<wl>(0, r))] = v[r];
+        at(integral_constant<int, 2 * kPhases - 1>{});
         lds_barrier();
         std::uint32_t it, ot;
         staged(a, tl, t, it, ot);
@@ -541,9 +549,20 @@ struct FftPass {
         }
     }
 
-    // End of prefetch slice S: registers [slice_end(S - 1), slice_end(S)) of
-    // kPhases + 1 slices.
-    static constexpr int slice_end(int s) { return (s + 1) * kE / (kPhases + 1); }
+    // Hook points of process() that issue a prefetch slice: inside each
+    // exchange, after this wave's LDS writes (measured against right after
+    // each digit: C3a 150.3-150.6 -> 147.2-148.5 us, C3b 65.0-65.6 ->
+    // 64.1-64.3 us; both sets: 148.2-148.6 / 64.2-64.5 us). Slice 0 goes out
+    // before digit 0; slice S covers registers [slice_end(S - 1), slice_end(S)).
+    static constexpr unsigned kSliceMask = kPhases == 2 ? 0b1010u : kPhases == 3 ? 0b101010u : 0b10101010u;
+    static constexpr bool slice_at(int k) { return (kSliceMask >> k) & 1u; }
+    static constexpr int slice_before(int k) {  // slices issued at hook points below k
+        int c = 0;
+        for (int j = 0; j < k; ++j) c += slice_at(j) ? 1 : 0;
+        return c;
+    }
+    static constexpr int kSlices = 1 + slice_before(2 * kPhases);
+    static constexpr int slice_end(int s) { return (s + 1) * kE / kSlices; }
 
     // One tile of the persistent walk: prefetch the next tile into `next`,
     // process the current one from `cur`. Returns whether a next tile exists.
@@ -565,17 +584,18 @@ struct FftPass {
         // for the prefetch too.
         const Tile tn = decode(a, range_base + following, m);
         // The prefetch goes out in kPhases + 1 slices: the first before digit
-        // 0, one after each digit (the last before the final store), so a
-        // tile's loads do not all queue in the address unit at once (C3b
-        // 70.4 -> 62.6-64.9 us, C3a 156.5 -> 150 us). No instruction moves across the slice
+        // 0, one inside each exchange (the last in the final store's), so a
+        // tile's loads do not all queue in the address unit at once (all
+        // before digit 0: C3b 70.4 us, C3a 156.5 us; sliced: 64.1 / 147.2 us). No instruction moves across the slice
         // boundaries, so every use of `cur` comes after the first slice is
         // issued: the wait for `cur` then counts the prefetch as younger and
         // does not wait for it (or for the previous tile's stores).
         load<0, slice_end(0)>(a, tn, tt, m, next, more);
         __builtin_amdgcn_sched_barrier(0);
-        process(a, tl, tt, m, cur, bs, lds, [&](auto digit_done) {
-            constexpr int S = decltype(digit_done)::value + 1;
-            if constexpr (S < kPhases + 1) {
+        process(a, tl, tt, m, cur, bs, lds, [&](auto point) {
+            constexpr int K = decltype(point)::value;
+            if constexpr (slice_at(K)) {
+                constexpr int S = slice_before(K) + 1;
                 __builtin_amdgcn_sched_barrier(0);
                 load<slice_end(S - 1), slice_end(S)>(a, tn, tt, m, next, more);
                 __builtin_amdgcn_sched_barrier(0);
