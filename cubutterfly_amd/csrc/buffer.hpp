@@ -33,14 +33,18 @@ __device__ __forceinline__ T buffer_load(__amdgpu_buffer_rsrc_t r, std::uint32_t
     }
 }
 
-// AUX: the instruction's cache-policy bits.
+// AUX: the instruction's cache-policy bits. T is a 4-, 8- or 16-byte type.
 template <class T, int AUX = 0>
 __device__ __forceinline__ void buffer_store(T x, __amdgpu_buffer_rsrc_t r, std::uint32_t byte_off,
                                              std::uint32_t scalar_off = 0) {
-    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- or 8-byte elements");
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 16, "4-, 8- or 16-byte elements");
     if constexpr (sizeof(T) == 4) {
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(std::uint32_t, x), r, static_cast<int>(byte_off),
                                               static_cast<int>(scalar_off), AUX);
+    } else if constexpr (sizeof(T) == 16) {
+        using V4 = __attribute__((ext_vector_type(4))) std::uint32_t;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(V4, x), r, static_cast<int>(byte_off),
+                                               static_cast<int>(scalar_off), AUX);
     } else {
         using V2 = __attribute__((ext_vector_type(2))) std::uint32_t;
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(V2, x), r, static_cast<int>(byte_off),

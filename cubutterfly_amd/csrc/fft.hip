@@ -398,6 +398,13 @@ struct FftPass {
         if (kLaneOnly || reg_bytes < 4096u) buffer_store<float2, kStoreAux>(x, dst, lane_bytes + reg_bytes);
         else buffer_store<float2, kStoreAux>(x, dst, lane_bytes, reg_bytes);
     }
+    // Two consecutive outputs as one 16-byte store.
+    static __device__ __forceinline__ void store2_at(float2 x0, float2 x1, __amdgpu_buffer_rsrc_t dst,
+                                                     std::uint32_t lane_bytes, std::uint32_t reg_bytes) {
+        const float4 x = make_float4(x0.x, x0.y, x1.x, x1.y);
+        if (kLaneOnly || reg_bytes < 4096u) buffer_store<float4, kStoreAux>(x, dst, lane_bytes + reg_bytes);
+        else buffer_store<float4, kStoreAux>(x, dst, lane_bytes, reg_bytes);
+    }
 
     // Registers [R0, R1) of a tile. `valid` false: an empty buffer range, so
     // every load returns zero without touching memory (keeps a prefetch
@@ -465,6 +472,10 @@ struct FftPass {
         for (int r = 0; r < kE; ++r) lds[L::split(index<wl>(t, 0), index<wl>(0, r))] = v[r];
         at(integral_constant<int, 2 * kPhases - 1>{});
         lds_barrier();
+        if constexpr (kPairedStore) {
+            store_pairs(a, t, lds, dst);
+            return;
+        }
         std::uint32_t it, ot;
         staged(a, tl, t, it, ot);
         // Unnormalised plans (scale 1) skip the products: a wave-uniform
@@ -483,6 +494,41 @@ struct FftPass {
                 staged(a, Tile{}, T * std::uint32_t(r), ir, orr);
                 const float2 x = lds[L::split(it, ir)];
                 store_at(make_float2(x.x * a.scale, x.y * a.scale), dst, ot * 8u, orr * 8u);
+            }
+        }
+    }
+
+    // One-row tiles store pairs of neighbouring outputs, one 16-byte store per
+    // lane: pair j = t + T r (r < kE / 2) holds outputs 2j and 2j + 1, read
+    // from LDS at their tile indices (bit-reversed, or as they are for a
+    // bit-reversed output order). The index of 2j splits into a thread part
+    // (2t) and a register part (2 T r) over disjoint bits, and output 2j + 1
+    // differs from it in one bit that is clear in both parts: the top one
+    // after bit reversal, bit 0 otherwise.
+    static constexpr bool kPairedStore = SINGLE && LI == 0;
+    static __device__ __forceinline__ std::uint32_t pair_index(std::uint32_t g) {
+        return (ORD & 2) != 0 ? g : brev(g, LT);
+    }
+    static __device__ __forceinline__ void store_pairs(const FftArgs& a, std::uint32_t t, const float2* lds,
+                                                       __amdgpu_buffer_rsrc_t dst) {
+        constexpr std::uint32_t kSecond = (ORD & 2) != 0 ? 1u : 1u << (LT - 1);
+        const std::uint32_t it = pair_index(2u * t), ot = 2u * t;
+        // Unnormalised plans (scale 1) skip the products: a wave-uniform
+        // branch over two copies of the store loop.
+        if (a.scale == 1.0f) {
+#pragma unroll
+            for (int r = 0; r < kE / 2; ++r) {
+                const std::uint32_t ir = pair_index(2u * T * std::uint32_t(r));
+                const float2 x0 = lds[L::split(it, ir)], x1 = lds[L::split(it, ir | kSecond)];
+                store2_at(x0, x1, dst, ot * 8u, 2u * T * std::uint32_t(r) * 8u);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < kE / 2; ++r) {
+                const std::uint32_t ir = pair_index(2u * T * std::uint32_t(r));
+                const float2 x0 = lds[L::split(it, ir)], x1 = lds[L::split(it, ir | kSecond)];
+                store2_at(make_float2(x0.x * a.scale, x0.y * a.scale), make_float2(x1.x * a.scale, x1.y * a.scale),
+                          dst, ot * 8u, 2u * T * std::uint32_t(r) * 8u);
             }
         }
     }

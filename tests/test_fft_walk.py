@@ -129,3 +129,31 @@ def test_model_catches_a_missing_barrier():
         + intervals[first_tile_last_reads + 2:]
     with pytest.raises(AssertionError):
         check(merged)
+
+
+@pytest.mark.parametrize("lt,db", [(14, 5), (13, 5), (12, 4)])
+@pytest.mark.parametrize("bitrev_out", [False, True])
+def test_paired_store_addresses(lt, db, bitrev_out):
+    # FftPass::store_pairs: pair j = t + T r holds outputs 2j, 2j + 1; their
+    # LDS words come from a thread part (index of 2t) and a register part
+    # (index of 2 T r), XOR-combined, the second output's by one more bit.
+    # That must equal the swizzled word of each output's own tile index, and
+    # the pairs must cover every output once.
+    threads = 1 << (lt - db)
+    regs = 1 << db
+
+    def index(g):
+        return g if bitrev_out else brev(g, lt)
+
+    second = 1 if bitrev_out else 1 << (lt - 1)
+    seen = set()
+    for t in range(threads):
+        it = index(2 * t)
+        for r in range(regs // 2):
+            ir = index(2 * threads * r)
+            assert it & ir == 0 and (it | ir) & second == 0
+            j = t + threads * r
+            assert swizzled(it, lt, db) ^ swizzled(ir, lt, db) == swizzled(index(2 * j), lt, db)
+            assert swizzled(it, lt, db) ^ swizzled(ir | second, lt, db) == swizzled(index(2 * j + 1), lt, db)
+            seen.update((2 * j, 2 * j + 1))
+    assert seen == set(range(1 << lt))
