@@ -11,6 +11,7 @@ import pytest
 import cubutterfly_amd as cb
 import oracle
 from cubutterfly_amd import workloads
+from golden import make_full_size_hashes as golden
 from gpu_util import run_plan
 
 pytestmark = pytest.mark.gpu
@@ -36,6 +37,7 @@ def test_c1_full_size_bit_exact(torch_gpu, lib, stream):
     x = workloads.fwht_integer_input(12, 4096, seed=1)
     got = run_plan(torch_gpu, lib, fwht32(4096, 4096), x, stream)
     np.testing.assert_array_equal(got, oracle.fwht_f32(x, threads=THREADS))
+    assert golden.sha256(got) == golden.load()["c1"]["output_sha256"]
 
 
 @pytest.mark.parametrize("log_n", list(range(1, 14)))
@@ -72,6 +74,7 @@ def test_c5_quarot_full_size(torch_gpu, lib, stream, rows, n):
     x = workloads.quarot_input(rows, n, seed=5)
     got = run_plan(torch_gpu, lib, fwht16(n, rows, scale), x, stream)
     check_fp16(got, oracle.fwht_f16_final(x, scale, threads=THREADS))
+    assert golden.sha256(got) == golden.load()["c5a" if n == 4096 else "c5b"]["output_sha256"]
 
 
 @pytest.mark.parametrize("log_n", [1, 3, 5, 6, 8, 11, 13])

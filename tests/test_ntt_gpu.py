@@ -12,6 +12,7 @@ import pytest
 import cubutterfly_amd as cb
 import oracle
 from cubutterfly_amd import workloads
+from golden import make_full_size_hashes as golden
 from gpu_util import run_plan
 
 pytestmark = pytest.mark.gpu
@@ -48,6 +49,7 @@ def test_c2_negacyclic_full_size(torch_gpu, lib, stream):
     fwd = run_plan(torch_gpu, lib, ntt(1 << 16, 64, Q30, 32, ring=neg), x, stream)
     expected = oracle.ntt_negacyclic(x.astype(np.uint64), Q30, threads=THREADS)
     np.testing.assert_array_equal(fwd.astype(np.uint64), expected)
+    assert golden.sha256(fwd) == golden.load()["c2"]["output_sha256"]
     back = run_plan(torch_gpu, lib, ntt(1 << 16, 64, Q30, 32, inverse=True, ring=neg), fwd, stream)
     np.testing.assert_array_equal(back, x)
     inv_ref = oracle.ntt_negacyclic(x.astype(np.uint64), Q30, inverse=True, threads=THREADS)

@@ -16,6 +16,7 @@ import pytest
 import cubutterfly_amd as cb
 import oracle
 from cubutterfly_amd import rns, workloads
+from golden import make_full_size_hashes as golden
 from gpu_util import to_device, to_host
 
 pytestmark = pytest.mark.gpu
@@ -60,6 +61,7 @@ def test_c4_full_size_round_trip(torch_gpu, rlib):
     got, info = run(torch_gpu, rlib, fwd_cfg, x.ravel(), x.size, False, stream)
     expected = oracle.rns(x, moduli, roots, output_bit_reversed=True, threads=oracle.default_threads())
     np.testing.assert_array_equal(got.reshape(32, n), expected)
+    assert golden.sha256(got.reshape(32, n)) == golden.load()["c4"]["output_sha256"]
     assert info["prepared"] and info["placement"] == "separate"
     inv_cfg = rns.request(log_n, list(zip(moduli, roots)), inverse=True)
     back, _ = run(torch_gpu, rlib, inv_cfg, got, x.size, True, stream)
