@@ -131,16 +131,19 @@ constexpr int digit_bits_for(int lb, bool single);
 // LDS image of a tile (8-byte complex words).
 //
 // One-pass tiles of one whole row of 2^12 .. 2^14 points are unpadded, with
-// the low four word bits XORed with index bits [DB, DB + 4) and [LT - 4, LT)
-// (DB the digit width). A 16-lane group of a 64-bit LDS access covers all
-// banks when its 16 words differ in those four low bits, and every access of
-// these tiles varies across a group in exactly one of the three fields: the
-// lowest four index bits (phase exchanges with the register window above
-// them), the digit's lowest four bits (the exchange into the last digit), or
-// the top four bits (the bit-reversed read of the final store). The other
-// two fields are constant across the group, so the XOR is a bijection on it.
-// A plain 1-in-16 pad left the bit-reversed read with every lane of a group
-// on one bank.
+// the low four word bits XORed with index bits [DB, DB + 4) and
+// [LT - 5, LT - 1) (DB the digit width). A 16-lane group of a 64-bit LDS
+// access covers all banks when its 16 words differ in those four low bits,
+// and every access of these tiles varies across a group in one of the three
+// fields: the lowest four index bits (phase exchanges with the register
+// window above them), the digit's lowest four bits (the exchange into the
+// last digit), or bits LT - 5 .. LT - 2 (the bit-reversed reads of the paired
+// final store: outputs 2j and 2j + 1, j varying in its low four bits). The
+// XOR of the varying field with the others, constant or overlapping in one
+// bit, stays a bijection on it (checked by enumeration for 2^12, 2^13 and
+// 2^14 points). Keyed on the top four bits instead, the paired reads of
+// 2^14-point tiles fell on 8 bank pairs per group; a plain 1-in-16 pad left
+// the unpaired bit-reversed read on one.
 //
 // Other row tiles pad each row by 1/16 and 1 word; column tiles pad rows and
 // swizzle columns.
@@ -158,7 +161,7 @@ struct FftLds {
              : COL ? (1u << LT) * ((1u << LI) + 1u) : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
     static __device__ __forceinline__ std::uint32_t addr(std::uint32_t i) {
         if constexpr (kXor) {
-            return i ^ (((i >> DB) ^ (i >> (LT - 4))) & 15u);
+            return i ^ (((i >> DB) ^ (i >> (LT - 5))) & 15u);
         } else if constexpr (COL) {
             const std::uint32_t cc = i & ((1u << LI) - 1u), x = i >> LI;
             return x * ((1u << LI) + 1u) + (cc ^ ((x >> 3) & ((1u << LI) - 1u)));

@@ -34,7 +34,7 @@ def brev(x, bits):
 
 def swizzled(i, lt, db):
     """FftLds<...>::split for one-row tiles: the unpadded XOR-swizzled image."""
-    return i ^ (((i >> db) ^ (i >> (lt - 4))) & 15)
+    return i ^ (((i >> db) ^ (i >> (lt - 5))) & 15)
 
 
 def phase_index(s, db, t, r):
