@@ -921,7 +921,7 @@ class FwhtExecutor final : public Executor {
     // tile per wave.
     FwhtExecutor(const Request& r, FwhtKind kind, Launch launch, PitchedLaunch pitched, PitchedLaunch rows_kernel,
                  unsigned resident)
-        : r_(r), kind_(kind), launch_(launch), pitched_(pitched), rows_kernel_(rows_kernel) {
+        : r_(r), launch_(launch), pitched_(pitched), rows_kernel_(rows_kernel) {
         norm_ = r.normalize ? 1.0f / static_cast<float>(r.n) : 1.0f;
         scale_ = r.fp16_final ? r.output_scale : 1.0f;
         const std::uint64_t total = r.n * r.batch;
@@ -1009,7 +1009,6 @@ class FwhtExecutor final : public Executor {
 
   private:
     Request r_;
-    FwhtKind kind_;
     Launch launch_;
     PitchedLaunch pitched_;
     PitchedLaunch rows_kernel_;  // the 32-register or the lane kernel (packed or pitched rows)
