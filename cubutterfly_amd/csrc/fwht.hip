@@ -92,8 +92,11 @@ __device__ __forceinline__ void exchange(float (&v)[kE], float* lds, unsigned t)
 // FP32 results stored straight from the last phase (one element per lane,
 // a wave covering 256 consecutive bytes) use nontemporal stores: each output
 // is written once and not read again, and C1 measured 25.7 -> 20.9 us on
-// MI355X. The FP16 and 16-byte vector stores keep the default policy, where
-// the hint measured slower (C5b 50.2 -> 55.3 us) or no faster (C5a).
+// MI355X. So do the 32-register kernel's runs (wide_store_run). The
+// 16-register kernel's 16-byte vector stores, 32 bytes apart across the
+// lanes, keep the default policy, where the hint measured slower (C5b 50.2
+// -> 55.3 us; regrouped through LDS into 1 KiB per wave instruction, 51.7-
+// 52.2 against 51.1-53.8 us).
 
 // 16 bytes at byte offset `off` of a buffer resource.
 __device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t r, unsigned off) {
@@ -531,7 +534,9 @@ __device__ __forceinline__ void wide_unpack_first_stage(const unsigned (&w)[wide
 }
 
 // Stores `run` consecutive results (run * sizeof(T) bytes: 8, 16, 32 or 64)
-// at byte offset `off` of the tile's output buffer.
+// at byte offset `off` of the tile's output buffer, nontemporal: a wave's
+// store instruction covers 512 bytes or more of consecutive output, written
+// once (C5a 49.1-49.7 -> 47.2-47.6 us).
 template <class Io, int RUN>
 __device__ __forceinline__ void wide_store_run(__amdgpu_buffer_rsrc_t r, unsigned off, const float* x) {
     constexpr int kWords = RUN * int(sizeof(typename Io::T)) / 4;
@@ -547,12 +552,12 @@ __device__ __forceinline__ void wide_store_run(__amdgpu_buffer_rsrc_t r, unsigne
     using V4 = __attribute__((ext_vector_type(4))) unsigned;
     using V2 = __attribute__((ext_vector_type(2))) unsigned;
     if constexpr (kWords == 2) {
-        __builtin_amdgcn_raw_buffer_store_b64(V2{w[0], w[1]}, r, static_cast<int>(off), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(V2{w[0], w[1]}, r, static_cast<int>(off), 0, 2);
     } else {
 #pragma unroll
         for (int k = 0; k < kWords / 4; ++k)
             __builtin_amdgcn_raw_buffer_store_b128(V4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]}, r,
-                                                   static_cast<int>(off + 16u * k), 0, 0);
+                                                   static_cast<int>(off + 16u * k), 0, 2);
     }
 }
 
