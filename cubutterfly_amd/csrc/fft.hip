@@ -576,6 +576,7 @@ struct FftPass {
     }
     static __device__ __forceinline__ void store_pairs(const FftArgs& a, std::uint32_t t, const float2* lds,
                                                        __amdgpu_buffer_rsrc_t dst) {
+        static_assert(L::kXor, "the thread / register split of a pair's index needs the XOR-linear image");
         constexpr std::uint32_t kSecond = (ORD & 2) != 0 ? 1u : 1u << (LT - 1);
         const std::uint32_t it = pair_index(2u * t), ot = 2u * t;
         // Unnormalised plans (scale 1) skip the products: a wave-uniform
