@@ -146,8 +146,11 @@ constexpr int digit_bits_for(int lb, bool single);
 // the unpaired bit-reversed read on one.
 //
 // Other row tiles pad each row by 1/16 and 1 word; column tiles pad rows and
-// swizzle columns.
-template <bool COL, int LT, int LI, bool SINGLE>
+// swizzle columns. Column tiles whose lanes hold every other column (PAIRED:
+// FftPass::logical_thread) also rotate the column index (bit 0 to the top),
+// so a 16-lane group's columns 2c + h, c consecutive, land on 16 distinct
+// 8-byte bank pairs again instead of 8 (checked by enumeration).
+template <bool COL, int LT, int LI, bool SINGLE, bool PAIRED = false>
 struct FftLds {
     static constexpr int DB = digit_bits_for(LT + LI, SINGLE);
     static constexpr bool kXor = SINGLE && LI == 0 && LT >= DB + 8;
@@ -163,7 +166,9 @@ struct FftLds {
         if constexpr (kXor) {
             return i ^ (((i >> DB) ^ (i >> (LT - 5))) & 15u);
         } else if constexpr (COL) {
-            const std::uint32_t cc = i & ((1u << LI) - 1u), x = i >> LI;
+            std::uint32_t cc = i & ((1u << LI) - 1u);
+            const std::uint32_t x = i >> LI;
+            if constexpr (PAIRED) cc = (cc >> 1) | ((cc & 1u) << (LI - 1));
             return x * ((1u << LI) + 1u) + (cc ^ ((x >> 3) & ((1u << LI) - 1u)));
         } else {
             const std::uint32_t x = i & ((1u << LT) - 1u), rr = i >> LT;
@@ -204,7 +209,8 @@ struct FftPass {
     // Prefetching needs registers for two tiles: with 16 values per thread
     // that fits the 128-register budget for passes of at most two digits.
     static constexpr bool kPrefetch = DB == 5 || kPhases <= 2;
-    using L = FftLds<COL, LT, LI, SINGLE>;
+    static constexpr bool kPairedColumns = COL && LI == 6 && kE == 16;
+    using L = FftLds<COL, LT, LI, SINGLE, kPairedColumns>;
 
     template <int P>
     static constexpr int window() {  // transform-relative register window start
@@ -421,7 +427,6 @@ struct FftPass {
     // two column values (a 2 x 2 transpose of lane bit 5 with the column bit)
     // leaves each lane both rows of its own column. The stores run the same
     // transpose backwards on the last digit's register pairs.
-    static constexpr bool kPairedColumns = COL && LI == 6 && kE == 16;
     static __device__ __forceinline__ std::uint32_t logical_thread(std::uint32_t tid) {
         if constexpr (kPairedColumns) return (tid & ~63u) | (2u * (tid & 31u)) | ((tid >> 5) & 1u);
         else return tid;

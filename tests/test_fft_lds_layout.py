@@ -59,3 +59,33 @@ def test_top_four_bit_key_conflicted_the_paired_read():
     old = lambda i: i ^ (((i >> db) ^ (i >> (lt - 4))) & 15)
     low = {old(brev(2 * t, lt)) & 15 for t in range(16)}
     assert len(low) < 16
+
+
+def column_addr(i, li, paired):
+    """FftLds for column tiles: rows padded by one word, the column index
+    XOR-swizzled by the row's bits from 3 up, and for paired-column tiles
+    first rotated (bit 0 to the top)."""
+    cc, x = i & ((1 << li) - 1), i >> li
+    if paired:
+        cc = (cc >> 1) | ((cc & 1) << (li - 1))
+    return x * ((1 << li) + 1) + (cc ^ ((x >> 3) & ((1 << li) - 1)))
+
+
+def test_paired_column_tiles_are_conflict_free():
+    # 64-column tiles of 2^8 rows (C3a's column passes), 1024 threads whose
+    # lane l holds logical column 2 (l mod 32) + l / 32 (FftPass::
+    # logical_thread); the two digit layouts. The rotation keeps every 16-lane
+    # group on 16 distinct bank pairs, where the unrotated image put it on 8.
+    lt, li, db, threads = 8, 6, 4, 1024
+    logical = lambda tid: (tid & ~63) | (2 * (tid & 31)) | ((tid >> 5) & 1)
+    phase = lambda s, t, r: (t & ((1 << s) - 1)) | (r << s) | ((t >> s) << (s + db))
+    words = 1 << (lt + li)
+    assert sorted(column_addr(i, li, True) for i in range(words)) == sorted(column_addr(i, li, False) for i in range(words))
+    for paired, distinct in [(True, 16), (False, 8)]:
+        worst = 16
+        for s in (li + 4, li):
+            for r in range(1 << db):
+                for g in range(0, threads, 16):
+                    low = {column_addr(phase(s, logical(t), r), li, paired) % 16 for t in range(g, g + 16)}
+                    worst = min(worst, len(low))
+        assert worst == distinct
