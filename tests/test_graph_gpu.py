@@ -1,7 +1,8 @@
 """Plans captured into a HIP graph (torch.cuda.graph) and replayed several
 times, with eager work between replays, match their eager results on every
 replay: one-, two- and three-pass FFT, one- and two-pass NTT, FWHT (packed and
-pitched), a semantic-boundary plan and a rank-2 composition. Execution
+pitched; the lane-swap and MFMA lowerings too), a semantic-boundary plan and
+a rank-2 composition. Execution
 allocates nothing and records no memset, so capture is legal for every plan
 (reference execution semantics, docs/c_api.md:29-33)."""
 import numpy as np
@@ -27,8 +28,8 @@ def fwht(n, batch, **kw):
     return cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch, **kw)
 
 
-def fwht16(n, batch):
-    return cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [n], compute=cb.ComputeType.FP32, batch=batch, output_scale=n ** -0.5, output_rounding=cb.OutputRounding.FINAL_STORAGE)
+def fwht16(n, batch, **kw):
+    return cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [n], compute=cb.ComputeType.FP32, batch=batch, output_scale=n ** -0.5, output_rounding=cb.OutputRounding.FINAL_STORAGE, **kw)
 
 
 CASES = {
@@ -44,7 +45,14 @@ CASES = {
                           output_batch_stride=1040), np.float32, 7 * 1040 + 1024),
     "boundary": (fft(256, 6, input_strides=[6], input_batch_stride=1), np.complex64, 6 * 256),
     "rank2": (fft([64, 128], 2), np.complex64, 2 * 64 * 128),
+    "fwht-fp16-lanes": (fwht16(128, 4096 + 7), np.float16, (4096 + 7) * 128),
+    "fwht-fp32-lanes": (fwht(256, 300), np.float32, 300 * 256),
+    "fwht-fp16-mfma": (fwht16(4096, 64, arithmetic_policy=cb.ArithmeticPolicy.ALLOW_FP16_MMA), np.float16, 1 << 18),
 }
+
+# Explicit lowerings of some cases (the others use the default).
+ALGORITHMS = {"fwht-fp16-lanes": "fwht-fp16-fp32-lanes-r64", "fwht-fp32-lanes": "fwht-fp32-lanes-r64",
+              "fwht-fp16-mfma": "fwht-fp16-mfma16"}
 
 
 def host_data(dtype, size, seed):
@@ -61,7 +69,10 @@ def test_replays_match_eager(torch_gpu, lib, case):
     t, dtype, span = CASES[case]
     torch = torch_gpu
     stream = torch.cuda.Stream()
-    with cb.Plan(lib, t, stream=stream.cuda_stream) as plan:
+    kw = {"algorithm": ALGORITHMS[case]} if case in ALGORITHMS else {}
+    with cb.Plan(lib, t, stream=stream.cuda_stream, **kw) as plan:
+        if kw:
+            assert plan.algorithm_name() == kw["algorithm"]
         out_span = plan.output_size() // np.dtype(dtype).itemsize
         assert plan.input_size() == span * np.dtype(dtype).itemsize
         ws_bytes = plan.workspace_size()
