@@ -657,6 +657,96 @@ void launch_wide(const void* in, void* out, std::uint64_t rows, std::uint64_t in
                        static_cast<unsigned>(rows), in_pitch, out_pitch, norm, scale);
 }
 
+// ---- 32 registers per thread, short rows (2^7 and 2^8 points) ----------------
+//
+// A workgroup of 128 threads owns a tile of 4096 elements, 2^(12 - log n)
+// whole rows. Phase 0: thread t holds the 32 consecutive elements from 32 t
+// and butterflies element bits 0-4. Phase 1 (one LDS exchange): registers
+// hold element bits 5 .. log n - 1 (register bits kP .. 4) and, below them,
+// element bits 0 .. kP - 1 as passengers (kP = 10 - log n), so each thread
+// butterflies the remaining bits and ends with runs of 2^kP consecutive
+// results (8 or 16 bytes) that leave as vector stores; the thread bits are
+// element bits kP .. 4 and the row. Same stages in the same order as the
+// other kernels, so results are bit-identical.
+// LDS image: the low five word bits XORed with word bits 5-9 rotated right
+// by log n - 5 (a bijection, linear over bits), which puts every 32-lane
+// group of both exchange accesses on 32 distinct banks.
+template <int LOG_N>
+struct ShortMap {
+    static constexpr int kP = 10 - LOG_N;  // passenger bits of phase 1
+    static constexpr int kB1 = LOG_N - 5;  // butterfly bits of phase 1
+    static __device__ __forceinline__ constexpr unsigned lds_word(unsigned i) {
+        const unsigned hi = (i >> 5) & 31u;
+        const unsigned rot = ((hi >> kB1) | (hi << (5 - kB1))) & 31u;
+        return i ^ rot;
+    }
+    // Phase 1: element of (thread t, register r), split into thread and
+    // register parts over disjoint bits.
+    static __device__ __forceinline__ constexpr unsigned i1_thread(unsigned t) {
+        return ((t & ((1u << kB1) - 1u)) << kP) | ((t >> kB1) << LOG_N);
+    }
+    static __device__ __forceinline__ constexpr unsigned i1_register(unsigned r) {
+        return (r & ((1u << kP) - 1u)) | ((r >> kP) << 5);
+    }
+};
+
+// Rows at input + k * in_pitch / output + k * out_pitch (elements; packed
+// rows have pitch n); rows past `rows` are absent (the buffer range drops
+// their accesses; every access lies in one row). One tile per workgroup.
+template <int LOG_N, class Io>
+__global__ __launch_bounds__(128) void fwht_short_kernel(const typename Io::T* __restrict__ input,
+                                                         typename Io::T* output, unsigned rows,
+                                                         std::uint64_t in_pitch, std::uint64_t out_pitch,
+                                                         float norm, float scale) {
+    static_assert(LOG_N >= 7 && LOG_N <= 8, "the lengths this lowering is offered for");
+    using T = typename Io::T;
+    using M = ShortMap<LOG_N>;
+    constexpr unsigned kN = 1u << LOG_N;
+    constexpr unsigned kRows = 1u << (12 - LOG_N);
+    constexpr unsigned kB = sizeof(T);
+    constexpr int kRun = 1 << M::kP;
+    __shared__ float lds[4096];
+    const unsigned t = threadIdx.x;
+    const std::uint64_t row0 = std::uint64_t(blockIdx.x) * kRows;
+    const unsigned present = unsigned(min(std::uint64_t(kRows), rows - row0));
+    auto span = [&](const T* base, std::uint64_t pitch) {
+        return make_rsrc(base + row0 * pitch, unsigned(((present - 1u) * pitch + kN) * kB));
+    };
+    // Phase 0: elements 32 t .. 32 t + 31 = row t >> (log n - 5), columns from
+    // (t mod 2^(log n - 5)) * 32.
+    const unsigned row = t >> M::kB1, col = (t & ((1u << M::kB1) - 1u)) << kLW;
+    unsigned w[wide_words<Io>()];
+    wide_load<Io>(span(input, in_pitch), unsigned((row * in_pitch + col) * kB), w);
+    float v[kW];
+    wide_unpack_first_stage<Io>(w, v);
+    wide_stages<1, kLW>(v);
+    const unsigned base0 = M::lds_word(t << kLW);
+#pragma unroll
+    for (int r = 0; r < kW; ++r) lds[base0 ^ unsigned(r)] = v[r];
+    lds_barrier();
+    const unsigned base1 = M::lds_word(M::i1_thread(t));
+#pragma unroll
+    for (int r = 0; r < kW; ++r) v[r] = lds[base1 ^ M::lds_word(M::i1_register(unsigned(r)))];
+    wide_stages<M::kP, kLW>(v);
+    finalize<kW>(v, norm, scale);
+    // Run g: register bits kP .. 4 = g, element row (t >> kB1), column
+    // ((t mod 2^kB1) << kP) + (g << 5).
+    const __amdgpu_buffer_rsrc_t dst = span(output, out_pitch);
+    const unsigned out_row = t >> M::kB1, out_col = (t & ((1u << M::kB1) - 1u)) << M::kP;
+#pragma unroll
+    for (int g = 0; g < kW / kRun; ++g)
+        wide_store_run<Io, kRun>(dst, unsigned((out_row * out_pitch + out_col + (unsigned(g) << 5)) * kB),
+                                 v + g * kRun);
+}
+
+template <int LOG_N, class Io>
+void launch_short(const void* in, void* out, std::uint64_t rows, std::uint64_t in_pitch, std::uint64_t out_pitch,
+                  float norm, float scale, unsigned grid, hipStream_t stream) {
+    hipLaunchKernelGGL((fwht_short_kernel<LOG_N, Io>), dim3(grid), dim3(128), 0, stream,
+                       static_cast<const typename Io::T*>(in), static_cast<typename Io::T*>(out),
+                       static_cast<unsigned>(rows), in_pitch, out_pitch, norm, scale);
+}
+
 // ---- 64 elements per lane, no LDS (rows of 2^5 .. 2^8 points) --------------
 //
 // A wave owns 4096 consecutive elements (4096 / n rows) and each lane 64 of
@@ -889,8 +979,21 @@ WideLaunch wide_table_entry(int log_n, std::integer_sequence<int, L...>) {
 }
 
 // The 32-register kernel: FP16 rows of 2^11 .. 2^13 points, row count within 32 bits.
+// For FP16 rows of 2^7 and 2^8 points, the short-row form of the same
+// lowering (fwht_short_kernel: 4096-element tiles of whole rows, one LDS
+// exchange, a tile's pitched span within 31-bit byte offsets), without a
+// persistent variant. At 2^6 points its 32-byte runs leave as two 16-byte
+// stores with 16-byte gaps across the lanes, and it measured 64 us against
+// 47 us for C5b's volume; it is not offered there.
 WideLaunch wide_launcher(const Request& r) {
-    if (!r.fp16_final || r.log_n < 11 || r.log_n > 13 || r.batch > 0xffffffffull) return {};
+    if (!r.fp16_final || r.batch > 0xffffffffull) return {};
+    if (r.log_n >= 7 && r.log_n <= 8) {
+        const std::uint64_t rows_per_tile = std::uint64_t{1} << (12 - r.log_n);
+        const std::uint64_t pitch = r.pitched ? std::max(r.in_batch_stride, r.out_batch_stride) : r.n;
+        if (rows_per_tile * pitch * 2 >= (std::uint64_t{1} << 31)) return {};
+        return WideLaunch{r.log_n == 7 ? launch_short<7, F16Io> : launch_short<8, F16Io>, nullptr, nullptr};
+    }
+    if (r.log_n < 11 || r.log_n > 13) return {};
     return wide_table_entry(int(r.log_n), std::make_integer_sequence<int, 3>{});
 }
 
@@ -948,7 +1051,8 @@ class FwhtExecutor final : public Executor {
                      std::string(r.log_n >= 7 ? ", bits 6+ in registers" : "") + ", no LDS";
         } else {
             const bool wide = kind != FwhtKind::Resident;
-            const int lb = wide ? static_cast<int>(r.log_n) : r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
+            const bool short_rows = wide && r.log_n < 11;  // fwht_short_kernel: 4096-element tiles
+            const int lb = short_rows ? 12 : wide ? static_cast<int>(r.log_n) : r.log_n <= 12 ? 12 : static_cast<int>(r.log_n);
             const std::uint64_t rows_per_tile = std::uint64_t{1} << (lb - int(r.log_n));
             tiles = pitched_ || wide ? (r.batch + rows_per_tile - 1) / rows_per_tile
                                      : (total + (1ull << lb) - 1) >> lb;
@@ -956,8 +1060,8 @@ class FwhtExecutor final : public Executor {
             const int regs_log = wide ? kLW : kLE;
             threads = 1u << (lb - regs_log);
             regs = 1u << regs_log;
-            phases = wide ? 3u : unsigned((r.log_n + kLE - 1) / kLE);
-            lds = ((1u << lb) + ((1u << lb) >> regs_log)) * 4ull;
+            phases = short_rows ? 2u : wide ? 3u : unsigned((r.log_n + kLE - 1) / kLE);
+            lds = short_rows ? 4096ull * 4 : ((1u << lb) + ((1u << lb) >> regs_log)) * 4ull;
             // Grid: one workgroup per tile (measured at least as fast as a
             // persistent, occupancy-sized grid for every BASELINE shape once
             // the kernel's prefetch overlapped), capped at the launch limit;
@@ -965,11 +1069,15 @@ class FwhtExecutor final : public Executor {
             // prefetch.
             grid_ = static_cast<unsigned>(std::min<std::uint64_t>(tiles, 0x7fffffffull));
             if (kind == FwhtKind::WidePersistent) grid_ = std::min(grid_, resident);
-            reason = wide ? "one row per workgroup (" + std::to_string(threads) +
-                                " threads x 32 registers, phases of bits 0-4, 5-9 and 10+, the last carrying the low "
-                                "element bits so results leave as 8- to 64-byte vectors)"
-                          : "whole rows resident in one workgroup (" + std::to_string(threads) +
-                                " threads x 16 registers, padded LDS exchange)";
+            reason = short_rows
+                         ? "whole rows resident in one workgroup (128 threads x 32 registers, phases of bits 0-4 "
+                           "and 5+, the second carrying the low element bits so results leave as 8- to 32-byte "
+                           "vectors, one swizzled LDS exchange)"
+                     : wide ? "one row per workgroup (" + std::to_string(threads) +
+                                  " threads x 32 registers, phases of bits 0-4, 5-9 and 10+, the last carrying the low "
+                                  "element bits so results leave as 8- to 64-byte vectors)"
+                            : "whole rows resident in one workgroup (" + std::to_string(threads) +
+                                  " threads x 16 registers, padded LDS exchange)";
             reason += std::string(grid_ < tiles ? ", persistent grid with next-tile prefetch" : "");
         }
         require(tiles <= 0xffffffffull, "FWHT batch exceeds the tile index range");
@@ -1027,9 +1135,9 @@ class FwhtExecutor final : public Executor {
 // and explicit choices.
 std::vector<FwhtKind> fwht_kinds(const Request& r) {
     std::vector<FwhtKind> kinds = {FwhtKind::Resident};
-    if (wide_launcher(r)) {
+    if (const WideLaunch wide = wide_launcher(r)) {
         kinds.push_back(FwhtKind::Wide);
-        kinds.push_back(FwhtKind::WidePersistent);
+        if (wide.walk) kinds.push_back(FwhtKind::WidePersistent);
         if (r.log_n == 12) std::swap(kinds[0], kinds[1]);
     }
     if (lane_launcher(r)) kinds.push_back(FwhtKind::Lanes);

@@ -111,7 +111,8 @@ def test_measure_lists_both_lowerings(torch_gpu, lib, stream, tmp_path):
 
 @pytest.mark.parametrize("log_n,fp16", [(10, True), (14, True), (12, False)])
 def test_other_shapes_refuse_the_wide_lowering(lib, log_n, fp16):
-    # Only FP16 rows of 2^11..2^13 points (FP32 words would spill the registers).
+    # Only FP16 rows of 2^7, 2^8 (the short-row kernel) and 2^11..2^13 points
+    # (FP32 words would spill the registers).
     with pytest.raises(cb.AbiError) as e:
         cb.Plan(lib, transform(log_n, 8, fp16), **explicit(wide_name(fp16)))
     assert e.value.status == cb.Status.NOT_SUPPORTED
