@@ -10,8 +10,13 @@ configuration: W untimed eager calls, then a HIP graph of 20 calls captured and
 replayed R = max(7, ceil(K / 20)) times back to back, each replay bracketed by
 HIP events on the plans' stream; the time per call is the MEDIAN replay / 20
 (the reference's protocol: 10 warmups, a graph of 20 calls, median of 7
-replays). The calls rotate over buffer sets larger than twice the 256 MB
-Infinity Cache, so inputs come from HBM.
+replays). The default K = 1200 gives 60 replays: on MI355X the first dozen or
+so replays after the GPU has idled run up to 12% slower than the rest (a
+clock / power transient, e.g. C5b 46.9, 48.4, ... 52.0, then 46.2-46.9 us per
+call from about the 25th replay on, whatever the eager warmup), so the median
+of 7 reads the transient and the median of 60 the sustained rate. The calls
+rotate over buffer sets larger than twice the 256 MB Infinity Cache, so
+inputs come from HBM.
 
 The default runs all seven BASELINE configurations. Rank 0 prints ONE JSON
 line: the driver's fields for the headline configuration (--headline, default
@@ -600,7 +605,7 @@ def measure(torch, lib, name, args, mapping=None):
 def main():
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=140)
+    parser.add_argument("--steps", type=int, default=1200)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="all", choices=["all"] + sorted(WORKLOADS))
     parser.add_argument("--headline", default=DEFAULT_HEADLINE, choices=BASELINE_CONFIGS)
