@@ -48,11 +48,12 @@ CASES = {
     "fwht-fp16-lanes": (fwht16(128, 4096 + 7), np.float16, (4096 + 7) * 128),
     "fwht-fp32-lanes": (fwht(256, 300), np.float32, 300 * 256),
     "fwht-fp16-mfma": (fwht16(4096, 64, arithmetic_policy=cb.ArithmeticPolicy.ALLOW_FP16_MMA), np.float16, 1 << 18),
+    "fwht-fp16-short": (fwht16(256, 16 * 40 + 3), np.float16, (16 * 40 + 3) * 256),
 }
 
 # Explicit lowerings of some cases (the others use the default).
 ALGORITHMS = {"fwht-fp16-lanes": "fwht-fp16-fp32-lanes-r64", "fwht-fp32-lanes": "fwht-fp32-lanes-r64",
-              "fwht-fp16-mfma": "fwht-fp16-mfma16"}
+              "fwht-fp16-mfma": "fwht-fp16-mfma16", "fwht-fp16-short": "fwht-fp16-fp32-resident-r32"}
 
 
 def host_data(dtype, size, seed):
