@@ -154,28 +154,45 @@ class SearchTrace {
     std::uint64_t id_ = 0;
 };
 
-// Mean milliseconds of one execution: 3 untimed runs, then 20 between two
-// events on the selection stream (the reference's host-event-loop protocol,
-// warmup 3 / repeat 20).
-// Mean time of one execute over `sets` rotating input / output buffers
-// (in_place: the input buffers only).
-double time_executor(Executor& e, const std::vector<DeviceScratch>& in, const std::vector<DeviceScratch>& out,
-                     bool in_place, void* ws, hipStream_t stream) {
-    constexpr int kWarmup = 3, kRepeat = 20;
+// Milliseconds per execution of each candidate, over `sets` rotating input /
+// output buffers (in_place: the input buffers only). Every candidate first
+// runs kWarmup untimed calls; then kRounds rounds each time one block of
+// kCalls calls per candidate, in candidate order, between two events on the
+// selection stream; a candidate's figure is its median block / kCalls.
+// Interleaving gives every candidate the same clock state: on MI355X the
+// first few hundred calls after an idle gap run up to 12% slower than the
+// sustained rate (a power / clock transient), which timing the candidates
+// one after another would charge to whichever came first.
+constexpr int kWarmup = 3, kRounds = 7, kCalls = 10;
+std::vector<double> time_executors(const std::vector<std::unique_ptr<Executor>>& es,
+                                   const std::vector<DeviceScratch>& in, const std::vector<DeviceScratch>& out,
+                                   bool in_place, void* ws, hipStream_t stream) {
     const std::size_t sets = in.size();
-    auto run = [&](int i) {
+    auto run = [&](Executor& e, int i) {
         const std::size_t k = std::size_t(i) % sets;
         e.execute(in[k].ptr, in_place ? in[k].ptr : out[k].ptr, ws, stream);
     };
-    for (int i = 0; i < kWarmup; ++i) run(i);
+    for (const auto& e : es)
+        for (int i = 0; i < kWarmup; ++i) run(*e, i);
+    std::vector<std::vector<double>> blocks(es.size());
     Event start, stop;
-    hip_check(hipEventRecord(start.e, stream), "MEASURE event record");
-    for (int i = 0; i < kRepeat; ++i) run(i);
-    hip_check(hipEventRecord(stop.e, stream), "MEASURE event record");
-    hip_check(hipEventSynchronize(stop.e), "MEASURE synchronize");
-    float ms = 0.0f;
-    hip_check(hipEventElapsedTime(&ms, start.e, stop.e), "MEASURE elapsed time");
-    return double(ms) / kRepeat;
+    for (int round = 0; round < kRounds; ++round) {
+        for (std::size_t c = 0; c < es.size(); ++c) {
+            hip_check(hipEventRecord(start.e, stream), "MEASURE event record");
+            for (int i = 0; i < kCalls; ++i) run(*es[c], round * kCalls + i);
+            hip_check(hipEventRecord(stop.e, stream), "MEASURE event record");
+            hip_check(hipEventSynchronize(stop.e), "MEASURE synchronize");
+            float ms = 0.0f;
+            hip_check(hipEventElapsedTime(&ms, start.e, stop.e), "MEASURE elapsed time");
+            blocks[c].push_back(double(ms) / kCalls);
+        }
+    }
+    std::vector<double> result;
+    for (auto& b : blocks) {
+        std::sort(b.begin(), b.end());
+        result.push_back(b[b.size() / 2]);
+    }
+    return result;
 }
 
 }  // namespace
@@ -320,7 +337,9 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     require(!built.empty(), "no candidate lowering to measure");
     while (sets > 1 && sets * footprint + ws_bytes > budget) --sets;
     trace.event("inventory", "\"key\":" + json::quote(key) + ",\"candidate_count\":" + std::to_string(names.size()) +
-                                 ",\"timing_protocol\":\"event-loop\",\"warmup\":3,\"repeat\":20," +
+                                 ",\"timing_protocol\":\"interleaved-rounds\",\"warmup\":" +
+                                 std::to_string(kWarmup) + ",\"rounds\":" + std::to_string(kRounds) +
+                                 ",\"calls_per_round\":" + std::to_string(kCalls) + "," +
                                  "\"buffer_sets\":" + std::to_string(sets) + ",\"input_bytes\":" +
                                  std::to_string(in_bytes) + ",\"output_bytes\":" + std::to_string(out_bytes) +
                                  ",\"workspace_bytes\":" + std::to_string(ws_bytes) + ",\"scratch_bytes\":" +
@@ -347,8 +366,9 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     std::size_t best = 0;
     double best_ms = std::numeric_limits<double>::infinity();
     std::string results;
+    const std::vector<double> times = time_executors(built, in, out, r.in_place, ws->ptr, sel->stream);
     for (std::size_t i = 0; i < built.size(); ++i) {
-        const double ms = time_executor(*built[i], in, out, r.in_place, ws->ptr, sel->stream);
+        const double ms = times[i];
         char text[64];
         std::snprintf(text, sizeof text, "=%.4f ms", ms);
         results += (i ? ", " : "") + built[i]->algorithm + text;
