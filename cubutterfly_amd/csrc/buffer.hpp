@@ -20,16 +20,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, st
 // byte_off: per-lane offset; scalar_off: a wave-uniform offset carried in
 // the instruction's scalar operand (outside the range check: callers use it
 // only where every access lies inside the resource's range). T is a 4- or
-// 8-byte type.
-template <class T>
+// 8-byte type. AUX: the instruction's cache-policy bits.
+template <class T, int AUX = 0>
 __device__ __forceinline__ T buffer_load(__amdgpu_buffer_rsrc_t r, std::uint32_t byte_off, std::uint32_t scalar_off = 0) {
     static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- or 8-byte elements");
     if constexpr (sizeof(T) == 4) {
         return __builtin_bit_cast(
-            T, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0));
+            T, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(byte_off), static_cast<int>(scalar_off), AUX));
     } else {
         return __builtin_bit_cast(
-            T, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), static_cast<int>(scalar_off), 0));
+            T, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), static_cast<int>(scalar_off), AUX));
     }
 }
 

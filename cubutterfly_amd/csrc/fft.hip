@@ -387,13 +387,18 @@ struct FftPass {
     // the tile origin enters only the thread part. A partial one-pass tile
     // keeps the whole offset in the lane offset, which the range check sees.
     static constexpr bool kLaneOnly = SINGLE && LI > 0;
+    // One-pass tiles read the caller's input once: nontemporal loads (C3b
+    // 56.2-56.3 -> 55.6-55.8 us). Multi-pass tiles keep the default policy
+    // (their later passes read the intermediate back from the caches; C3a
+    // measured slower with nontemporal loads).
+    static constexpr int kLoadAux = SINGLE ? 2 : 0;
     // (Two-pass register offsets depend on l1 / l2 at run time, so the choice
     // is a wave-uniform branch there; keeping small offsets in the lane offset
     // measured faster than always using the scalar offset.)
     static __device__ __forceinline__ float2 load_at(__amdgpu_buffer_rsrc_t src, std::uint32_t lane_bytes,
                                                      std::uint32_t reg_bytes) {
-        if (kLaneOnly || reg_bytes < 4096u) return buffer_load<float2>(src, lane_bytes + reg_bytes);
-        return buffer_load<float2>(src, lane_bytes, reg_bytes);
+        if (kLaneOnly || reg_bytes < 4096u) return buffer_load<float2, kLoadAux>(src, lane_bytes + reg_bytes);
+        return buffer_load<float2, kLoadAux>(src, lane_bytes, reg_bytes);
     }
     // Final-pass stores (the caller's output, written once) are nontemporal
     // where a wave's stores form segments of at least 512 bytes: one-pass
