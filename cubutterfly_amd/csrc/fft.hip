@@ -665,10 +665,62 @@ struct FftPass {
         // copied between registers: a copy would make the wait for its loads
         // also wait for the prefetch issued after them.
         float2 w[kE];
+        if constexpr (kDeep) {  // three buffers in turn, two tiles ahead
+            Tile t1 = decode(a, range_base + pos + stride, m);
+            load(a, t1, t, m, w, pos + stride < range_end);
+            float2 x[kE];
+            for (;;) {
+                if (!step2(a, t, m, pos, stride, range_base, range_end, tl, t1, bs, v, w, x, lds)) break;
+                if (!step2(a, t, m, pos, stride, range_base, range_end, tl, t1, bs, w, x, v, lds)) break;
+                if (!step2(a, t, m, pos, stride, range_base, range_end, tl, t1, bs, x, v, w, lds)) break;
+            }
+            return;
+        }
         for (;;) {
             if (!step(a, t, m, pos, stride, range_base, range_end, tl, bs, v, w, lds)) break;
             if (!step(a, t, m, pos, stride, range_base, range_end, tl, bs, w, v, lds)) break;
         }
+    }
+    // Column passes with 4-bit digits walk two tiles ahead: the tile after
+    // `next` (already loading) is prefetched into a third buffer `far`, so a
+    // workgroup keeps two tiles of loads in flight (123 VGPRs, within the
+    // 128 of 4 waves per SIMD; C3a 141.0-141.5 -> 138.7 us, its first pass
+    // reading from HBM). The row passes would spill with a third buffer, and
+    // the 5-bit one-row tiles have no room for it.
+    static constexpr bool kDeep = COL && DB == 4;
+    // One tile of the depth-two walk (see step): prefetch the tile two ahead
+    // into `far` in the same slices, process `cur`; `next` stays allocated
+    // throughout, as `cur` does through its stores. Returns whether the
+    // following tile exists; `tl_next` is the tile in `next`.
+    static __device__ __forceinline__ bool step2(const FftArgs& a, std::uint32_t t, std::uint32_t m, std::uint32_t& pos,
+                                                 std::uint32_t stride, std::uint32_t range_base,
+                                                 std::uint32_t range_end, Tile& tl, Tile& tl_next, float2 (&bs)[3],
+                                                 float2 (&cur)[kE], float2 (&next)[kE], float2 (&far)[kE], float2* lds) {
+        std::uint32_t tt = t;
+        asm volatile("" : "+v"(tt));
+        const std::uint32_t following = pos + stride, ahead = pos + 2 * stride;
+        const bool more = following < range_end, more2 = ahead < range_end;
+        if constexpr (COL) bases_of(bs, a, tt, tl.c0, m);
+        const Tile tf = decode(a, range_base + ahead, m);
+        load<0, slice_end(0)>(a, tf, tt, m, far, more2);
+        __builtin_amdgcn_sched_barrier(0);
+        process(a, tl, tt, m, cur, bs, lds, [&](auto point) {
+            constexpr int K = decltype(point)::value;
+            if constexpr (slice_at(K)) {
+                constexpr int S = slice_before(K) + 1;
+                __builtin_amdgcn_sched_barrier(0);
+                load<slice_end(S - 1), slice_end(S)>(a, tf, tt, m, far, more2);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        });
+#pragma unroll
+        for (int r = 0; r < kE; ++r) opaque(cur[r]);
+#pragma unroll
+        for (int r = 0; r < kE; ++r) opaque(next[r]);
+        pos = following;
+        tl = tl_next;
+        tl_next = tf;
+        return more;
     }
 
     // Hook points of process() that issue a prefetch slice: inside each
