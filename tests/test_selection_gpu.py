@@ -177,6 +177,9 @@ def test_plan_trace(torch_gpu, lib, stream, tmp_path, monkeypatch):
     assert {r["schema"] for r in rows} == {"cubutterfly-plan-search-trace-v1"}
     phases = [r["phase"] for r in rows]
     assert phases[0] == "inventory" and phases[-1] == "selected"
+    # Candidates are timed in interleaved rounds, each scored by its median block.
+    assert rows[0]["timing_protocol"] == "interleaved-rounds"
+    assert rows[0]["rounds"] >= 3 and rows[0]["calls_per_round"] >= 1
     results = [r for r in rows if r["phase"] == "result"]
     assert len(results) == rows[0]["candidate_count"] and all(r["kernel_ms"] > 0 for r in results)
     assert rows[-1]["algorithm"] == chosen
