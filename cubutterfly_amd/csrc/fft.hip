@@ -318,7 +318,9 @@ struct FftPass {
     }
 
     // `between` runs after this wave's LDS writes, before the barrier.
-    template <int FROM, int TO, class Between>
+    // RELABEL: the reading threads take the last phase's relabelled
+    // positions (last_thread_index).
+    template <int FROM, int TO, bool RELABEL = false, class Between>
     static __device__ __forceinline__ void exchange(float2 (&v)[kE], float2* lds, std::uint32_t t,
                                                     Between&& between) {
         lds_barrier();
@@ -326,8 +328,29 @@ struct FftPass {
         for (int r = 0; r < kE; ++r) lds[L::split(index<FROM>(t, 0), index<FROM>(0, r))] = v[r];
         between();
         lds_barrier();
+        const std::uint32_t it = RELABEL ? last_thread_index(t) : index<TO>(t, 0);
 #pragma unroll
-        for (int r = 0; r < kE; ++r) v[r] = lds[L::split(index<TO>(t, 0), index<TO>(0, r))];
+        for (int r = 0; r < kE; ++r) v[r] = lds[L::split(it, index<TO>(0, r))];
+    }
+
+    // One-row 5-bit tiles store their results straight from registers. The
+    // last phase holds tile positions 0-4 in registers (p = thread part |
+    // r), and its threads are relabelled so that for every register the 64
+    // lanes of a wave hold 64 consecutive outputs (output k = bitrev(p)):
+    // lane bits 0-3 take position bits LT-2..LT-5 (output bits 1-4), lane
+    // bit 4 position bit LT-1 (output bit 0), lane bit 5 position bit LT-6
+    // (output bit 5), the wave index bits 5 and up. Each store instruction
+    // then writes 512 contiguous bytes, and the final LDS round trip is gone
+    // (C3b 55.9-56.1 -> 54.5-54.7 us against the paired stores through LDS).
+    // The relabelled reads keep every 16-lane group on 16 distinct bank
+    // pairs of the XOR image: its lanes vary position bits LT-5..LT-2, the
+    // image's second key field.
+    static constexpr bool kDirectStore = SINGLE && LI == 0 && ORD == 0 && DB == 5;
+    static __device__ __forceinline__ std::uint32_t last_thread_index(std::uint32_t t) {
+        const std::uint32_t l = t & 63u, w = t >> 6;
+        return ((l & 1u) << (LT - 2)) | (((l >> 1) & 1u) << (LT - 3)) | (((l >> 2) & 1u) << (LT - 4)) |
+               (((l >> 3) & 1u) << (LT - 5)) | (((l >> 4) & 1u) << (LT - 1)) | (((l >> 5) & 1u) << (LT - 6)) |
+               (w << 5);
     }
 
     struct Tile {
@@ -505,7 +528,9 @@ struct FftPass {
             at(integral_constant<int, 2>{});
         }
         if constexpr (kPhases > 2) {
-            exchange<tile_window<1>(), tile_window<2>()>(v, lds, t, [&] { at(integral_constant<int, 3>{}); });
+            static_assert(!kDirectStore || kPhases == 3, "the relabelled phase is the last of three");
+            exchange<tile_window<1>(), tile_window<2>(), kDirectStore>(v, lds, t,
+                                                                     [&] { at(integral_constant<int, 3>{}); });
             digit<2>(v, bs[2]);
             at(integral_constant<int, 4>{});
         }
@@ -539,6 +564,21 @@ struct FftPass {
             const std::uint32_t tb = natural_offset(a, tl, index<wl>(t, 0)) * 8u;
 #pragma unroll
             for (int r = 0; r < kE; ++r) store_at(v[r], dst, tb, natural_offset(a, Tile{}, index<wl>(0, r)) * 8u);
+            return;
+        }
+        if constexpr (kDirectStore) {
+            static_assert(wl == 0, "registers hold tile positions 0-4");
+            at(integral_constant<int, 2 * kPhases - 1>{});
+            const std::uint32_t kt = brev(last_thread_index(t), LT) * 8u;
+            if (a.scale == 1.0f) {
+#pragma unroll
+                for (int r = 0; r < kE; ++r) store_at(v[r], dst, kt, brev_const(std::uint32_t(r), LT) * 8u);
+            } else {
+#pragma unroll
+                for (int r = 0; r < kE; ++r)
+                    store_at(make_float2(v[r].x * a.scale, v[r].y * a.scale), dst, kt,
+                             brev_const(std::uint32_t(r), LT) * 8u);
+            }
             return;
         }
         // Final pass: bit-reversed positions -> natural order through LDS.

@@ -89,3 +89,33 @@ def test_paired_column_tiles_are_conflict_free():
                     low = {column_addr(phase(s, logical(t), r), li, paired) % 16 for t in range(g, g + 16)}
                     worst = min(worst, len(low))
         assert worst == distinct
+
+
+def last_thread_index(t, lt):
+    """FftPass::last_thread_index: the relabelled last phase of one-row 5-bit
+    tiles (direct stores)."""
+    l, w = t & 63, t >> 6
+    return (((l & 1) << (lt - 2)) | (((l >> 1) & 1) << (lt - 3)) | (((l >> 2) & 1) << (lt - 4)) |
+            (((l >> 3) & 1) << (lt - 5)) | (((l >> 4) & 1) << (lt - 1)) | (((l >> 5) & 1) << (lt - 6)) | (w << 5))
+
+
+@pytest.mark.parametrize("lt", [13, 14])
+def test_direct_store_relabelling(lt):
+    # One-row tiles of 2^13 / 2^14 points store their results from registers:
+    # thread t, register r holds tile position last_thread_index(t) | r, whose
+    # output index is its bit reversal. The relabelling is a bijection, every
+    # register of a wave stores 64 consecutive outputs (512 contiguous bytes),
+    # and its LDS reads keep each 16-lane group on 16 distinct bank pairs.
+    db, threads = 5, 1 << (lt - 5)
+    assert sorted(last_thread_index(t, lt) | r for t in range(threads) for r in range(32)) == list(range(1 << lt))
+    for r in range(32):
+        for w in range(threads // 64):
+            ks = sorted(brev(last_thread_index(64 * w + l, lt) | r, lt) for l in range(64))
+            assert ks == list(range(ks[0], ks[0] + 64)) and ks[0] % 64 == 0
+        for g in range(0, threads, 16):
+            low = {addr(last_thread_index(t, lt) | r, lt, db) & 15 for t in range(g, g + 16)}
+            assert len(low) == 16, (r, g)
+    # A relabelling with lanes on position bits LT-4..LT-1 (the plain reversal
+    # of output bits 0-3) would leave two lanes per bank pair.
+    plain = lambda t: ((int(format(t & 15, "04b")[::-1], 2)) << (lt - 4)) | ((t >> 4) << 5)
+    assert min(len({addr(plain(t) | 0, lt, db) & 15 for t in range(g, g + 16)}) for g in range(0, threads, 16)) < 16

@@ -18,6 +18,10 @@ checks, per interval between barriers:
 * every read hits a word written in the latest write interval of the same
   tile (no stale word from the previous tile or an earlier phase).
 
+The natural-order 2^13 / 2^14-point tiles store straight from registers
+instead (FftPass::kDirectStore): their last exchange reads with relabelled
+threads and no final store exchange follows; the model covers that walk too.
+
 The same holds for an enumeration in which each lane stores two neighbouring
 outputs (the removed "paired final stores" variant's read pattern): its
 reads still sit in the one read interval that the next tile's first barrier
@@ -45,10 +49,19 @@ def window(lt, db, p):
     return max(lt - db * (p + 1), 0)
 
 
-def walk(lt, db, tiles, store_order):
+def last_thread_index(t, lt):
+    """FftPass::last_thread_index (one-row 5-bit tiles with direct stores)."""
+    l, w = t & 63, t >> 6
+    return (((l & 1) << (lt - 2)) | (((l >> 1) & 1) << (lt - 3)) | (((l >> 2) & 1) << (lt - 4)) |
+            (((l >> 3) & 1) << (lt - 5)) | (((l >> 4) & 1) << (lt - 1)) | (((l >> 5) & 1) << (lt - 6)) | (w << 5))
+
+
+def walk(lt, db, tiles, store_order, direct=False):
     """Per-interval LDS events of `tiles` consecutive tiles: a list of
     intervals, each a list of (tile, kind, wave, word, tag) with kind 'w' or
-    'r' and tag naming the layout step a read must see."""
+    'r' and tag naming the layout step a read must see. direct: the last
+    phase's reads take the relabelled threads and the results leave from
+    registers (no final store exchange)."""
     threads = 1 << (lt - db)
     regs = 1 << db
     phases = (lt + db - 1) // db
@@ -56,6 +69,8 @@ def walk(lt, db, tiles, store_order):
     for tile in range(tiles):
         for p in range(phases):
             last = p == phases - 1
+            if last and direct:
+                break
             # barrier, writes of digit p's layout, barrier, reads
             writes, reads = [], []
             s_from = window(lt, db, p)
@@ -66,7 +81,9 @@ def walk(lt, db, tiles, store_order):
                 s_to = window(lt, db, p + 1)
                 for t in range(threads):
                     for r in range(regs):
-                        reads.append((tile, "r", t // 64, swizzled(phase_index(s_to, db, t, r), lt, db), p))
+                        i = (last_thread_index(t, lt) | r) if direct and p + 1 == phases - 1 else \
+                            phase_index(s_to, db, t, r)
+                        reads.append((tile, "r", t // 64, swizzled(i, lt, db), p))
             else:
                 for t, words in store_order(threads, regs):
                     for i in words:
@@ -116,6 +133,14 @@ def check(intervals):
 def test_walk_lds_protocol_has_no_hazard(lt, db, order):
     store = natural_store(lt) if order == "natural" else paired_store(lt)
     check(walk(lt, db, 2, store))
+
+
+@pytest.mark.parametrize("lt", [14, 13])
+def test_walk_with_direct_stores_has_no_hazard(lt):
+    # The one-row 5-bit tiles' default (natural order): the relabelled last
+    # exchange, then stores from registers; the next tile's first exchange
+    # barrier closes the last read interval.
+    check(walk(lt, 5, 3, None, direct=True))
 
 
 def test_model_catches_a_missing_barrier():
