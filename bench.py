@@ -6,17 +6,18 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|c1|c2|c3a|c3
 
 A step is one call of the hot path over one batch of a BASELINE configuration
 (C2 and C4: forward then inverse), inputs already resident in HBM. Per
-configuration: W untimed eager calls, then a HIP graph of 20 calls captured and
-replayed R = max(7, ceil(K / 20)) times back to back, each replay bracketed by
-HIP events on the plans' stream; the time per call is the MEDIAN replay / 20
-(the reference's protocol: 10 warmups, a graph of 20 calls, median of 7
-replays). The default K = 1200 gives 60 replays: on MI355X the first dozen or
-so replays after the GPU has idled run up to 12% slower than the rest (a
-clock / power transient, e.g. C5b 46.9, 48.4, ... 52.0, then 46.2-46.9 us per
-call from about the 25th replay on, whatever the eager warmup), so the median
-of 7 reads the transient and the median of 60 the sustained rate. The calls
-rotate over buffer sets larger than twice the 256 MB Infinity Cache, so
-inputs come from HBM.
+configuration: W untimed eager calls, then a HIP graph of 20 calls captured,
+replayed untimed for at least 30 replays and 50 ms of GPU time (the settle
+phase), and then, queued behind it with no host synchronisation in between,
+replayed R = max(7, ceil(K / 20)) times, each replay bracketed by HIP events
+on the plans' stream; the time per call is the MEDIAN replay / 20 (the
+reference's protocol: 10 warmups, a graph of 20 calls, median of 7 replays).
+The settle phase exists because on MI355X the first two dozen replays after
+the GPU has idled run up to 12% slower than the rest (a clock / power
+transient, e.g. C5b 46.9, 48.4, ... 52.0, then 46.2-46.9 us per call from
+about the 25th replay on, whatever the eager warmup): the timed replays then
+read the sustained rate at any K. The calls rotate over buffer sets larger
+than twice the 256 MB Infinity Cache, so inputs come from HBM.
 
 The default runs all seven BASELINE configurations. Rank 0 prints ONE JSON
 line: the driver's fields for the headline configuration (--headline, default
@@ -44,6 +45,10 @@ HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 CALLS_PER_GRAPH = 20
 MIN_REPLAYS = 7
+# Untimed graph replays queued right before the timed ones: at least this
+# many, covering at least this much GPU time.
+SETTLE_REPLAYS = 30
+SETTLE_MS = 50.0
 TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
 BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5a", "c5b"]
 DEFAULT_HEADLINE = "c5a"
@@ -380,6 +385,13 @@ class FwhtFp16(OnePlan):
         self.bytes_per_call = 2 * rows * n * 2
         self.scale = float(np.float32(1.0 / np.sqrt(n)))
 
+    def plan_args(self):
+        # The MFMA lowering is taken by name (ALLOW_FP16_MMA keeps the
+        # stage-ordered kernel as its default).
+        if self.mma and not self.mapping:
+            return {"algorithm": "fwht-fp16-mfma16"}
+        return super().plan_args()
+
     def descriptor(self, cb):
         policy = cb.ArithmeticPolicy.ALLOW_FP16_MMA if self.mma else cb.ArithmeticPolicy.STRICT
         return cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [self.n], self.rows, compute=cb.ComputeType.FP32,
@@ -463,6 +475,19 @@ def time_graph_replays(torch, workload, stream, steps, warmup):
     with torch.cuda.stream(stream):  # replay() launches on the current stream
         graph.replay()  # the first replay uploads the graph
         torch.cuda.synchronize()
+        # One replay timed alone sizes the settle phase.
+        probe = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        probe[0].record(stream)
+        graph.replay()
+        probe[1].record(stream)
+        torch.cuda.synchronize()
+        replay_ms = max(probe[0].elapsed_time(probe[1]), 1e-3)
+        settle = max(SETTLE_REPLAYS, int(SETTLE_MS / replay_ms) + 1)
+        # Untimed replays, then the timed ones, queued back to back with no
+        # host synchronisation in between: the GPU never idles before the
+        # timed region, so it is measured past the post-idle clock transient.
+        for _ in range(settle):
+            graph.replay()
         for start, stop in marks:
             start.record(stream)
             graph.replay()
@@ -653,8 +678,10 @@ def main():
         "roofline": dict(head["roofline"], kernel=head["kernel"]),
         "timing": ("eager calls" if args.eager else
                    f"median of {len(head['ms_per_call_replays'])} replays of a HIP graph of {CALLS_PER_GRAPH} "
-                   "calls, HIP events on the plans' stream (ms_per_call_first7: the median of the first "
-                   f"{MIN_REPLAYS}, the reference's protocol, which on MI355X reads a clock transient)"),
+                   f"calls, HIP events on the plans' stream, after an untimed settle phase of at least "
+                   f"{SETTLE_REPLAYS} replays and {SETTLE_MS:.0f} ms queued back to back with the timed replays "
+                   f"(ms_per_call_first7: the median of the first {MIN_REPLAYS} timed replays, the reference's "
+                   "protocol)"),
         "per_config": entries,
     }
     if "cpu_baseline" in head:

@@ -1150,14 +1150,19 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
     supported(r.log_n <= kMaxResidentLog,
               "FWHT lengths above 2^" + std::to_string(kMaxResidentLog) + " are not yet lowered for gfx950");
     supported(!r.allow_mma || r.fp16_final, "MFMA Hadamard blocks require FP16 storage");
-    // ALLOW_FP16_MMA: the MFMA Hadamard-block kernel is the default where it
-    // covers the request; the stage-ordered VALU kernels stay candidates.
+    // ALLOW_FP16_MMA permits the MFMA Hadamard-block kernel but does not make
+    // it the default: the stage-ordered VALU kernels are bit-exact and, on
+    // MI355X, faster at both QuaRot shapes (sustained, 16384 x 4096: 45.4
+    // against 49.0 us; 524288 x 128: 47.6 against 48.4 us). The reference
+    // likewise keeps its native selection unless a calibrated MMA profile
+    // wins (src/mapping_selector.cpp:13-44). The MFMA kernel is taken by name
+    // (EXPLICIT) or when MEASURE times it fastest.
     const bool mfma = r.allow_mma && fwht_mfma_covers(r);
     if (r.variant == fwht_mfma_name()) {
         supported(r.allow_mma, "'" + r.variant + "' needs the ALLOW_FP16_MMA arithmetic policy");
         supported(mfma, "'" + r.variant + "' covers packed FP16 rows of 2 to 4096 points only");
+        return make_fwht_mfma_executor(r);
     }
-    if (mfma && (r.variant.empty() || r.variant == fwht_mfma_name())) return make_fwht_mfma_executor(r);
     const Launch launch = r.fp16_final ? resident_launcher<F16Io>(r.log_n) : resident_launcher<F32Io>(r.log_n);
     require(launch != nullptr, "FWHT length has no launcher");
     PitchedLaunch pitched = nullptr;
@@ -1193,6 +1198,11 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
     if (r.allow_mma && !mfma)
         e->reason += "; ALLOW_FP16_MMA requested, but the MFMA Hadamard-block kernel covers packed rows of 2 to 4096 "
                      "points only: stage-ordered VALU kernel used";
+    else if (r.allow_mma && r.variant.empty())
+        e->reason += "; ALLOW_FP16_MMA requested: stage-ordered VALU kernel kept as the default (bit-exact, and "
+                     "faster than the MFMA Hadamard-block kernel on MI355X); " + fwht_mfma_name() +
+                     " is available by name or MEASURE, with a different accumulation order (up to one fp16 ulp "
+                     "from the stage-ordered result, beyond the 2e-3 bound where |y| >= 4)";
     return e;
 }
 
@@ -1202,7 +1212,7 @@ std::vector<std::string> fwht_candidates(const Request& r) {
     make_fwht_executor(v);  // the default lowering exists (throws NotSupported otherwise)
     std::vector<std::string> names;
     for (FwhtKind k : fwht_kinds(r)) names.push_back(FwhtExecutor::name(r, k));
-    if (r.allow_mma && fwht_mfma_covers(r)) names.insert(names.begin(), fwht_mfma_name());
+    if (r.allow_mma && fwht_mfma_covers(r)) names.push_back(fwht_mfma_name());
     return names;
 }
 

@@ -32,7 +32,17 @@
 // No LDS is used. Accumulation order differs from the radix-2 stage order of
 // the STRICT kernels, so results can differ from them by one fp16 ulp where a
 // value sits near a rounding boundary; this lowering is taken only when the
-// caller allows MFMA arithmetic.
+// caller names it (or MEASURE picks it) under the ALLOW_FP16_MMA policy.
+//
+// Rows stay independent. The block matrices I (x) H(2^t) hold zeros for the
+// element pairs of different rows (rows shorter than 16 points in the first
+// contraction, 32..128-point rows in the second), and on the matrix cores
+// inf * 0 and NaN * 0 are NaN, so one non-finite input would turn outputs of
+// its neighbouring rows into NaN (the hi / lo split would also turn an inf
+// into NaN, inf - inf). A wave whose tile holds any non-finite input
+// therefore runs the radix-2 stages on the VALU instead, in stage order, with
+// lane exchanges for the index bits held across lanes: every row of such a
+// tile is then bit-identical to the stage-ordered kernels and the oracle.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -71,6 +81,63 @@ __device__ __forceinline__ half4 hadamard_block(unsigned lane, int t) {
 // fp16 narrowing two separate roundings.
 __device__ __forceinline__ void opaque(float& x) { asm volatile("" : "+v"(x)); }
 
+// y = (x * norm) * scale rounded to fp32 twice, then one RNE narrowing, for
+// the four values of one 8-byte store.
+__device__ __forceinline__ unsigned short narrow(float x, float norm, float scale) {
+    float y = (x * norm) * scale;
+    opaque(y);
+    return __half_as_ushort(__float2half_rn(y));
+}
+
+// The tile's transform for a wave that holds a non-finite input: radix-2
+// stages over element bits 0 .. LOG_N - 1 in order, fp32, each pair (x at
+// the lower index, y at the upper) -> (x + y, x - y) as the oracle forms
+// them. Lane l holds a[i2][j] = element i2 * 256 + (l % 16) * 16 +
+// 4 (l / 16) + j: element bits 0-1 are register bits (j), bits 2-3 lane
+// bits 4-5, bits 4-7 lane bits 0-3, bits 8-11 register bits (i2). Results
+// leave in the input's own layout.
+template <int LOG_N>
+__device__ __forceinline__ void stage_ordered_tile(const half4 (&a)[16], unsigned lane, unsigned lane_bytes,
+                                                   __amdgpu_buffer_rsrc_t dst, float norm, float scale) {
+    using U2 = __attribute__((ext_vector_type(2))) unsigned;
+    float v[16][4];
+#pragma unroll
+    for (int i2 = 0; i2 < 16; ++i2)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[i2][j] = float(a[i2][j]);
+#pragma unroll
+    for (int b = 0; b < LOG_N; ++b) {
+        if (b < 2 || b >= 8) {  // both elements of a pair in this lane's registers
+            const int dj = b < 2 ? 1 << b : 0, di = b >= 8 ? 1 << (b - 8) : 0;
+#pragma unroll
+            for (int i2 = 0; i2 < 16; ++i2)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if ((i2 & di) || (j & dj)) continue;
+                    const float x = v[i2][j], y = v[i2 + di][j + dj];
+                    v[i2][j] = x + y;
+                    v[i2 + di][j + dj] = x - y;
+                }
+        } else {  // the partner lies in lane l ^ m; the upper lane keeps x - y
+            const int m = b < 4 ? 16 << (b - 2) : 1 << (b - 4);
+            const bool upper = (lane & unsigned(m)) != 0u;
+#pragma unroll
+            for (int i2 = 0; i2 < 16; ++i2)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float other = __shfl_xor(v[i2][j], m);
+                    v[i2][j] = upper ? other - v[i2][j] : v[i2][j] + other;
+                }
+        }
+    }
+#pragma unroll
+    for (int i2 = 0; i2 < 16; ++i2) {
+        const U2 packed = {unsigned(narrow(v[i2][0], norm, scale)) | (unsigned(narrow(v[i2][1], norm, scale)) << 16),
+                           unsigned(narrow(v[i2][2], norm, scale)) | (unsigned(narrow(v[i2][3], norm, scale)) << 16)};
+        __builtin_amdgcn_raw_buffer_store_b64(packed, dst, int(lane_bytes + 512u * unsigned(i2)), 0, 0);
+    }
+}
+
 template <int LOG_N>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void fwht_mfma_kernel(const __half* __restrict__ input,
                                                                         __half* output, std::uint64_t total,
@@ -101,6 +168,23 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void fwht_mfma_kernel(const __
     for (int i2 = 0; i2 < 16; ++i2) {
         const U2 raw = __builtin_amdgcn_raw_buffer_load_b64(src, int(lane_bytes + 512u * i2), 0, 0);
         a[i2] = __builtin_bit_cast(half4, raw);
+    }
+    // Any inf or NaN in the wave's tile (exponent field all ones): the
+    // stage-ordered VALU transform, so rows stay independent. The branch is
+    // wave-uniform.
+    unsigned special = 0u;
+#pragma unroll
+    for (int i2 = 0; i2 < 16; ++i2) {
+        const U2 raw = __builtin_bit_cast(U2, a[i2]);
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            special |= unsigned((raw[w] & 0x7c00u) == 0x7c00u);
+            special |= unsigned((raw[w] & 0x7c000000u) == 0x7c000000u);
+        }
+    }
+    if (__any(int(special))) {
+        stage_ordered_tile<LOG_N>(a, lane, lane_bytes, dst, norm, scale);
+        return;
     }
 
     float v[16][4];
@@ -150,11 +234,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void fwht_mfma_kernel(const __
     for (int k2 = 0; k2 < 16; ++k2) {
         unsigned short h[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float y = (v[k2][r] * norm) * scale;
-            opaque(y);
-            h[r] = __half_as_ushort(__float2half_rn(y));
-        }
+        for (int r = 0; r < 4; ++r) h[r] = narrow(v[k2][r], norm, scale);
         if constexpr (t1 > 0) {
             const U2 packed = {unsigned(h[0]) | (unsigned(h[1]) << 16), unsigned(h[2]) | (unsigned(h[3]) << 16)};
             __builtin_amdgcn_raw_buffer_store_b64(packed, dst, int(lane_bytes + 512u * k2), 0, 0);
@@ -198,7 +278,9 @@ class FwhtMfmaExecutor final : public Executor {
         algorithm = fwht_mfma_name();
         reason = "MFMA 16x16 Hadamard blocks (v_mfma_f32_16x16x16_f16, fp32 accumulation; fp32 intermediates enter "
                  "the second contraction as hi + lo fp16 parts), bits 8+ butterflied in registers; one 4096-element "
-                 "tile per wave, no LDS; accumulation order differs from the radix-2 stage order";
+                 "tile per wave, no LDS; accumulation order differs from the radix-2 stage order, so an output can "
+                 "differ from the stage-ordered result by one fp16 ulp (beyond 2e-3 where |y| >= 4); tiles holding "
+                 "inf or NaN run the stage-ordered radix-2 stages instead, keeping rows independent";
         const int t0 = r.log_n < 4 ? int(r.log_n) : 4;
         const int t1 = r.log_n <= 4 ? 0 : (r.log_n < 8 ? int(r.log_n) - 4 : 4);
         json::Writer w;

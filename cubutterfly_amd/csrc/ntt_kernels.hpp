@@ -757,7 +757,7 @@ void add_rows() {
 
 // The planner's split (l1 = split_l1): u32 with 16- and 32-column tiles,
 // u64 with 16 (32-column u64 tiles and other splits are instantiated by
-// ntt_alt_shapes.hip).
+// ntt_alt_u32.hip and ntt_alt_u64.hip).
 template <class W, bool LAZY, int LOG_N>
 void add_two_pass() {
     constexpr int l1 = split_l1(LOG_N), l2 = LOG_N - l1;
@@ -807,7 +807,7 @@ void register_alt_u32();
 void register_alt_u64();
 
 // Splits l1 of two-pass lengths with kernels: the planner's split_l1 and the
-// neighbouring ones that ntt_alt_shapes.hip instantiates.
+// neighbouring ones that ntt_alt_u32.hip and ntt_alt_u64.hip instantiate.
 constexpr bool alt_split(int log_n, int l1) {
     return log_n >= 15 && log_n <= 17 && (l1 == split_l1(log_n) - 1 || l1 == split_l1(log_n) + 1);
 }

@@ -108,7 +108,12 @@ typedef enum cubutterflyPlacement {
 
 /* ALLOW_FP16_MMA lets the FP16 FWHT use MFMA 16x16 Hadamard blocks, whose
  * accumulation order differs from the radix-2 stage order (reference
- * cubutterfly.h:86-90). */
+ * cubutterfly.h:86-90). The default lowering under it stays the bit-exact
+ * stage-ordered kernel; the MFMA lowering ("fwht-fp16-mfma16") is taken by
+ * name or by MEASURE. Unlike the reference, which admits the policy only for
+ * native-compute STAGE_STORAGE forward FWHTs (semantic_contract.cpp:204-210),
+ * this library admits it for the FP16 FWHTs it executes: FP32 compute with
+ * FINAL_STORAGE rounding, either direction and placement, any output scale. */
 typedef enum cubutterflyArithmeticPolicy {
     CUBUTTERFLY_ARITHMETIC_STRICT = 0,
     CUBUTTERFLY_ARITHMETIC_ALLOW_FP16_MMA = 1

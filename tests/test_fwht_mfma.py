@@ -1,12 +1,15 @@
-"""Selection of the MFMA Hadamard-block FP16 FWHT (no GPU needed): taken by
-default under ALLOW_FP16_MMA where it covers the request, never under STRICT,
-and a request it cannot cover names the VALU fallback in its selection reason
-(reference include/cubutterfly/cubutterfly.h:86-90)."""
+"""Selection of the MFMA Hadamard-block FP16 FWHT (no GPU needed). Under
+ALLOW_FP16_MMA the default stays the bit-exact stage-ordered VALU kernel (the
+reference keeps its native selection unless a calibrated MMA profile wins,
+src/mapping_selector.cpp:13-44); the MFMA kernel is taken by name and is a
+MEASURE candidate; STRICT never uses it (reference
+include/cubutterfly/cubutterfly.h:86-90)."""
 import pytest
 
 import cubutterfly_amd as cb
 
 MMA = cb.ArithmeticPolicy.ALLOW_FP16_MMA
+MFMA = "fwht-fp16-mfma16"
 
 
 def fp16(n, batch, policy=MMA, **kw):
@@ -16,21 +19,33 @@ def fp16(n, batch, policy=MMA, **kw):
 
 
 @pytest.mark.parametrize("n,batch", [(4096, 16384), (128, 524288), (2, 3), (16, 5), (512, 7)])
-def test_allow_mma_selects_the_mfma_kernel(lib, n, batch):
+def test_allow_mma_default_is_the_stage_ordered_kernel(lib, n, batch):
+    with cb.Plan(lib, fp16(n, batch, policy=cb.ArithmeticPolicy.STRICT)) as strict:
+        expected = strict.algorithm_name()
     with cb.Plan(lib, fp16(n, batch)) as plan:
-        assert plan.algorithm_name() == "fwht-fp16-mfma16"
+        assert plan.algorithm_name() == expected
+        assert plan.algorithm_name() != MFMA
+        reason = plan.selection_reason()
+        assert "stage-ordered VALU kernel kept as the default" in reason and MFMA in reason
+
+
+@pytest.mark.parametrize("n,batch", [(4096, 16384), (128, 524288), (2, 3), (16, 5), (512, 7)])
+def test_allow_mma_explicit_name_selects_the_mfma_kernel(lib, n, batch):
+    with cb.Plan(lib, fp16(n, batch), algorithm=MFMA) as plan:
+        assert plan.algorithm_name() == MFMA
         m = plan.mapping()
         assert m["lds_bytes"] == 0 and m["tile_elements"] == 4096
         assert m["tiles"] == -(-n * batch // 4096)
         assert m["mfma_per_tile"] == (48 if n > 16 else 16)
-        assert "MFMA" in plan.selection_reason()
+        reason = plan.selection_reason()
+        assert "MFMA" in reason and "one fp16 ulp" in reason and "inf or NaN" in reason
 
 
 def test_strict_never_uses_mfma(lib):
     with cb.Plan(lib, fp16(4096, 64, policy=cb.ArithmeticPolicy.STRICT)) as plan:
         assert plan.algorithm_name() == "fwht-fp16-fp32-resident-r32"
     with pytest.raises(cb.AbiError) as e:
-        cb.Plan(lib, fp16(4096, 64, policy=cb.ArithmeticPolicy.STRICT), algorithm="fwht-fp16-mfma16")
+        cb.Plan(lib, fp16(4096, 64, policy=cb.ArithmeticPolicy.STRICT), algorithm=MFMA)
     assert e.value.status == cb.Status.NOT_SUPPORTED and "ALLOW_FP16_MMA" in e.value.detail
 
 
@@ -49,5 +64,5 @@ def test_uncovered_requests_name_the_valu_fallback(lib):
         assert plan.algorithm_name().endswith("-pitched")
         assert "stage-ordered VALU kernel used" in plan.selection_reason()
     with pytest.raises(cb.AbiError) as e:
-        cb.Plan(lib, fp16(8192, 4), algorithm="fwht-fp16-mfma16")
+        cb.Plan(lib, fp16(8192, 4), algorithm=MFMA)
     assert e.value.status == cb.Status.NOT_SUPPORTED

@@ -99,14 +99,31 @@ def test_prepare_sweeps_the_candidates(torch_gpu, rlib, inverse):
     np.testing.assert_array_equal(to_host(torch_gpu, yd, np.uint64).reshape(limbs, n), expected)
 
 
-def reference_layout(log_n, negacyclic, inverse, in_rev, out_rev):
-    """Config and input of tests/test_rns_ntt.cu:113-162."""
+def wide_domain(log_n, negacyclic):
+    """The reference's large-modulus fixture (tests/test_rns_ntt.cu:856-867):
+    the first prime 2^62 + 1 + 8192 k, with the 7th power of its primitive
+    root of the transform's order as the explicit root. 4q exceeds the word,
+    so only fully reduced arithmetic applies."""
+    q = (1 << 62) + 1
+    while not oracle.is_prime(q):
+        q += 8192
+    root_bits = log_n + (1 if negacyclic else 0)
+    root = pow(oracle.find_primitive_root(root_bits, q), 7, q)
+    assert pow(root, 1 << root_bits, q) == 1 and pow(root, 1 << (root_bits - 1), q) == q - 1
+    return q, root
+
+
+def reference_layout(log_n, negacyclic, inverse, in_rev, out_rev, wide=False):
+    """Config and input of tests/test_rns_ntt.cu:113-162 (`wide`: domain 0
+    replaced by the large-modulus fixture, :856-868)."""
     n = 1 << log_n
     root_bits = log_n + (1 if negacyclic else 0)
     domains = []
     for d, q in enumerate(PRIMES):
         root = pow(oracle.find_primitive_root(root_bits, q), 3 if d == 0 else 5, q)
         domains.append((q, root))
+    if wide:
+        domains[0] = wide_domain(log_n, negacyclic)
     slots = [(1, 3, 5), (0, 0, 2), (0, 6, 0), (1, 2, 6), (0, 5, 3)]  # (domain, input slot, output slot)
     polys = [{"domain": d, "input_offset": i * (n + 17) + 11, "output_offset": o * (n + 17) + 11}
              for d, i, o in slots]
@@ -149,6 +166,27 @@ def test_reference_layout(torch_gpu, rlib, log_n, negacyclic, inverse, in_rev, o
     cfg, domains, polys, data = reference_layout(log_n, negacyclic, inverse, in_rev, out_rev)
     got, _ = run(torch_gpu, rlib, cfg, data, data.size, in_place, torch_gpu.cuda.Stream())
     np.testing.assert_array_equal(got, expected_layout(cfg, domains, polys, data, in_place))
+
+
+# The reference's further cases (tests/test_rns_ntt.cu:853-868): log n 18
+# (cyclic forward, natural -> bit-reversed), log n 20 (negacyclic inverse,
+# bit-reversed -> natural) and the large-modulus domain at log n 12, through
+# the RNS plan in both placements.
+EDGE_CASES = [(18, False, False, False, True, False), (20, True, True, True, False, False),
+              (12, True, True, True, False, True)]
+
+
+@pytest.mark.parametrize("log_n,negacyclic,inverse,in_rev,out_rev,wide", EDGE_CASES)
+@pytest.mark.parametrize("in_place", [False, True])
+def test_reference_edge_cases(torch_gpu, rlib, log_n, negacyclic, inverse, in_rev, out_rev, wide, in_place):
+    print(f"case rns edge log_n={log_n} neg={negacyclic} inv={inverse} in_rev={in_rev} out_rev={out_rev} "
+          f"wide={wide} in_place={in_place}", flush=True)
+    cfg, domains, polys, data = reference_layout(log_n, negacyclic, inverse, in_rev, out_rev, wide)
+    got, info = run(torch_gpu, rlib, cfg, data, data.size, in_place, torch_gpu.cuda.Stream())
+    np.testing.assert_array_equal(got, expected_layout(cfg, domains, polys, data, in_place))
+    if wide:  # 4q > 2^64: no lazy candidate
+        assert domains[0][0] > 1 << 62
+        assert all(c["mapping"].startswith("strict") for c in info["candidates"])
 
 
 def test_graph_replay_matches_eager(torch_gpu, rlib):

@@ -115,7 +115,7 @@ def ntt_words(log_n, batch, bits, inverse):
 
 
 @pytest.mark.parametrize("bits", [32, 64])
-@pytest.mark.parametrize("log_n", [10, 13, 14, 15, 16, 17])
+@pytest.mark.parametrize("log_n", [10, 13, 14, 15, 16, 17, 18, 20])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_every_ntt_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path, bits, log_n, inverse):
     print(f"case ntt candidates u{bits} log_n={log_n} inverse={inverse}", flush=True)

@@ -29,19 +29,30 @@ def fft(log_n, batch):
 
 
 def both(torch, lib, stream, desc, host, dtype):
-    """(Execute output, ExecuteNoAlloc output) of one plan on `host`."""
+    """(Execute output, ExecuteNoAlloc output) of one plan on `host`; the
+    outputs are sized by the plan (the zero-extended embedding changes it)."""
     x = to_device(torch, host)
     with cb.Plan(lib, desc, stream=stream) as plan:
         ws_bytes = plan.workspace_size()
         assert 0 < ws_bytes <= LIMIT
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
         plan.set_workspace(ws, ws_bytes)
-        y_bound = torch.full_like(x, -1)
+        assert plan.input_size() == x.numel() * x.element_size()
+        out_elems = plan.output_size() // x.element_size()
+        y_bound = torch.full((out_elems,), -1, dtype=x.dtype, device="cuda")
         plan.execute(x, y_bound)
-        y_static = torch.full_like(x, -1)
+        y_static = torch.full((out_elems,), -1, dtype=x.dtype, device="cuda")
         lib("ExecuteNoAlloc", plan.context, plan.handle, x.data_ptr(), y_static.data_ptr())
         torch.cuda.synchronize()
     return to_host(torch, y_bound, dtype), to_host(torch, y_static, dtype)
+
+
+def fill_scratch(torch, lib, stream):
+    """C2's forward through ExecuteNoAlloc: leaves 16 MiB of non-zero
+    intermediate words in the shared array for the next plan to find."""
+    host = workloads.ntt_input(16, 64, Q30, seed=11).astype(np.uint32)
+    bound, static = both(torch, lib, stream, ntt(16, 64), host, np.uint32)
+    np.testing.assert_array_equal(static, bound)
 
 
 def test_header_states_the_limit():
@@ -88,3 +99,40 @@ def test_plans_without_workspace_and_oversized_plans(torch_gpu, lib, stream):
     with cb.Plan(lib, ntt(16, 2), stream=stream) as plan:
         status = lib.fn("ExecuteNoAlloc")(plan.context, plan.handle, ct.c_void_p(0x1000), ct.c_void_p(0x1000))
         assert status == cb.Status.INVALID_VALUE
+
+
+def test_composite_embedding_and_boundary_plans_after_a_larger_plan(torch_gpu, lib, stream):
+    # Rank-2 FFT (row plan, transposes, workspace ping-pong buffers), the
+    # zero-extended embedding (gather with zero fill, padded transform) and a
+    # strided boundary plan, each run right after a larger plan filled the
+    # shared array with non-zero data: no plan may read a word it did not
+    # write first, so both entry points agree bit for bit.
+    rng = np.random.default_rng(5)
+    cases = [
+        ("rank-2 fft 64 x 2^15", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64, 1 << 15],
+                                            compute=cb.ComputeType.FP32, batch=1), (64 << 15,), np.complex64),
+        ("rank-2 fft 64 x 128, batch 2", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64, 128],
+                                              compute=cb.ComputeType.FP32, batch=2), (2 * 64 * 128,), np.complex64),
+        ("zero-extended fft 3000 x 4", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [3000],
+                                                  compute=cb.ComputeType.FP32, batch=4,
+                                                  length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING),
+         (4 * 3000,), np.complex64),
+        ("zero-extended fwht 1000 x 5", cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1000],
+                                                   compute=cb.ComputeType.FP32, batch=5,
+                                                   length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING),
+         (5 * 1000,), np.float32),
+        ("strided fwht 2^12 x 8, rows interleaved", cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [4096],
+                                                               compute=cb.ComputeType.FP32, batch=8,
+                                                               input_strides=[8], input_batch_stride=1),
+         (8 * 4096,), np.float32),
+    ]
+    for name, desc, shape, dtype in cases:
+        print(f"case no-alloc {name} after C2's forward", flush=True)
+        fill_scratch(torch_gpu, lib, stream)
+        if dtype == np.complex64:
+            host = (rng.standard_normal(shape) + 1j * rng.standard_normal(shape)).astype(np.complex64)
+        else:
+            host = rng.standard_normal(shape).astype(np.float32)
+        bound, static = both(torch_gpu, lib, stream, desc, host, dtype)
+        width = np.uint64 if dtype == np.complex64 else np.uint32
+        np.testing.assert_array_equal(static.view(width), bound.view(width), err_msg=name)
