@@ -239,8 +239,11 @@ RnsLowering lower(const RnsConfig& config, const RnsMapping& m, bool same_offset
 std::vector<RnsMapping> candidates(const RnsConfig& c) {
     std::uint64_t max_q = 0;
     for (const auto& d : c.domains) max_q = std::max(max_q, d.modulus);
-    std::vector<bool> arithmetic{false};
-    if (max_q < (std::uint64_t{1} << 62)) arithmetic.push_back(true);  // lazy fits: strict is a second choice
+    // Lazy butterflies need 4q below the word: where they fit they are the
+    // static plan and fully reduced ones a second choice; a modulus of 2^62
+    // or more leaves only the fully reduced ones.
+    std::vector<bool> arithmetic{true};
+    if (max_q < (std::uint64_t{1} << 62)) arithmetic = {false, true};
     std::vector<RnsMapping> out;
     for (const bool strict : arithmetic) {
         out.push_back({strict, false, 0});
@@ -525,7 +528,7 @@ int cubutterflyRnsCreate(const char* config_json_text, cubutterflyRnsPlan* resul
                                          [](const cbw::NttPolynomial& p) { return p.input_offset == p.output_offset; });
         // The static plan until Prepare selects (private scratch allocated
         // here, outside execution; reference :286-366).
-        plan->select(lower(plan->config, RnsMapping{}, plan->same_offsets));
+        plan->select(lower(plan->config, candidates(plan->config).front(), plan->same_offsets));
         *result = plan.release();
     });
 }

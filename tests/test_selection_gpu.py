@@ -104,18 +104,27 @@ def test_every_fft_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path
         fft_ok(torch_gpu, lib, t, stream, log_n, batch, inverse, **opts)
 
 
-QDEF = 1152921504606584833  # include/cuntt/ntt.hpp:17
+QDEF = 1152921504606584833  # include/cuntt/ntt.hpp:17; 2^18 | q - 1
+Q2_21 = 1152921504577486849  # tests/test_rns_ntt.cu:19; 2^21 | q - 1 (negacyclic up to 2^20 points)
+
+
+def modulus(bits, log_n):
+    return Q30 if bits == 32 else QDEF if log_n <= 17 else Q2_21
 
 
 def ntt_words(log_n, batch, bits, inverse):
     if bits == 32:
         return ntt(log_n, batch, inverse)
     return cb.describe(cb.Operator.NTT, cb.DataType.UINT64, [1 << log_n], compute=cb.ComputeType.UINT64, batch=batch,
-                       modulus=QDEF, word_bits=64, ntt_ring=cb.NttRing.NEGACYCLIC, inverse=inverse)
+                       modulus=modulus(bits, log_n), word_bits=64, ntt_ring=cb.NttRing.NEGACYCLIC, inverse=inverse)
 
 
-@pytest.mark.parametrize("bits", [32, 64])
-@pytest.mark.parametrize("log_n", [10, 13, 14, 15, 16, 17, 18, 20])
+# u64 adds 2^18 and 2^20, where its 32-column tiles are MEASURE candidates
+# (the 30-bit u32 modulus has no 2^19-th roots of unity).
+NTT_CANDIDATE_CASES = [(b, l) for b in (32, 64) for l in (10, 13, 14, 15, 16, 17)] + [(64, 18), (64, 20)]
+
+
+@pytest.mark.parametrize("bits,log_n", NTT_CANDIDATE_CASES)
 @pytest.mark.parametrize("inverse", [False, True])
 def test_every_ntt_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path, bits, log_n, inverse):
     print(f"case ntt candidates u{bits} log_n={log_n} inverse={inverse}", flush=True)
@@ -135,7 +144,7 @@ def test_every_ntt_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path
     if 15 <= log_n <= 17:
         expected += [f"{base}-h{l1 - 1}", f"{base}-h{l1 + 1}"]
     assert names == expected
-    q = Q30 if bits == 32 else QDEF
+    q = modulus(bits, log_n)
     rng = np.random.default_rng(log_n)
     words = np.uint32 if bits == 32 else np.uint64
     x = rng.integers(0, np.iinfo(words).max, (batch, 1 << log_n), dtype=np.uint64, endpoint=True).astype(words)

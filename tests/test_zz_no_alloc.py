@@ -109,8 +109,8 @@ def test_composite_embedding_and_boundary_plans_after_a_larger_plan(torch_gpu, l
     # write first, so both entry points agree bit for bit.
     rng = np.random.default_rng(5)
     cases = [
-        ("rank-2 fft 64 x 2^15", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64, 1 << 15],
-                                            compute=cb.ComputeType.FP32, batch=1), (64 << 15,), np.complex64),
+        ("rank-2 fft 64 x 2^13", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64, 1 << 13],
+                                            compute=cb.ComputeType.FP32, batch=1), (64 << 13,), np.complex64),
         ("rank-2 fft 64 x 128, batch 2", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64, 128],
                                               compute=cb.ComputeType.FP32, batch=2), (2 * 64 * 128,), np.complex64),
         ("zero-extended fft 3000 x 4", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [3000],
