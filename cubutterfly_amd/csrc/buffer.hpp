@@ -34,6 +34,15 @@ __device__ __forceinline__ T buffer_load(__amdgpu_buffer_rsrc_t r, std::uint32_t
 }
 
 // AUX: the instruction's cache-policy bits. T is a 4-, 8- or 16-byte type.
+//
+// A buffer store of more than 8 bytes needs one wait state before an
+// instruction that overwrites its data VGPRs; the GCN rule the compiler
+// follows exempts stores whose scalar offset is an SGPR, so for those it
+// emits none (`buffer_store_dwordx4 v[4:7], v30, s[0:3], s8 offen` directly
+// followed by `v_mul_f32 v7, ...`). On gfx950 such stores wrote overwritten
+// values: wrong results, no fault. 16-byte stores therefore carry their
+// scalar part in the lane offset (the scalar operand is the constant 0, and
+// the compiler keeps the wait state); 4- and 8-byte stores are not affected.
 template <class T, int AUX = 0>
 __device__ __forceinline__ void buffer_store(T x, __amdgpu_buffer_rsrc_t r, std::uint32_t byte_off,
                                              std::uint32_t scalar_off = 0) {
@@ -43,8 +52,8 @@ __device__ __forceinline__ void buffer_store(T x, __amdgpu_buffer_rsrc_t r, std:
                                               static_cast<int>(scalar_off), AUX);
     } else if constexpr (sizeof(T) == 16) {
         using V4 = __attribute__((ext_vector_type(4))) std::uint32_t;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(V4, x), r, static_cast<int>(byte_off),
-                                               static_cast<int>(scalar_off), AUX);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(V4, x), r, static_cast<int>(byte_off + scalar_off),
+                                               0, AUX);
     } else {
         using V2 = __attribute__((ext_vector_type(2))) std::uint32_t;
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(V2, x), r, static_cast<int>(byte_off),
