@@ -12,10 +12,14 @@
 // memory.
 //
 // Twiddles: a radix-16 phase of the merged-twist transform needs, per thread,
-// the 15 (or fewer) table entries of one block of the stage tree. The host
-// lays those entries out contiguously per block ("chunks", in stage execution
-// order, padded to 16 bytes), so a thread fetches its phase twiddles with a
-// few 16-byte loads from one address.
+// the 15 (or fewer) table entries of one block of the stage tree (its
+// "chunk", in stage execution order, padded to whole 16-byte pieces). A
+// phase's chunks are stored piece-major: piece e of every chunk of the phase,
+// in chunk order, then piece e + 1. Threads that hold consecutive chunks
+// (the lanes of a row pass, where every lane has its own block) then read
+// piece e as one contiguous run per load instruction -- 1 KiB over 8 cache
+// lines for a wave -- instead of 64 pieces one chunk apart (64 or more lines
+// per instruction, which filled the address unit's queue).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -116,13 +120,19 @@ constexpr int chunk_stride(int lt, bool ct, bool last, int p, int pair_bytes) {
     const int e = chunk_entries(lt, ct, last, p);
     return (e + per16 - 1) / per16 * per16;
 }
+// Chunks of one phase: one per block of the stage tree at chunk_shift,
+// over the 2^(prefix_bits + lt) entries the pass covers.
+constexpr std::uint64_t chunk_count(int lt, int prefix_bits, bool ct, int p) {
+    return (std::uint64_t{1} << (prefix_bits + lt)) >> chunk_shift(lt, ct, p);
+}
 
-// Appends one pass's twiddle chunks (layout above) to `out` and
+// Appends one pass's twiddle chunks (piece-major, layout above) to `out` and
 // records each phase's offset from `base`. prefix_bits: 0 for column and
 // one-pass tiles, l1 for row tiles (their block index carries 2^l1 + row).
 template <class W>
 void append_pass_chunks(std::vector<TwPair<W>>& out, std::size_t base, const std::vector<TwPair<W>>& table, int lt,
                         int prefix_bits, bool ct, bool last, std::uint32_t (&phase_off)[3]) {
+    constexpr std::size_t per16 = 16 / sizeof(TwPair<W>) > 0 ? 16 / sizeof(TwPair<W>) : 1;
     for (int p = 0; p < num_phases(lt); ++p) {
         phase_off[p] = static_cast<std::uint32_t>(out.size() - base);
         const int entries = chunk_entries(lt, ct, last, p);
@@ -130,17 +140,21 @@ void append_pass_chunks(std::vector<TwPair<W>>& out, std::size_t base, const std
         const int shift = chunk_shift(lt, ct, p);
         const int stride = chunk_stride(lt, ct, last, p, int(sizeof(TwPair<W>)));
         const int ws = window_start(lt, ct, p);
-        const std::uint64_t first = (std::uint64_t{1} << (prefix_bits + lt)) >> shift;
-        for (std::uint64_t idx = first; idx < 2 * first; ++idx) {
-            std::vector<TwPair<W>> chunk(std::size_t(stride), TwPair<W>{W(0), W(0)});
-            int e = 0;
+        const std::uint64_t count = chunk_count(lt, prefix_bits, ct, p);
+        const std::size_t start = out.size();
+        out.resize(start + std::size_t(count) * std::size_t(stride), TwPair<W>{W(0), W(0)});
+        for (std::uint64_t c = 0; c < count; ++c) {
+            const std::uint64_t idx = count + c;  // block index in the stage tree
+            std::size_t e = 0;
             for (int s = 0; s < active_stages(lt, ct, p); ++s) {
                 const int k = exec_stage(lt, ct, p, s);
                 if (scale_stage(lt, ct, last, k)) continue;
-                for (int j = 0; j < stage_count(lt, ws, k); ++j)
-                    chunk[std::size_t(e++)] = table.at((idx << (shift - k - 1)) + std::uint64_t(j));
+                for (int j = 0; j < stage_count(lt, ws, k); ++j, ++e) {
+                    const std::size_t piece = e / per16, slot = e % per16;
+                    out[start + (piece * std::size_t(count) + std::size_t(c)) * per16 + slot] =
+                        table.at((idx << (shift - k - 1)) + std::uint64_t(j));
+                }
             }
-            out.insert(out.end(), chunk.begin(), chunk.end());
         }
     }
 }
@@ -227,6 +241,10 @@ __device__ __forceinline__ void gs_scale_butterfly(W& x, W& y, const DeviceDomai
 }
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Orders one wave's LDS accesses around an exchange that stays inside the
+// wave: a wave's LDS instructions execute in issue order, so only the
+// compiler has to be kept from moving reads above writes (no code).
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("" ::: "memory"); }
 
 __device__ __forceinline__ std::uint32_t brev(std::uint32_t x, std::uint32_t bits) {
     return bits ? __brev(x) >> (32 - bits) : 0u;
@@ -298,6 +316,14 @@ struct Pass {
     // (Nontemporal final stores measured slower for C4, whose bit-reversed
     // output lands in 8-byte segments: 60.6 -> 71-73 us.)
     static constexpr int kStoreAux = (!CT && !SINGLE) ? 17 : 0;
+    // Row tiles of at most 2^10-point rows: every phase layout keeps a row in
+    // 2^(LT-4) <= 64 consecutive threads (phase_index puts the row bits at
+    // t >> (LT - 4)), so the register-window exchanges never leave a wave.
+    // Their barriers would only hold the workgroup's waves in step; a wave
+    // that has its data computes while the others still wait for theirs.
+    // The staged boundary permutations (PIN / POUT) mix rows across waves
+    // and keep their barriers.
+    static constexpr bool kWaveLocal = !COL && LT - kLE <= 6;
     static_assert(SINGLE ? (L1 == 0 && L2 == LT) : (COL ? LT == L1 : LT == L2), "pass bits");
     static_assert(LT >= 1 && LB >= kLE && LB <= 13, "tile shape");
 
@@ -471,12 +497,15 @@ struct Pass {
     static __device__ __forceinline__ void load_chunk(Chunk<P>& c, const PassArgs<W>& a, const Tile& tl,
                                                       std::uint32_t t, __amdgpu_buffer_rsrc_t tw) {
         if constexpr (P < kPhases) {
-            constexpr int stride = chunk_stride(LT, CT, kLast, P, int(sizeof(TwPair<W>)));
-            const std::uint32_t base = (a.phase_off[P] + chunk_index<P>(tl, t) * std::uint32_t(stride)) *
-                                       std::uint32_t(sizeof(TwPair<W>));
+            // Piece e of chunk c sits at (e * count + c) * 16 bytes from the
+            // phase's table: the per-piece step is a compile-time constant
+            // (scalar offset), the chunk a lane offset.
+            constexpr std::uint32_t step = 16u * std::uint32_t(chunk_count(LT, (COL || SINGLE) ? 0 : L1, CT, P));
+            const std::uint32_t base =
+                a.phase_off[P] * std::uint32_t(sizeof(TwPair<W>)) + 16u * chunk_index<P>(tl, t);
 #pragma unroll
             for (int e = 0; e < chunk_loads<P>(); ++e)
-                c.raw[e] = __builtin_amdgcn_raw_buffer_load_b128(tw, int(base + 16u * e), 0, 0);
+                c.raw[e] = __builtin_amdgcn_raw_buffer_load_b128(tw, int(base), int(step * std::uint32_t(e)), 0);
         }
     }
 
@@ -526,11 +555,13 @@ struct Pass {
     // phase's chunk up front kept them all live and cost occupancy).
     template <int FROM, int TO, class Between>
     static __device__ __forceinline__ void exchange(W (&v)[kE], W* lds, std::uint32_t t, Between&& between) {
-        lds_barrier();
+        if constexpr (kWaveLocal) wave_lds_fence();
+        else lds_barrier();
 #pragma unroll
         for (int r = 0; r < kE; ++r) lds[L::template at<FROM>(t, r)] = v[r];
         between();
-        lds_barrier();
+        if constexpr (kWaveLocal) wave_lds_fence();
+        else lds_barrier();
 #pragma unroll
         for (int r = 0; r < kE; ++r) v[r] = lds[L::template at<TO>(t, r)];
     }
