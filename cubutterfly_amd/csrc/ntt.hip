@@ -15,6 +15,9 @@
 // J. Symb. Comp. 2014): result in [0, 2q) for any word a. With 4q below the
 // word size ("lazy"), forward values live in [0, 4q) and inverse values in
 // [0, 2q); otherwise every butterfly keeps [0, 2q). Outputs are canonical.
+// A Barrett variant (`-barrett`, moduli below 2^(k-2)) keeps canonical values
+// and multiplies by bare twiddles with one constant per modulus (see
+// ntt_kernels.hpp), so its tables hold one word per entry instead of a pair.
 #include <hip/hip_runtime.h>
 
 #include "json.hpp"
@@ -48,6 +51,8 @@ void ensure_registered() {
         register_u32_strict();
         register_u64_lazy();
         register_u64_strict();
+        register_u32_barrett();
+        register_u64_barrett();
         register_alt_u32();
         register_alt_u64();
         return true;
@@ -105,6 +110,7 @@ template <class W>
 struct EngineImplT {
     NttEngineConfig cfg;
     bool lazy = false;
+    int arith = kStrict;
     std::uint32_t l1 = 0, l2 = 0;
     DeviceBuffer tables, domains, poly_domain, in_off, out_off;
     struct Launch {
@@ -124,7 +130,10 @@ struct EngineImplT {
         const unsigned bits = sizeof(W) * 8;
         std::uint64_t max_q = 0;
         for (const auto& d : c.domains) max_q = std::max(max_q, d.modulus);
-        lazy = !c.force_strict && max_q < (std::uint64_t{1} << (bits - 2));
+        lazy = !c.force_strict && !c.barrett && max_q < (std::uint64_t{1} << (bits - 2));
+        supported(!c.barrett || max_q < (std::uint64_t{1} << (bits - 2)),
+                  "Barrett arithmetic needs every modulus below 2^" + std::to_string(bits - 2));
+        arith = c.barrett ? kBarrett : lazy ? kLazy : kStrict;
         const std::uint64_t polys = c.polynomials.empty() ? c.batch : c.polynomials.size();
         require(polys >= 1 && polys <= 0xffffffffull, "NTT batch must be in [1, 2^32)");
         const bool offsets = !c.polynomials.empty();
@@ -159,7 +168,7 @@ struct EngineImplT {
             const std::uint64_t per_tile = std::uint64_t{1} << li;
             const std::uint64_t tiles = (polys + per_tile - 1) / per_tile;
             Launch L{};
-            L.fn = find_pass<W>(PassKey{lazy, int(log_n), int(log_n), li, false, ct, perm_in, perm_out, true});
+            L.fn = find_pass<W>(PassKey{arith, int(log_n), int(log_n), li, false, ct, perm_in, perm_out, true});
             L.grid = unsigned(tiles);
             L.args = base;
             L.args.tiles = unsigned(tiles);
@@ -199,9 +208,9 @@ struct EngineImplT {
             B.prefix_bits = int(l1);
             B.last = ct;
             A.fn = find_pass<W>(
-                PassKey{lazy, int(log_n), int(l1), col_li, true, ct, ct && perm_in, !ct && perm_out, false});
+                PassKey{arith, int(log_n), int(l1), col_li, true, ct, ct && perm_in, !ct && perm_out, false});
             B.fn = find_pass<W>(
-                PassKey{lazy, int(log_n), int(l2), rli, false, ct, !ct && perm_in, ct && perm_out, false});
+                PassKey{arith, int(log_n), int(l2), rli, false, ct, !ct && perm_in, ct && perm_out, false});
             if (ct) {  // forward: A reads the input, B writes the output
                 A.args.in_off = in_off.as<std::uint64_t>();
                 A.args.reduce_input = c.reduce_input;
@@ -223,12 +232,19 @@ struct EngineImplT {
         }
         // Device domain records and their twiddle chunks (one layout for all
         // domains, so the phase offsets are shared).
+        if (arith == kBarrett) build_tables<W>(c, n, ct);
+        else build_tables<TwPair<W>>(c, n, ct);
+    }
+
+    // Entry E: a Shoup pair, or the bare twiddle word (Barrett).
+    template <class E>
+    void build_tables(const NttEngineConfig& c, std::uint64_t n, bool ct) {
         std::vector<DeviceDomain<W>> host_domains;
-        std::vector<TwPair<W>> all_tables;
+        std::vector<E> all_tables;
         for (const auto& d : c.domains) {
             const std::uint64_t q = d.modulus;
             const std::uint64_t root = c.inverse ? invmod(d.root, q) : d.root;
-            auto table = make_table<W>(log_n, q, root, c.negacyclic);
+            const auto pairs = make_table<W>(c.log_n, q, root, c.negacyclic);
             DeviceDomain<W> dd{};
             dd.q = W(q);
             dd.q2 = W(2 * q);
@@ -236,24 +252,36 @@ struct EngineImplT {
             dd.rwp = shoup_factor<W>(1, q);
             const std::uint64_t ninv = invmod(n % q, q);
             dd.ninv = {W(ninv), shoup_factor<W>(ninv, q)};
-            const std::uint64_t last = mulmod(table[1].w, ninv, q);
+            const std::uint64_t last = mulmod(pairs[1].w, ninv, q);
             dd.last = {W(last), shoup_factor<W>(last, q)};
-            if (ct && lazy)  // lazy Cooley-Tukey butterflies take -w (ct_butterfly)
-                for (auto& e : table) e.w = W(0) - e.w;
+            unsigned qbits = 0;
+            while (qbits < 64 && (q >> qbits) != 0) ++qbits;
+            dd.qbits = qbits;
+            // mu = floor(2^(2b+1) / q) < 2^(b+2) fits the word for q < 2^(k-2).
+            dd.mu = qbits + 2 <= sizeof(W) * 8 ? W((u128{1} << (2 * qbits + 1)) / q) : W(0);
+            std::vector<E> table(pairs.size());
+            for (std::size_t k = 0; k < pairs.size(); ++k) {
+                if constexpr (std::is_same_v<E, W>) {
+                    table[k] = pairs[k].w;
+                } else {
+                    table[k] = pairs[k];
+                    if (ct && lazy) table[k].w = W(0) - table[k].w;  // lazy Cooley-Tukey butterflies take -w
+                }
+            }
             dd.tw = all_tables.size();
             for (auto& L : launches)
-                append_pass_chunks<W>(all_tables, std::size_t(dd.tw), table, L.lt, L.prefix_bits, ct, L.last,
+                append_pass_chunks<E>(all_tables, std::size_t(dd.tw), table, L.lt, L.prefix_bits, ct, L.last,
                                       L.args.phase_off);
             host_domains.push_back(dd);
         }
-        require(all_tables.size() * sizeof(TwPair<W>) < 0x7fffffffull, "NTT twiddle tables exceed 2 GiB");
+        require(all_tables.size() * sizeof(E) < 0x7fffffffull, "NTT twiddle tables exceed 2 GiB");
         tables.upload(all_tables);
         domains.upload(host_domains);
         const std::size_t per_domain = all_tables.size() / c.domains.size();
         for (auto& L : launches) {
-            L.args.tw_bytes = static_cast<std::uint32_t>(per_domain * sizeof(TwPair<W>));
+            L.args.tw_bytes = static_cast<std::uint32_t>(per_domain * sizeof(E));
             L.args.domains = domains.as<DeviceDomain<W>>();
-            L.args.tw = tables.as<TwPair<W>>();
+            L.args.tw = tables.as<E>();
             L.args.poly_domain = poly_domain.as<std::uint32_t>();
         }
     }
@@ -301,6 +329,7 @@ NttEngine::NttEngine(const NttEngineConfig& c) : impl_(new Impl) {
     const bool other_split = two && c.split_high && c.split_high != std::uint32_t(split_l1(int(c.log_n)));
     algorithm_ = std::string("ntt-u") + std::to_string(c.word_bits) + (c.negacyclic ? "-negacyclic" : "-cyclic") +
                  (two ? "-two-pass-r16" : "-resident-r16") + (c.force_strict ? "-strict" : "") +
+                 (c.barrett ? "-barrett" : "") +
                  (two && c.wide_columns ? "-c32" : "") +
                  (other_split ? "-h" + std::to_string(c.split_high) : "");
     json::Writer w;
@@ -314,7 +343,7 @@ NttEngine::NttEngine(const NttEngineConfig& c) : impl_(new Impl) {
         .field("direction", c.inverse ? "inverse" : "forward")
         .field("input_order", c.input_bit_reversed ? "bit_reversed" : "natural")
         .field("output_order", c.output_bit_reversed ? "bit_reversed" : "natural")
-        .field("arithmetic", "shoup")
+        .field("arithmetic", c.barrett ? "barrett" : "shoup")
         .field("lazy_reduction", impl_->u32 ? impl_->u32->lazy : impl_->u64->lazy)
         .key("shape")
         .value_raw(impl_->u32 ? impl_->u32->json_shape : impl_->u64->json_shape)
@@ -409,6 +438,7 @@ class NttExecutor final : public Executor {
         supported(r.variant.empty() || std::find(names.begin(), names.end(), r.variant) != names.end(),
                   "'" + r.variant + "' is not a lowering of this NTT (available: " + join(names) + ")");
         c.force_strict = r.variant == default_name(r) + "-strict" + suffix;
+        c.barrett = r.variant == default_name(r) + "-barrett" + suffix;
         c.wide_columns = r.variant.empty() ? wide_columns_default(r) : r.variant == default_name(r) + "-c32" + suffix;
         for (const std::uint32_t h : other_splits(r))
             if (r.variant == default_name(r) + "-h" + std::to_string(h) + suffix) c.split_high = h;
@@ -419,6 +449,7 @@ class NttExecutor final : public Executor {
                      ? "whole polynomials resident in one workgroup (radix-16 register windows, LDS exchange)"
                      : "two passes over high/low index bits (coalesced column and row tiles), merged-twist "
                        "Cooley-Tukey / Gentleman-Sande with Shoup arithmetic";
+        if (c.barrett) reason += "; Barrett products (one constant per modulus, single-word twiddle tables)";
     }
     std::size_t workspace_bytes() const override { return engine_->workspace_bytes(); }
     void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
@@ -447,6 +478,7 @@ std::vector<std::string> ntt_candidates(const Request& r) {
         if (wide_columns_default(r)) std::rotate(names.begin(), names.end() - 1, names.end());  // the default first
     }
     for (const std::uint32_t h : other_splits(r)) names.push_back(default_name(r) + "-h" + std::to_string(h) + suffix);
+    if (r.modulus < (std::uint64_t{1} << (r.word_bits - 2))) names.push_back(default_name(r) + "-barrett" + suffix);
     return names;
 }
 

@@ -44,6 +44,7 @@ struct NttEngineConfig {
     bool output_bit_reversed = false;
     bool reduce_input = true;  // reduce arbitrary words mod q on load
     bool force_strict = false; // fully reduced butterflies even where lazy ones fit
+    bool barrett = false;      // Barrett products on canonical values (moduli below 2^(word bits - 2))
     bool wide_columns = false; // two-pass: 32-column tiles in the column pass (`-c32`)
     std::uint32_t split_high = 0;  // two-pass: high (column-pass) bits; 0 = the planner's split (`-h<l1>`)
     std::vector<NttDomain> domains;

@@ -30,6 +30,7 @@
 #include <cstddef>
 #include <map>
 #include <tuple>
+#include <type_traits>
 #include <vector>
 
 namespace cbw {
@@ -45,12 +46,24 @@ struct alignas(2 * sizeof(W)) TwPair {
     W w, wp;
 };
 
+// Arithmetic of a pass: Shoup products on fully reduced values ([0, 2q)
+// between stages), Shoup products on lazy ranges, or Barrett products on
+// canonical values with one constant per domain instead of a Shoup factor per
+// twiddle (tables of single words).
+constexpr int kStrict = 0, kLazy = 1, kBarrett = 2;
+
+// A twiddle table entry: a Shoup pair, or the bare twiddle for Barrett.
+template <class W, int AR>
+using Entry = std::conditional_t<AR == kBarrett, W, TwPair<W>>;
+
 template <class W>
 struct DeviceDomain {
     W q, q2, nq, rwp;     // modulus, 2q, -q mod 2^k, floor(2^k / q) (Shoup factor of 1)
     TwPair<W> ninv;       // n^-1 with its Shoup factor
     TwPair<W> last;       // Tinv[1] * n^-1 (final inverse stage)
-    std::uint64_t tw;     // offset of this domain's chunk tables in PassArgs::tw (TwPairs)
+    W mu;                 // Barrett: floor(2^(2b+1) / q), b = qbits
+    std::uint32_t qbits;  // Barrett: bit length of q
+    std::uint64_t tw;     // offset of this domain's chunk tables in PassArgs::tw (entries)
 };
 
 template <class W>
@@ -58,13 +71,13 @@ struct PassArgs {
     const W* in;
     W* out;
     const DeviceDomain<W>* domains;
-    const TwPair<W>* tw;               // all domains' chunk tables, concatenated
+    const void* tw;                    // all domains' chunk tables (Entry), concatenated
     const std::uint32_t* poly_domain;  // per polynomial (null: domain 0)
     const std::uint64_t* in_off;       // per polynomial word offset (null: p << log n)
     const std::uint64_t* out_off;
     std::uint32_t polys, tiles;
     std::uint32_t reduce_input;
-    std::uint32_t phase_off[3];  // chunk array of each phase, TwPairs from the domain's table start
+    std::uint32_t phase_off[3];  // chunk array of each phase, entries from the domain's table start
     std::uint32_t tw_bytes;      // bytes of one domain's chunk tables (buffer range of the twiddle reads)
 };
 
@@ -114,9 +127,9 @@ constexpr int chunk_offset(int lt, bool ct, bool last, int p, int s) {
 constexpr int chunk_entries(int lt, bool ct, bool last, int p) {
     return chunk_offset(lt, ct, last, p, active_stages(lt, ct, p));
 }
-// Chunk stride in TwPairs: a multiple of 16 bytes.
-constexpr int chunk_stride(int lt, bool ct, bool last, int p, int pair_bytes) {
-    const int per16 = 16 / pair_bytes > 0 ? 16 / pair_bytes : 1;
+// Chunk stride in entries: a multiple of 16 bytes.
+constexpr int chunk_stride(int lt, bool ct, bool last, int p, int entry_bytes) {
+    const int per16 = 16 / entry_bytes > 0 ? 16 / entry_bytes : 1;
     const int e = chunk_entries(lt, ct, last, p);
     return (e + per16 - 1) / per16 * per16;
 }
@@ -129,20 +142,20 @@ constexpr std::uint64_t chunk_count(int lt, int prefix_bits, bool ct, int p) {
 // Appends one pass's twiddle chunks (piece-major, layout above) to `out` and
 // records each phase's offset from `base`. prefix_bits: 0 for column and
 // one-pass tiles, l1 for row tiles (their block index carries 2^l1 + row).
-template <class W>
-void append_pass_chunks(std::vector<TwPair<W>>& out, std::size_t base, const std::vector<TwPair<W>>& table, int lt,
+template <class E>
+void append_pass_chunks(std::vector<E>& out, std::size_t base, const std::vector<E>& table, int lt,
                         int prefix_bits, bool ct, bool last, std::uint32_t (&phase_off)[3]) {
-    constexpr std::size_t per16 = 16 / sizeof(TwPair<W>) > 0 ? 16 / sizeof(TwPair<W>) : 1;
+    constexpr std::size_t per16 = 16 / sizeof(E) > 0 ? 16 / sizeof(E) : 1;
     for (int p = 0; p < num_phases(lt); ++p) {
         phase_off[p] = static_cast<std::uint32_t>(out.size() - base);
         const int entries = chunk_entries(lt, ct, last, p);
         if (entries == 0) continue;
         const int shift = chunk_shift(lt, ct, p);
-        const int stride = chunk_stride(lt, ct, last, p, int(sizeof(TwPair<W>)));
+        const int stride = chunk_stride(lt, ct, last, p, int(sizeof(E)));
         const int ws = window_start(lt, ct, p);
         const std::uint64_t count = chunk_count(lt, prefix_bits, ct, p);
         const std::size_t start = out.size();
-        out.resize(start + std::size_t(count) * std::size_t(stride), TwPair<W>{W(0), W(0)});
+        out.resize(start + std::size_t(count) * std::size_t(stride), E{});
         for (std::uint64_t c = 0; c < count; ++c) {
             const std::uint64_t idx = count + c;  // block index in the stage tree
             std::size_t e = 0;
@@ -240,6 +253,49 @@ __device__ __forceinline__ void gs_scale_butterfly(W& x, W& y, const DeviceDomai
     y = shoup(u - v + span, d.last.w, d.last.wp, d.nq);
 }
 
+// Barrett (the constants of the reference's GPU-NTT-compatible provider,
+// src/ntt_hybrid2d.cuh:53-71, mu = floor(2^(2b+1) / q) for the bit length b
+// of q, q < 2^(k-2)): for canonical a, w < q, P = a w < 2^(2b),
+// t = floor(P / 2^(b-2)) < 2^(b+2) and Q = floor(t mu / 2^(b+3)) satisfy
+// floor(P / q) - 1 <= Q <= floor(P / q), so P - Q q (formed modulo the word)
+// lies in [0, 2q) and one conditional subtraction makes it canonical.
+__device__ __forceinline__ std::uint32_t barrett(std::uint32_t a, std::uint32_t w, const DeviceDomain<std::uint32_t>& d) {
+    const std::uint64_t p = std::uint64_t(a) * w;
+    const std::uint32_t t = std::uint32_t(p >> (d.qbits - 2u));
+    const std::uint32_t quo = std::uint32_t((std::uint64_t(t) * d.mu) >> (d.qbits + 3u));
+    return min(std::uint32_t(p) - quo * d.q, std::uint32_t(p) - quo * d.q - d.q);
+}
+__device__ __forceinline__ std::uint64_t barrett(std::uint64_t a, std::uint64_t w, const DeviceDomain<std::uint64_t>& d) {
+    const std::uint64_t lo = a * w, hi = __umul64hi(a, w);
+    const std::uint32_t s = d.qbits - 2u;  // 0 .. 60; (hi << 1) << (63 - s) is hi << (64 - s), 0 at s = 0
+    const std::uint64_t t = (lo >> s) | ((hi << 1) << (63u - s));
+    const std::uint64_t plo = t * d.mu, phi = __umul64hi(t, d.mu);
+    const std::uint32_t s2 = d.qbits + 3u;  // 5 .. 65 (wave-uniform)
+    const std::uint64_t quo = s2 >= 64u ? phi >> (s2 - 64u) : (plo >> s2) | ((phi << 1) << (63u - s2));
+    const std::uint64_t r = lo - quo * d.q;
+    return r >= d.q ? r - d.q : r;
+}
+
+// x - m if x >= m else x (x < 2m), with no register-class constraint on m
+// (the u64 csub pins -m to scalar registers, which some kernels of this
+// arithmetic cannot satisfy).
+__device__ __forceinline__ std::uint32_t reduce_once(std::uint32_t x, std::uint32_t m) { return min(x, x - m); }
+__device__ __forceinline__ std::uint64_t reduce_once(std::uint64_t x, std::uint64_t m) { return x >= m ? x - m : x; }
+
+// Barrett butterflies keep every value canonical (inputs and outputs in [0, q)).
+template <class W>
+__device__ __forceinline__ void ct_barrett(W& x, W& y, W w, const DeviceDomain<W>& d) {
+    const W u = x, v = barrett(y, w, d);
+    x = reduce_once(u + v, d.q);
+    y = reduce_once(u - v + d.q, d.q);
+}
+template <class W>
+__device__ __forceinline__ void gs_barrett(W& x, W& y, W w, const DeviceDomain<W>& d) {
+    const W u = x, v = y;
+    x = reduce_once(u + v, d.q);
+    y = barrett(reduce_once(u - v + d.q, d.q), w, d);
+}
+
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 // Orders one wave's LDS accesses around an exchange that stays inside the
 // wave: a wave's LDS instructions execute in issue order, so only the
@@ -296,8 +352,11 @@ struct Lds {
 // lines, 16 words per thread. COL tiles hold 2^LI adjacent columns (stride
 // 2^L2) of the high L1 bits; ROW tiles hold 2^LI rows of the low L2 bits; one
 // -pass (SINGLE) tiles hold 2^LI whole polynomials (L1 = 0, L2 = LT).
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
+template <class W, int AR, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
 struct Pass {
+    static constexpr bool LAZY = AR == kLazy;
+    static constexpr bool BARRETT = AR == kBarrett;
+    using E = Entry<W, AR>;
     static constexpr int LB = LT + LI;
     static constexpr std::uint32_t T = 1u << (LB - kLE);
     static constexpr int kPhases = num_phases(LT);
@@ -486,7 +545,7 @@ struct Pass {
     // 16-byte loads that hold one phase's chunk.
     template <int P>
     static constexpr int chunk_loads() {
-        return (chunk_entries(LT, CT, kLast, P) * int(sizeof(TwPair<W>)) + 15) / 16;
+        return (chunk_entries(LT, CT, kLast, P) * int(sizeof(E)) + 15) / 16;
     }
     template <int P>
     struct Chunk {
@@ -502,7 +561,7 @@ struct Pass {
             // (scalar offset), the chunk a lane offset.
             constexpr std::uint32_t step = 16u * std::uint32_t(chunk_count(LT, (COL || SINGLE) ? 0 : L1, CT, P));
             const std::uint32_t base =
-                a.phase_off[P] * std::uint32_t(sizeof(TwPair<W>)) + 16u * chunk_index<P>(tl, t);
+                a.phase_off[P] * std::uint32_t(sizeof(E)) + 16u * chunk_index<P>(tl, t);
 #pragma unroll
             for (int e = 0; e < chunk_loads<P>(); ++e)
                 c.raw[e] = __builtin_amdgcn_raw_buffer_load_b128(tw, int(base), int(step * std::uint32_t(e)), 0);
@@ -524,7 +583,11 @@ struct Pass {
                 TwPair<W> tp{};
                 if (!scale) {
                     const int e = off + int(std::uint32_t(g) & gmask);
-                    if constexpr (sizeof(W) == 4) {
+                    if constexpr (BARRETT && sizeof(W) == 4) {
+                        tp.w = c.raw[e >> 2][e & 3];
+                    } else if constexpr (BARRETT) {
+                        tp.w = (std::uint64_t(c.raw[e >> 1][(e & 1) * 2 + 1]) << 32) | c.raw[e >> 1][(e & 1) * 2];
+                    } else if constexpr (sizeof(W) == 4) {
                         tp.w = c.raw[e >> 1][(e & 1) * 2];
                         tp.wp = c.raw[e >> 1][(e & 1) * 2 + 1];
                     } else {
@@ -536,10 +599,17 @@ struct Pass {
                 for (int lo = 0; lo < (1 << jb); ++lo) {
                     const int r = (g << (jb + 1)) | lo;
                     const int r2 = r | (1 << jb);
-                    if constexpr (CT) {
+                    if constexpr (CT && BARRETT) {
+                        ct_barrett<W>(v[r], v[r2], tp.w, d);
+                    } else if constexpr (CT) {
                         ct_butterfly<W, LAZY>(v[r], v[r2], tp, d);
                     } else if (scale) {
+                        // The final inverse stage scales by n^-1 with the
+                        // domain's Shoup pairs in every arithmetic ([0, 2q):
+                        // the last pass's final reduction follows).
                         gs_scale_butterfly<W, LAZY>(v[r], v[r2], d);
+                    } else if constexpr (BARRETT) {
+                        gs_barrett<W>(v[r], v[r2], tp.w, d);
                     } else {
                         gs_butterfly<W, LAZY>(v[r], v[r2], tp, d);
                     }
@@ -582,7 +652,7 @@ struct Pass {
     }
 
     static __device__ __forceinline__ __amdgpu_buffer_rsrc_t twiddles(const PassArgs<W>& a, const DeviceDomain<W>& d) {
-        return make_rsrc(a.tw + d.tw, a.tw_bytes);
+        return make_rsrc(static_cast<const E*>(a.tw) + d.tw, a.tw_bytes);
     }
 
     // The tile's butterflies and its store. c0 holds phase 0's twiddle chunk;
@@ -600,12 +670,15 @@ struct Pass {
         }
         if (kFirst && a.reduce_input) {
             // Arbitrary input words -> [0, 2q). A Cooley-Tukey first stage
-            // multiplies its upper operands by twiddles (any word is fine
-            // there), so only the lower half needs it.
+            // multiplies its upper operands by Shoup twiddles (any word is
+            // fine there), so only the lower half needs it. Barrett products
+            // need canonical operands: every word is reduced to [0, q).
             constexpr int top = CT ? stage_hi(LT, CT, 0) - window_start(LT, CT, 0) : kLE;
 #pragma unroll
-            for (int r = 0; r < kE; ++r)
-                if (!CT || LT < kLE || !((r >> top) & 1)) v[r] = shoup(v[r], W(1), d.rwp, d.nq);
+            for (int r = 0; r < kE; ++r) {
+                if constexpr (BARRETT) v[r] = reduce_once(shoup(v[r], W(1), d.rwp, d.nq), d.q);
+                else if (!CT || LT < kLE || !((r >> top) & 1)) v[r] = shoup(v[r], W(1), d.rwp, d.nq);
+            }
         }
         stages<0>(v, c0, d);
         if constexpr (kPhases > 1) {
@@ -663,6 +736,8 @@ struct Pass {
         u.rwp = uniform(d.rwp);
         u.ninv = {uniform(d.ninv.w), uniform(d.ninv.wp)};
         u.last = {uniform(d.last.w), uniform(d.last.wp)};
+        u.mu = uniform(d.mu);
+        u.qbits = uniform(d.qbits);
         u.tw = uniform(d.tw);
         return u;
     }
@@ -694,9 +769,9 @@ struct Pass {
     }
 };
 
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
+template <class W, int AR, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
 __global__ __launch_bounds__(1 << (LT + LI - kLE)) void ntt_pass_kernel(PassArgs<W> a) {
-    Pass<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>::run(a);
+    Pass<W, AR, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>::run(a);
 }
 
 // ---- launcher registry -----------------------------------------------------
@@ -705,18 +780,18 @@ template <class W>
 using PassLaunch = void (*)(const PassArgs<W>&, unsigned grid, hipStream_t);
 
 struct PassKey {
-    bool lazy;
+    int arith;  // kStrict, kLazy or kBarrett
     int log_n, lt, li;
     bool col, ct, pin, pout, single;
     bool operator<(const PassKey& o) const {
-        return std::tie(lazy, log_n, lt, li, col, ct, pin, pout, single) <
-               std::tie(o.lazy, o.log_n, o.lt, o.li, o.col, o.ct, o.pin, o.pout, o.single);
+        return std::tie(arith, log_n, lt, li, col, ct, pin, pout, single) <
+               std::tie(o.arith, o.log_n, o.lt, o.li, o.col, o.ct, o.pin, o.pout, o.single);
     }
 };
 
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
+template <class W, int AR, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
 void launch_pass(const PassArgs<W>& a, unsigned grid, hipStream_t stream) {
-    hipLaunchKernelGGL((ntt_pass_kernel<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>), dim3(grid),
+    hipLaunchKernelGGL((ntt_pass_kernel<W, AR, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>), dim3(grid),
                        dim3(1u << (LT + LI - kLE)), 0, stream, a);
 }
 
@@ -728,28 +803,28 @@ std::map<PassKey, PassLaunch<std::uint32_t>>& registry<std::uint32_t>();
 template <>
 std::map<PassKey, PassLaunch<std::uint64_t>>& registry<std::uint64_t>();
 
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
+template <class W, int AR, int LT, int LI, bool COL, bool CT, bool PIN, bool POUT, bool SINGLE, int L1, int L2>
 void add() {
-    registry<W>()[PassKey{LAZY, L1 + L2, LT, LI, COL, CT, PIN, POUT, SINGLE}] =
-        &launch_pass<W, LAZY, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>;
+    registry<W>()[PassKey{AR, L1 + L2, LT, LI, COL, CT, PIN, POUT, SINGLE}] =
+        &launch_pass<W, AR, LT, LI, COL, CT, PIN, POUT, SINGLE, L1, L2>;
 }
 
 // Boundary-permutation variants of one pass shape: a first pass may permute
 // its input, a last pass its output.
-template <class W, bool LAZY, int LT, int LI, bool COL, bool CT, bool SINGLE, int L1, int L2>
+template <class W, int AR, int LT, int LI, bool COL, bool CT, bool SINGLE, int L1, int L2>
 void add_variants() {
     constexpr bool first = SINGLE || (COL == CT);
     constexpr bool last = SINGLE || (COL != CT);
-    add<W, LAZY, LT, LI, COL, CT, false, false, SINGLE, L1, L2>();
-    if constexpr (first) add<W, LAZY, LT, LI, COL, CT, true, false, SINGLE, L1, L2>();
-    if constexpr (last) add<W, LAZY, LT, LI, COL, CT, false, true, SINGLE, L1, L2>();
-    if constexpr (first && last) add<W, LAZY, LT, LI, COL, CT, true, true, SINGLE, L1, L2>();
+    add<W, AR, LT, LI, COL, CT, false, false, SINGLE, L1, L2>();
+    if constexpr (first) add<W, AR, LT, LI, COL, CT, true, false, SINGLE, L1, L2>();
+    if constexpr (last) add<W, AR, LT, LI, COL, CT, false, true, SINGLE, L1, L2>();
+    if constexpr (first && last) add<W, AR, LT, LI, COL, CT, true, true, SINGLE, L1, L2>();
 }
 
-template <class W, bool LAZY, int LT, int LB>
+template <class W, int AR, int LT, int LB>
 void add_single() {
-    add_variants<W, LAZY, LT, LB - LT, false, true, true, 0, LT>();
-    add_variants<W, LAZY, LT, LB - LT, false, false, true, 0, LT>();
+    add_variants<W, AR, LT, LB - LT, false, true, true, 0, LT>();
+    add_variants<W, AR, LT, LB - LT, false, false, true, 0, LT>();
 }
 
 // Two-pass split used by the planner: l1 = min(8, log n / 2) high bits;
@@ -763,77 +838,79 @@ constexpr int kWideColLines = 5;
 constexpr int row_lines(int l1, int l2) { return l1 < kTileLog - l2 ? l1 : kTileLog - l2; }
 
 // Column passes of one split with 32-column tiles, where they fit.
-template <class W, bool LAZY, int L1, int L2>
+template <class W, int AR, int L1, int L2>
 void add_wide_columns() {
     if constexpr (L1 + kWideColLines <= 13 && L2 >= kWideColLines) {
-        add_variants<W, LAZY, L1, kWideColLines, true, true, false, L1, L2>();
-        add_variants<W, LAZY, L1, kWideColLines, true, false, false, L1, L2>();
+        add_variants<W, AR, L1, kWideColLines, true, true, false, L1, L2>();
+        add_variants<W, AR, L1, kWideColLines, true, false, false, L1, L2>();
     }
 }
 
 // Column passes of one split: 16-column tiles, and 32-column tiles (WIDE).
-template <class W, bool LAZY, int L1, int L2, bool WIDE>
+template <class W, int AR, int L1, int L2, bool WIDE>
 void add_columns() {
-    add_variants<W, LAZY, L1, kColLines, true, true, false, L1, L2>();
-    add_variants<W, LAZY, L1, kColLines, true, false, false, L1, L2>();
-    if constexpr (WIDE) add_wide_columns<W, LAZY, L1, L2>();
+    add_variants<W, AR, L1, kColLines, true, true, false, L1, L2>();
+    add_variants<W, AR, L1, kColLines, true, false, false, L1, L2>();
+    if constexpr (WIDE) add_wide_columns<W, AR, L1, L2>();
 }
 
-template <class W, bool LAZY, int L1, int L2>
+template <class W, int AR, int L1, int L2>
 void add_rows() {
     constexpr int rli = row_lines(L1, L2);
-    add_variants<W, LAZY, L2, rli, false, true, false, L1, L2>();
-    add_variants<W, LAZY, L2, rli, false, false, false, L1, L2>();
+    add_variants<W, AR, L2, rli, false, true, false, L1, L2>();
+    add_variants<W, AR, L2, rli, false, false, false, L1, L2>();
 }
 
 // The planner's split (l1 = split_l1): u32 with 16- and 32-column tiles,
 // u64 with 16 (32-column u64 tiles and other splits are instantiated by
 // ntt_alt_u32.hip and ntt_alt_u64.hip).
-template <class W, bool LAZY, int LOG_N>
+template <class W, int AR, int LOG_N>
 void add_two_pass() {
     constexpr int l1 = split_l1(LOG_N), l2 = LOG_N - l1;
-    add_columns<W, LAZY, l1, l2, sizeof(W) == 4>();
-    add_rows<W, LAZY, l1, l2>();
+    add_columns<W, AR, l1, l2, sizeof(W) == 4>();
+    add_rows<W, AR, l1, l2>();
 }
 
 // Another split of LOG_N (both tile widths), for MEASURE and RNS Prepare.
-template <class W, bool LAZY, int LOG_N, int L1>
+template <class W, int AR, int LOG_N, int L1>
 void add_split() {
     static_assert(L1 >= 4 && LOG_N - L1 >= 4 && LOG_N - L1 <= kTileLog, "split shape");
-    add_columns<W, LAZY, L1, LOG_N - L1, true>();
-    add_rows<W, LAZY, L1, LOG_N - L1>();
+    add_columns<W, AR, L1, LOG_N - L1, true>();
+    add_rows<W, AR, L1, LOG_N - L1>();
 }
 
 // 4 KiWord tiles; columns of 64 B (u32) / 128 B (u64).
-template <class W, bool LAZY>
+template <class W, int AR>
 void register_all() {
     constexpr int LB = kTileLog;
-    add_single<W, LAZY, 1, LB>();
-    add_single<W, LAZY, 2, LB>();
-    add_single<W, LAZY, 3, LB>();
-    add_single<W, LAZY, 4, LB>();
-    add_single<W, LAZY, 5, LB>();
-    add_single<W, LAZY, 6, LB>();
-    add_single<W, LAZY, 7, LB>();
-    add_single<W, LAZY, 8, LB>();
-    add_single<W, LAZY, 9, LB>();
-    add_single<W, LAZY, 10, LB>();
-    add_single<W, LAZY, 11, LB>();
-    add_single<W, LAZY, 12, LB>();
-    add_two_pass<W, LAZY, 13>();
-    add_two_pass<W, LAZY, 14>();
-    add_two_pass<W, LAZY, 15>();
-    add_two_pass<W, LAZY, 16>();
-    add_two_pass<W, LAZY, 17>();
-    add_two_pass<W, LAZY, 18>();
-    add_two_pass<W, LAZY, 19>();
-    add_two_pass<W, LAZY, 20>();
+    add_single<W, AR, 1, LB>();
+    add_single<W, AR, 2, LB>();
+    add_single<W, AR, 3, LB>();
+    add_single<W, AR, 4, LB>();
+    add_single<W, AR, 5, LB>();
+    add_single<W, AR, 6, LB>();
+    add_single<W, AR, 7, LB>();
+    add_single<W, AR, 8, LB>();
+    add_single<W, AR, 9, LB>();
+    add_single<W, AR, 10, LB>();
+    add_single<W, AR, 11, LB>();
+    add_single<W, AR, 12, LB>();
+    add_two_pass<W, AR, 13>();
+    add_two_pass<W, AR, 14>();
+    add_two_pass<W, AR, 15>();
+    add_two_pass<W, AR, 16>();
+    add_two_pass<W, AR, 17>();
+    add_two_pass<W, AR, 18>();
+    add_two_pass<W, AR, 19>();
+    add_two_pass<W, AR, 20>();
 }
 
 void register_u32_lazy();
 void register_u32_strict();
 void register_u64_lazy();
 void register_u64_strict();
+void register_u32_barrett();
+void register_u64_barrett();
 void register_alt_u32();
 void register_alt_u64();
 

@@ -195,7 +195,10 @@ struct RnsMapping {
     bool strict = false;      // fully reduced butterflies where lazy ones would fit
     bool wide = false;        // 32-column tiles in the column pass
     std::uint32_t split = 0;  // high (column-pass) bits; 0 = the planner's split
-    bool operator==(const RnsMapping& o) const { return strict == o.strict && wide == o.wide && split == o.split; }
+    bool barrett = false;     // Barrett products (one constant per domain, single-word twiddle tables)
+    bool operator==(const RnsMapping& o) const {
+        return strict == o.strict && wide == o.wide && split == o.split && barrett == o.barrett;
+    }
 };
 
 // A lowering's engines: the transform, and for one-pass in-place plans whose
@@ -217,6 +220,7 @@ RnsLowering lower(const RnsConfig& config, const RnsMapping& m, bool same_offset
     e.output_bit_reversed = config.output_reversed;
     e.reduce_input = false;  // canonical residues are the input contract
     e.force_strict = m.strict;
+    e.barrett = m.barrett;
     e.wide_columns = m.wide;
     e.split_high = m.split;
     e.domains = config.domains;
@@ -246,16 +250,20 @@ std::vector<RnsMapping> candidates(const RnsConfig& c) {
     if (max_q < (std::uint64_t{1} << 62)) arithmetic = {false, true};
     std::vector<RnsMapping> out;
     for (const bool strict : arithmetic) {
-        out.push_back({strict, false, 0});
+        out.push_back({strict, false, 0, false});
         if (c.log_n <= 12) continue;  // one pass: no columns, no split
-        out.push_back({strict, true, 0});
-        for (const std::uint32_t split : cbw::ntt_other_splits(c.log_n)) out.push_back({strict, false, split});
+        out.push_back({strict, true, 0, false});
+        for (const std::uint32_t split : cbw::ntt_other_splits(c.log_n)) out.push_back({strict, false, split, false});
     }
+    // Barrett products, as the reference's mapping offers them beside Shoup
+    // (src/rns_ntt.cu:331-346, rejected there too for moduli of 2^62 or more),
+    // at the planner's tiles and split.
+    if (max_q < (std::uint64_t{1} << 62)) out.push_back({false, false, 0, true});
     return out;
 }
 
 std::string mapping_name(const RnsMapping& m) {
-    return std::string(m.strict ? "strict" : "lazy") + (m.wide ? "-c32" : "-c16") +
+    return std::string(m.barrett ? "barrett" : m.strict ? "strict" : "lazy") + (m.wide ? "-c32" : "-c16") +
            (m.split ? "-h" + std::to_string(m.split) : "");
 }
 

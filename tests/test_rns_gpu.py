@@ -71,9 +71,10 @@ def test_c4_full_size_round_trip(torch_gpu, rlib):
 @pytest.mark.parametrize("inverse", [False, True])
 def test_prepare_sweeps_the_candidates(torch_gpu, rlib, inverse):
     # Prepare times every mapping the gfx950 engine offers this request --
-    # lazy and strict arithmetic (the 60-bit primes leave two spare bits),
-    # 16- and 32-column tiles, the neighbouring splits 7 / 9 of the 16 index
-    # bits -- and executes the fastest; the result stays bit-exact.
+    # lazy and strict Shoup arithmetic (the 60-bit primes leave two spare
+    # bits), 16- and 32-column tiles, the neighbouring splits 7 / 9 of the 16
+    # index bits, Barrett products -- and executes the fastest; the result
+    # stays bit-exact.
     print(f"case rns prepare sweep inverse={inverse}", flush=True)
     log_n, n, limbs = 16, 1 << 16, 4
     moduli = workloads.c4_moduli()[:limbs]
@@ -90,7 +91,8 @@ def test_prepare_sweeps_the_candidates(torch_gpu, rlib, inverse):
         info = plan.info()
     mappings = [c["mapping"] for c in info["candidates"]]
     assert mappings == ["lazy-c16", "lazy-c32", "lazy-c16-h7", "lazy-c16-h9",
-                        "strict-c16", "strict-c32", "strict-c16-h7", "strict-c16-h9"]
+                        "strict-c16", "strict-c32", "strict-c16-h7", "strict-c16-h9",
+                        "barrett-c16"]
     assert all(c["kernel_ms"] > 0 for c in info["candidates"])
     assert info["selected"] in mappings and info["source"] == "uncached_candidate_sweep"
     assert info["kernel_ms"] > 0 and info["mapping"]["algorithm"] in [c["algorithm"] for c in info["candidates"]]
@@ -228,7 +230,8 @@ def test_prepare_cache_contract(torch_gpu, rlib, tmp_path):
     assert len(records) == 1 and records[0].stem == first["cache_key"]
     record = json.loads(records[0].read_text())
     assert record["selected"] == first["selected"] and record["source"] == "candidate_sweep"
-    assert [c["mapping"] for c in record["candidates"]] == ["lazy-c16", "strict-c16"]  # one pass: arithmetic only
+    # One pass: arithmetic only (lazy, strict and Barrett products).
+    assert [c["mapping"] for c in record["candidates"]] == ["lazy-c16", "strict-c16", "barrett-c16"]
     assert record["validation"] == "finalists_bit_exact_against_static_plan"
     with rns.RnsPlan(rlib, cfg) as plan:
         plan.prepare(stream, cache_dir=tmp_path, cache="require")

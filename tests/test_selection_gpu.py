@@ -135,7 +135,7 @@ def test_every_ntt_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path
         names = measured(plan)
     # Lazy and strict; two-pass lengths add 32-column tiles (the static choice,
     # listed first, for u32 at 2^16) and at 2^15..2^17 the neighbouring
-    # splits of the high and low bits.
+    # splits of the high and low bits; Barrett products last.
     base = f"ntt-u{bits}-negacyclic-" + ("two-pass-r16" if log_n > 12 else "resident-r16")
     expected = [base, base + "-strict"] + ([base + "-c32"] if log_n >= 13 else [])
     if log_n == 16 and bits == 32:
@@ -143,6 +143,7 @@ def test_every_ntt_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path
     l1 = min(8, log_n // 2)
     if 15 <= log_n <= 17:
         expected += [f"{base}-h{l1 - 1}", f"{base}-h{l1 + 1}"]
+    expected.append(base + "-barrett")  # every modulus here is below 2^(word bits - 2)
     assert names == expected
     q = modulus(bits, log_n)
     rng = np.random.default_rng(log_n)
