@@ -52,17 +52,17 @@ struct RnsConfig {
 };
 
 void allowed_fields(const cbw::json::Value& v, std::initializer_list<const char*> names, const char* what) {
-    require(v.is_object(), std::string("RNS JSON ") + what + " must be an object");
+    require(v.is_object(), std::string("the RNS request's ") + what + " is not a JSON object");
     for (const auto& m : v.members)
         require(std::find_if(names.begin(), names.end(), [&](const char* n) { return m.first == n; }) != names.end(),
-                std::string("unknown RNS JSON ") + what + " field: " + m.first);
+                std::string("the RNS request's ") + what + " has a field this schema does not define: " + m.first);
 }
 
 bool order_value(const cbw::json::Value& v, const char* field) {
     const auto& s = v.as_string(field);
     if (s == "natural") return false;
     if (s == "bit_reversed") return true;
-    throw std::invalid_argument("invalid RNS JSON enum: " + s);
+    throw std::invalid_argument("RNS order must be \"natural\" or \"bit_reversed\", not " + s);
 }
 
 // Schema of the reference (src/rns_tuning.cpp:124-150).
@@ -71,21 +71,21 @@ RnsConfig parse_config(const std::string& text) {
     allowed_fields(j, {"schema_version", "log_n", "inverse", "ring", "input_order", "output_order", "domains",
                        "polynomials"},
                    "config");
-    require(j.at("schema_version").as_u64("schema_version") == 1, "unsupported RNS JSON schema_version");
+    require(j.at("schema_version").as_u64("schema_version") == 1, "RNS request schema_version must be 1");
     RnsConfig c;
     const auto log_n = j.at("log_n").as_u64("log_n");
-    require(log_n <= 0xffffffffull, "RNS JSON integer field overflows");
+    require(log_n <= 0xffffffffull, "RNS log_n does not fit 32 bits");
     c.log_n = static_cast<std::uint32_t>(log_n);
     c.inverse = j.at("inverse").as_bool("inverse");
     const auto& ring = j.at("ring").as_string("ring");
     if (ring == "cyclic") c.negacyclic = false;
     else if (ring == "negacyclic") c.negacyclic = true;
-    else throw std::invalid_argument("invalid RNS JSON enum: " + ring);
+    else throw std::invalid_argument("RNS ring must be \"cyclic\" or \"negacyclic\", not " + ring);
     c.input_reversed = order_value(j.at("input_order"), "input_order");
     c.output_reversed = order_value(j.at("output_order"), "output_order");
     const auto& domains = j.at("domains");
     const auto& polys = j.at("polynomials");
-    require(domains.is_array() && polys.is_array(), "RNS domains and polynomials must be arrays");
+    require(domains.is_array() && polys.is_array(), "RNS request needs JSON arrays of domains and polynomials");
     for (const auto& d : domains.items) {
         allowed_fields(d, {"modulus", "root"}, "domain");
         c.domains.push_back({d.at("modulus").as_u64("modulus"), d.at("root").as_u64("root")});
@@ -93,7 +93,7 @@ RnsConfig parse_config(const std::string& text) {
     for (const auto& p : polys.items) {
         allowed_fields(p, {"domain", "input_offset", "output_offset"}, "polynomial");
         const auto domain = p.at("domain").as_u64("domain");
-        require(domain <= 0xffffffffull, "RNS JSON integer field overflows");
+        require(domain <= 0xffffffffull, "RNS polynomial domain index does not fit 32 bits");
         c.polynomials.push_back({static_cast<std::uint32_t>(domain), p.at("input_offset").as_u64("input_offset"),
                                  p.at("output_offset").as_u64("output_offset")});
     }
@@ -127,28 +127,28 @@ std::string config_json(const RnsConfig& c) {
 // Validation rules of the reference plan constructor (src/rns_ntt.cu:259-300).
 void validate(const RnsConfig& c, std::uint64_t& input_extent, std::uint64_t& output_extent) {
     require(c.log_n >= 12 && c.log_n <= 20 && !c.domains.empty() && !c.polynomials.empty(),
-            "RNS requires log_n in [12,20], domains and polynomials");
+            "RNS plans take log_n from 12 to 20 and at least one domain and one polynomial");
     const std::uint64_t n = std::uint64_t{1} << c.log_n;
     std::vector<std::pair<std::uint64_t, std::uint64_t>> outputs;
     const std::uint64_t limit = (~std::uint64_t{0}) / sizeof(std::uint64_t) - n;
     input_extent = output_extent = 0;
     for (const auto& p : c.polynomials) {
         require(p.domain < c.domains.size() && p.input_offset <= limit && p.output_offset <= limit,
-                "invalid RNS polynomial domain or extent");
+                "RNS polynomial names a missing domain or its words run past the addressable range");
         input_extent = std::max(input_extent, p.input_offset + n);
         output_extent = std::max(output_extent, p.output_offset + n);
         outputs.emplace_back(p.output_offset, p.output_offset + n);
     }
     std::sort(outputs.begin(), outputs.end());
     for (std::size_t i = 1; i < outputs.size(); ++i)
-        require(outputs[i].first >= outputs[i - 1].second, "overlapping RNS output intervals");
+        require(outputs[i].first >= outputs[i - 1].second, "two RNS polynomials write overlapping output words");
     for (const auto& d : c.domains) {
         const std::uint64_t q = d.modulus;
         const std::uint64_t order = c.negacyclic ? 2 * n : n;
         require(q >= 3 && q < (std::uint64_t{1} << 63) && cbw::is_prime_u64(q) && d.root != 0 && d.root < q &&
                     (q - 1) % order == 0 && cbw::powmod(d.root, order, q) == 1 &&
                     cbw::powmod(d.root, order / 2, q) == q - 1,
-                "RNS requires prime modulus <2^63 and an explicit primitive ring root");
+                "each RNS domain needs a prime modulus below 2^63 and a root of exact ring order (2n negacyclic, n cyclic)");
     }
 }
 
@@ -172,17 +172,17 @@ void atomic_write(const std::string& directory, const std::string& path, const s
     ::mkdir(directory.c_str(), 0775);  // existing directory is fine
     std::string temp = path + ".tmp.XXXXXX";
     const int fd = ::mkstemp(temp.data());
-    if (fd < 0) throw std::runtime_error("cannot create RNS cache temporary file: " + std::string(std::strerror(errno)));
+    if (fd < 0) throw std::runtime_error("RNS cache: temporary file not created: " + std::string(std::strerror(errno)));
     const bool wrote = ::write(fd, contents.data(), contents.size()) == static_cast<ssize_t>(contents.size());
     const bool synced = ::fsync(fd) == 0;
     const bool closed = ::close(fd) == 0;
     if (!wrote || !synced || !closed) {
         std::remove(temp.c_str());
-        throw std::runtime_error("cannot write complete RNS cache record");
+        throw std::runtime_error("RNS cache: record only partly written");
     }
     if (std::rename(temp.c_str(), path.c_str()) != 0) {
         std::remove(temp.c_str());
-        throw std::runtime_error("cannot publish RNS cache record: " + std::string(std::strerror(errno)));
+        throw std::runtime_error("RNS cache: record not renamed into place: " + std::string(std::strerror(errno)));
     }
 }
 
@@ -331,7 +331,7 @@ int guarded(F&& body) noexcept {
         try { rns_error = e.what(); } catch (...) {}
         return 2;
     } catch (...) {
-        try { rns_error = "unknown RNS failure"; } catch (...) {}
+        try { rns_error = "RNS call failed with an unrecognised exception"; } catch (...) {}
         return 2;
     }
 }
@@ -399,7 +399,7 @@ double time_lowering(const cubutterflyRnsPlanOpaque& plan, const RnsLowering& l,
         cbw::hip_check(hipEventSynchronize(stop), "hipEventSynchronize");
         float ms = 0;
         cbw::hip_check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
-        if (!(ms > 0)) throw std::runtime_error("invalid RNS candidate timing");
+        if (!(ms > 0)) throw std::runtime_error("RNS candidate timed at zero or a non-finite time");
         release();
         return double(ms) / repeat;
     } catch (...) {
@@ -525,9 +525,9 @@ const char* cubutterflyRnsLastError(void) { return rns_error.c_str(); }
 
 int cubutterflyRnsCreate(const char* config_json_text, cubutterflyRnsPlan* result) {
     return guarded([&] {
-        require(result != nullptr, "result must be non-null");
+        require(result != nullptr, "RNS create needs a plan output pointer");
         *result = nullptr;
-        require(config_json_text != nullptr, "config JSON must be non-null");
+        require(config_json_text != nullptr, "RNS create needs request JSON text");
         auto plan = std::make_unique<cubutterflyRnsPlanOpaque>();
         plan->config = parse_config(config_json_text);
         validate(plan->config, plan->input_extent, plan->output_extent);
@@ -544,17 +544,17 @@ int cubutterflyRnsCreate(const char* config_json_text, cubutterflyRnsPlan* resul
 int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* cache_directory, int policy,
                           unsigned repetitions, void* stream_handle) {
     return guarded([&] {
-        require(plan != nullptr, "plan must be non-null");
-        require(!plan->prepared, "plan is already prepared; create another plan to retune");
-        require(placement == 0 || placement == 1, "invalid placement");
-        require(policy >= 0 && policy <= 2, "invalid cache policy");
-        require(repetitions > 0 && repetitions <= 1000, "RNS tuning repetitions must be in [1,1000]");
+        require(plan != nullptr, "RNS prepare needs a plan");
+        require(!plan->prepared, "RNS plan was prepared before: a plan is prepared once (create a new plan to search again)");
+        require(placement == 0 || placement == 1, "RNS placement must be 0 (separate buffers) or 1 (in place)");
+        require(policy >= 0 && policy <= 2, "RNS cache policy must be 0 (prefer), 1 (require) or 2 (refresh)");
+        require(repetitions > 0 && repetitions <= 1000, "RNS prepare repetitions must be between 1 and 1000");
         const auto stream = static_cast<hipStream_t>(stream_handle);
         hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
         cbw::hip_check(hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
         require(capture == hipStreamCaptureStatusNone, "RNS preparation must run outside graph capture");
         const std::string directory = cache_directory ? cache_directory : "";
-        require(!(directory.empty() && policy == 1), "RNS Require policy needs a nonempty cache_directory");
+        require(!(directory.empty() && policy == 1), "RNS cache policy require needs a cache directory");
         const std::string identity = identity_json(*plan, placement, repetitions);
         const std::string key = "rns-v1-" + hex64(fnv1a(identity));
         const std::string path = directory + "/" + key + ".json";
@@ -563,9 +563,9 @@ int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* ca
             std::ifstream input(path);
             std::stringstream buffer;
             buffer << input.rdbuf();
-            if (!input && !input.eof()) throw std::runtime_error("cannot read RNS cache record: " + path);
+            if (!input && !input.eof()) throw std::runtime_error("RNS cache: record unreadable: " + path);
             const auto record = cbw::json::parse(buffer.str());
-            require(record.at("schema_version").as_u64("schema_version") == 1, "unsupported RNS JSON schema_version");
+            require(record.at("schema_version").as_u64("schema_version") == 1, "RNS request schema_version must be 1");
             // Compare the complete identity: a file-name collision cannot
             // authorise another request's record.
             const auto& stored = record.at("identity");
@@ -593,9 +593,9 @@ int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* ca
                 return false;
             };
             if (!same(stored, reparsed, same))
-                throw std::runtime_error("RNS cache identity mismatch (incompatible record or hash collision): " + path);
+                throw std::runtime_error("RNS cache: record describes another request, device or protocol: " + path);
             require(record.at("source").as_string("source") == "candidate_sweep",
-                    "unsupported RNS cache measurement provenance");
+                    "RNS cache: record was not written by this library's candidate sweep");
             // The record names one of this request's candidates; it is rebuilt,
             // never trusted beyond that.
             const std::string selected = record.at("selected").as_string("selected");
@@ -604,7 +604,7 @@ int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* ca
                                          [&](const RnsMapping& m) { return mapping_name(m) == selected; });
             require(it != options.end(), "RNS cache record selects no mapping of this request: " + selected);
             plan->kernel_ms = record.at("kernel_ms").as_double("kernel_ms");
-            require(plan->kernel_ms > 0, "invalid RNS cache kernel_ms");
+            require(plan->kernel_ms > 0, "RNS cache: record holds no positive kernel time");
             plan->select(lower(plan->config, *it, plan->same_offsets));
             for (const auto& m : record.at("candidates").items)
                 plan->measurements.push_back({m.at("mapping").as_string("mapping"),
@@ -613,7 +613,7 @@ int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* ca
             plan->cache_hit = true;
             plan->source = "prepared_cache";
         } else {
-            if (policy == 1) throw std::runtime_error("required RNS prepared cache record is missing: " + path);
+            if (policy == 1) throw std::runtime_error("RNS cache policy require, but no record exists: " + path);
             std::vector<RnsMeasurement> tested;
             RnsLowering chosen = sweep(*plan, placement == 1, repetitions, stream, tested);
             const std::string selected = mapping_name(chosen.mapping);
@@ -645,12 +645,12 @@ int cubutterflyRnsPrepare(cubutterflyRnsPlan plan, int placement, const char* ca
 
 int cubutterflyRnsExecute(cubutterflyRnsPlan plan, const uint64_t* input, uint64_t* output, void* stream) {
     return guarded([&] {
-        require(plan != nullptr && plan->prepared, "plan must be prepared");
-        require(input != nullptr && output != nullptr, "device pointers must be non-null");
+        require(plan != nullptr && plan->prepared, "RNS execute needs a prepared plan");
+        require(input != nullptr && output != nullptr, "RNS execute needs input and output device pointers");
         require(reinterpret_cast<std::uintptr_t>(input) % alignof(std::uint64_t) == 0 &&
                     reinterpret_cast<std::uintptr_t>(output) % alignof(std::uint64_t) == 0,
-                "device pointers must be uint64 aligned");
-        require((input == output) == plan->in_place, "pointer aliasing does not match prepared placement");
+                "RNS input and output pointers must be 8-byte aligned");
+        require((input == output) == plan->in_place, "RNS input / output aliasing differs from the placement the plan was prepared for");
         int device = -1;
         cbw::hip_check(hipGetDevice(&device), "hipGetDevice");
         require(device == plan->device, "RNS plan used on a different device");
@@ -660,7 +660,7 @@ int cubutterflyRnsExecute(cubutterflyRnsPlan plan, const uint64_t* input, uint64
 
 int cubutterflyRnsInfoJson(cubutterflyRnsPlan plan, char* buffer, size_t* bytes) {
     return guarded([&] {
-        require(plan != nullptr && bytes != nullptr, "plan and bytes must be non-null");
+        require(plan != nullptr && bytes != nullptr, "RNS info needs a plan and a size pointer");
         cbw::json::Writer w;
         w.begin_object()
             .field("prepared", plan->prepared)
@@ -682,7 +682,7 @@ int cubutterflyRnsInfoJson(cubutterflyRnsPlan plan, char* buffer, size_t* bytes)
         const std::size_t capacity = *bytes;
         *bytes = text.size() + 1;
         if (!buffer) return;
-        require(capacity >= *bytes, "info JSON buffer is too small");
+        require(capacity >= *bytes, "RNS info buffer is smaller than the JSON text");
         std::memcpy(buffer, text.c_str(), *bytes);
     });
 }
