@@ -376,9 +376,13 @@ struct Pass {
     // output lands in 8-byte segments: 60.6 -> 71-73 us.) Forward column
     // passes whose tiles write whole 128-byte lines per row (u32 32-column,
     // u64 16-column tiles) store the intermediate nontemporally: C4 56.5 ->
-    // 54.9 us, C2 unchanged.
-    static constexpr int kStoreAux =
-        (!CT && !SINGLE) ? 17 : (COL && CT && !SINGLE && (sizeof(W) << LI) >= 128) ? 2 : 0;
+    // 54.9 us, C2 unchanged. Forward row passes that stage their stores
+    // (natural output through the LDS permutation, or native output through
+    // the wave's own rows, kStagedAux) write through as well: C2 38.6 ->
+    // 37.3 us, C4 54.2 -> 52.0 us.
+    static constexpr int kStoreAux = (!CT && !SINGLE) || (CT && !SINGLE && !COL && POUT) ? 17
+                                     : (COL && CT && !SINGLE && (sizeof(W) << LI) >= 128) ? 2
+                                                                                          : 0;
     // Row tiles of at most 2^10-point rows: every phase layout keeps a row in
     // 2^(LT-4) <= 64 consecutive threads (phase_index puts the row bits at
     // t >> (LT - 4)), so the register-window exchanges never leave a wave.
@@ -387,6 +391,14 @@ struct Pass {
     // The staged boundary permutations (PIN / POUT) mix rows across waves
     // and keep their barriers.
     static constexpr bool kWaveLocal = !COL && LT - kLE <= 6;
+    // Forward row tiles whose output stays in the transform's native order
+    // end with every thread holding 16 consecutive outputs of one row, so a
+    // store instruction would put its 64 lanes 16 words apart (64 cache lines
+    // per instruction). A wave's 1024 outputs are one contiguous run, and
+    // they go through the wave's own LDS rows instead: each 16-byte store
+    // instruction then covers 64 x 16 contiguous bytes.
+    static constexpr bool kStagedStore = !COL && CT && kLast && !POUT && kWaveLocal && LT + LI >= 10;
+    static constexpr int kStagedAux = SINGLE ? 0 : 17;
     static_assert(SINGLE ? (L1 == 0 && L2 == LT) : (COL ? LT == L1 : LT == L2), "pass bits");
     static_assert(LT >= 1 && LB >= kLE && LB <= 13, "tile shape");
 
@@ -717,6 +729,32 @@ struct Pass {
 #pragma unroll
             for (int r = 0; r < kE; ++r) {
                 store_at(lds[staged_lds(b, r)], dst, b.word * B, staged_word(r) * B);
+            }
+        } else if constexpr (kStagedStore) {
+            constexpr std::uint32_t B = sizeof(W);
+            constexpr int kPer = 16 / int(sizeof(W));  // words per 16-byte store
+            wave_lds_fence();
+#pragma unroll
+            for (int r = 0; r < kE; ++r) lds[L::template at<wl>(t, r)] = v[r];
+            wave_lds_fence();
+            // Lane l of wave w stores tile elements g0 + 64 kPer k + 0..kPer-1,
+            // g0 = 1024 w + kPer l: the thread, lane and register parts lie in
+            // disjoint index bits, so the LDS address and the output word
+            // (row k0 + rr at stride 2^L2 = 2^LT, or the dense one-pass
+            // element) split into a thread part plus a compile-time offset;
+            // kPer consecutive words never cross the image's 1-in-16 pad.
+            const std::uint32_t g0 = (t >> 6) * 1024u + std::uint32_t(kPer) * (t & 63u);
+            const std::uint32_t a0 = L::addr(g0);
+            const std::uint32_t w0 = natural_word(tl, g0) * B;
+#pragma unroll
+            for (int k = 0; k < kE / kPer; ++k) {
+                const std::uint32_t gk = 64u * std::uint32_t(kPer) * std::uint32_t(k);
+                const std::uint32_t ak = a0 + L::addr(gk);
+                using V4 = __attribute__((ext_vector_type(4))) std::uint32_t;
+                W x[kPer];
+#pragma unroll
+                for (int e = 0; e < kPer; ++e) x[e] = lds[ak + std::uint32_t(e)];
+                buffer_store<V4, kStagedAux>(__builtin_bit_cast(V4, x), dst, w0, gk * B);
             }
         } else {
             constexpr std::uint32_t B = sizeof(W);

@@ -251,7 +251,7 @@ def test_prepare_cache_contract(torch_gpu, rlib, tmp_path):
     with rns.RnsPlan(rlib, cfg) as plan:
         with pytest.raises(cb.AbiError) as info:
             plan.prepare(stream, cache_dir=tmp_path, cache="prefer")
-        assert "identity" in str(info.value)
+        assert "describes another request" in str(info.value)
 
 
 def test_execute_contract(torch_gpu, rlib):
