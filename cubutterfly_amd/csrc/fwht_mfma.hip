@@ -95,16 +95,30 @@ __device__ __forceinline__ unsigned short narrow(float x, float norm, float scal
 // them. Lane l holds a[i2][j] = element i2 * 256 + (l % 16) * 16 +
 // 4 (l / 16) + j: element bits 0-1 are register bits (j), bits 2-3 lane
 // bits 4-5, bits 4-7 lane bits 0-3, bits 8-11 register bits (i2). Results
-// leave in the input's own layout.
+// leave in the input's own layout. The tile is loaded again here, so that no
+// input register stays live into this path: the common path keeps its own
+// allocation and this one spills what does not fit.
+// This path needs about 200 VGPRs where the MFMA path needs 120, and the
+// kernel's allocation covers both: the kernel therefore asks for four waves
+// per SIMD (at most 128 VGPRs), so what does not fit spills here, in the
+// path that only tiles holding inf or NaN take. Scheduling barriers after
+// each group of four lane exchanges keep the compiler from hoisting all 64
+// of a stage at once.
 template <int LOG_N>
-__device__ __forceinline__ void stage_ordered_tile(const half4 (&a)[16], unsigned lane, unsigned lane_bytes,
+__device__ __forceinline__ void stage_ordered_tile(__amdgpu_buffer_rsrc_t src, unsigned lane, unsigned lane_bytes,
                                                    __amdgpu_buffer_rsrc_t dst, float norm, float scale) {
     using U2 = __attribute__((ext_vector_type(2))) unsigned;
+    // A fresh copy of the lane offset: addresses derived from it are computed
+    // here, not shared with (and kept live from) the common path.
+    asm volatile("" : "+v"(lane_bytes));
     float v[16][4];
 #pragma unroll
-    for (int i2 = 0; i2 < 16; ++i2)
+    for (int i2 = 0; i2 < 16; ++i2) {
+        const U2 raw = __builtin_amdgcn_raw_buffer_load_b64(src, int(lane_bytes + 512u * unsigned(i2)), 0, 0);
+        const half4 a = __builtin_bit_cast(half4, raw);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[i2][j] = float(a[i2][j]);
+        for (int j = 0; j < 4; ++j) v[i2][j] = float(a[j]);
+    }
 #pragma unroll
     for (int b = 0; b < LOG_N; ++b) {
         if (b < 2 || b >= 8) {  // both elements of a pair in this lane's registers
@@ -122,12 +136,14 @@ __device__ __forceinline__ void stage_ordered_tile(const half4 (&a)[16], unsigne
             const int m = b < 4 ? 16 << (b - 2) : 1 << (b - 4);
             const bool upper = (lane & unsigned(m)) != 0u;
 #pragma unroll
-            for (int i2 = 0; i2 < 16; ++i2)
+            for (int i2 = 0; i2 < 16; ++i2) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float other = __shfl_xor(v[i2][j], m);
                     v[i2][j] = upper ? other - v[i2][j] : v[i2][j] + other;
                 }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
 #pragma unroll
@@ -139,14 +155,17 @@ __device__ __forceinline__ void stage_ordered_tile(const half4 (&a)[16], unsigne
 }
 
 template <int LOG_N>
-__global__ __launch_bounds__(64 * kWavesPerBlock) void fwht_mfma_kernel(const __half* __restrict__ input,
-                                                                        __half* output, std::uint64_t total,
-                                                                        float norm, float scale) {
+__global__ __launch_bounds__(64 * kWavesPerBlock) __attribute__((amdgpu_waves_per_eu(4))) void fwht_mfma_kernel(
+    const __half* __restrict__ input, __half* output, std::uint64_t total, float norm, float scale) {
     constexpr int t0 = LOG_N < 4 ? LOG_N : 4;                        // transform bits among 0..3
     constexpr int t1 = LOG_N <= 4 ? 0 : (LOG_N < 8 ? LOG_N - 4 : 4);  // among 4..7
     constexpr int t2 = LOG_N <= 8 ? 0 : LOG_N - 8;                    // among 8..11
     const unsigned lane = threadIdx.x & 63u;
-    const std::uint64_t tile = std::uint64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    // The wave's tile, read back into scalar registers: the compiler treats
+    // threadIdx.x >> 6 as divergent, and a buffer resource built from it sat
+    // in vector registers, which wrapped every load and store in a
+    // readfirstlane loop.
+    const std::uint64_t tile = uniform(std::uint64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6));
     const std::uint64_t first = tile << kTileLog;
     if (first >= total) return;  // whole wave: no tile here
     // The tile's span (the last tile of a batch may be partial: the range
@@ -169,21 +188,28 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void fwht_mfma_kernel(const __
         const U2 raw = __builtin_amdgcn_raw_buffer_load_b64(src, int(lane_bytes + 512u * i2), 0, 0);
         a[i2] = __builtin_bit_cast(half4, raw);
     }
-    // Any inf or NaN in the wave's tile (exponent field all ones): the
-    // stage-ordered VALU transform, so rows stay independent. The branch is
-    // wave-uniform.
-    unsigned special = 0u;
+    // Any inf or NaN in the wave's tile (exponent field all ones, i.e. a
+    // half whose magnitude bits are 0x7c00 or more), from the per-half
+    // maxima of the magnitude bits (a tree of packed 16-bit maxima): such a
+    // tile runs the stage-ordered VALU transform instead, so rows stay
+    // independent. (Deciding after the contractions, to overlap this with the
+    // matrix cores, kept the inputs live across them and measured slower.)
+    using u16x2 = __attribute__((ext_vector_type(2))) unsigned short;
+    u16x2 mag[16];
 #pragma unroll
     for (int i2 = 0; i2 < 16; ++i2) {
         const U2 raw = __builtin_bit_cast(U2, a[i2]);
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            special |= unsigned((raw[w] & 0x7c00u) == 0x7c00u);
-            special |= unsigned((raw[w] & 0x7c000000u) == 0x7c000000u);
-        }
+        mag[i2] = __builtin_elementwise_max(__builtin_bit_cast(u16x2, raw[0] & 0x7fff7fffu),
+                                            __builtin_bit_cast(u16x2, raw[1] & 0x7fff7fffu));
     }
-    if (__any(int(special))) {
-        stage_ordered_tile<LOG_N>(a, lane, lane_bytes, dst, norm, scale);
+#pragma unroll
+    for (int span = 8; span >= 1; span >>= 1)
+#pragma unroll
+        for (int i2 = 0; i2 < span; ++i2) mag[i2] = __builtin_elementwise_max(mag[i2], mag[i2 + span]);
+    const bool special = mag[0][0] >= 0x7c00u || mag[0][1] >= 0x7c00u;
+    if (uniform(unsigned(__any(int(special)))) != 0u) {  // wave-uniform, and read into a scalar register so
+                                                          // the compiler branches rather than masking both paths
+        stage_ordered_tile<LOG_N>(src, lane, lane_bytes, dst, norm, scale);
         return;
     }
 
