@@ -14,6 +14,10 @@
 // two row passes instead: the rows of each 2^n0 x 2^n1 block transformed and
 // stored transposed, then the rows of the transposed block, stored back in
 // the original order (two HBM round trips where the transposes take four).
+// The transposing store writes segments of 2^(14 - n) elements for rows of
+// 2^n points; where an axis has 2^11 points or more (segments under 128
+// bytes) the block runs instead as column passes over axis 0 and a row pass
+// over axis 1 that stores whole rows (every segment 512 bytes or longer).
 //
 // FWHT needs none of this: the Sylvester Hadamard matrix of n0 * n1 points
 // is the Kronecker product H(n0) (x) H(n1), and the innermost-first axis
@@ -171,7 +175,16 @@ class CompositeExecutor final : public Executor {
         in_side_ = side(true, logs);
         out_side_ = side(false, logs);
         std::vector<std::string> names;
-        if (!flatten && r.op == Op::Fft && rank == 2) {
+        if (!flatten && r.op == Op::Fft && rank == 2 && std::max(logs[0], logs[1]) >= 11) {
+            // Axis 0 as column passes over each block, then the rows.
+            auto cols = make_fft_rank2_columns(axis_request(r.n, r.batch), logs[0]);
+            if (cols) {
+                columns_ = true;
+                children_.push_back(std::move(cols));
+                steps_.push_back(Step{false, 0, 0, 0, 0, 0});
+            }
+        }
+        if (!columns_ && !flatten && r.op == Op::Fft && rank == 2) {
             // Each axis as one row pass that stores its blocks transposed:
             // rows of the caller's layout, then rows of the transposed one,
             // which lands back in the original order. No transpose kernels.
@@ -186,7 +199,7 @@ class CompositeExecutor final : public Executor {
                 steps_.push_back(Step{false, 1, 0, 0, 0, 0});
             }
         }
-        if (transposing_) {
+        if (transposing_ || columns_) {
         } else if (flatten) {
             children_.push_back(plan_executor(axis_request(r.n, r.batch), sel));
             steps_.push_back(Step{false, 0, 0, 0, 0, 0});
@@ -228,10 +241,12 @@ class CompositeExecutor final : public Executor {
         algorithm = std::string(r.factored     ? "fwht-factored"
                                 : rank == 1    ? "zero-extended"
                                 : transposing_ ? "rank2-transposing"
+                                : columns_     ? "rank2-columns"
                                 : flatten      ? (rank == 2 ? "rank2-kronecker" : "rankN-kronecker")
                                                : (rank == 2 ? "rank2-transpose" : "rankN-composite")) +
                     "[" + joined + "]" + (direct_in_ ? "+direct-input" : "") + (direct_out_ ? "+direct-output" : "");
         reason = transposing_ ? "each axis one row pass with a transposing store (innermost axis first)"
+                 : columns_   ? "axis 0 as column passes over each block, then the rows stored in natural order"
                  : flatten    ? "FWHT of the flattened point count: H(n0 n1) = H(n0) (x) H(n1), same stage order"
                               : "one batched rank-1 plan per axis, innermost first, tiled transposes between";
         if (r.embedding) reason += "; sides zero-extended to / cut from the power-of-two extents";
@@ -240,7 +255,10 @@ class CompositeExecutor final : public Executor {
             .field("schema_version", 1u)
             .field("kind", "composition")
             .field("rank", rank)
-            .field("lowering", transposing_ ? "transposing-rows" : flatten ? "kronecker" : "transpose")
+            .field("lowering", transposing_ ? "transposing-rows"
+                               : columns_   ? "columns-then-rows"
+                               : flatten    ? "kronecker"
+                                            : "transpose")
             .field("zero_extended", r.embedding);
         w.begin_array("extents");
         for (auto e : r.extents) w.value(e);
@@ -257,6 +275,10 @@ class CompositeExecutor final : public Executor {
             if (s.transpose) {
                 w.field("step", "transpose").field("blocks", s.groups).field("rows", std::uint64_t{1} << s.log_rows)
                     .field("cols", std::uint64_t{1} << s.log_cols);
+            } else if (columns_) {
+                w.field("step", "axes");
+                w.begin_array("axes").value(0u).value(1u).end_array();
+                w.key("child").value_raw(children_[s.child]->mapping_json);
             } else {
                 w.field("step", "axis").field("axis", s.axis).key("child").value_raw(children_[s.child]->mapping_json);
             }
@@ -391,7 +413,7 @@ class CompositeExecutor final : public Executor {
     }
 
     Request r_;
-    bool transposing_ = false;
+    bool transposing_ = false, columns_ = false;
     bool direct_in_ = false, direct_out_ = false;
     NdSide in_side_, out_side_;
     std::vector<std::unique_ptr<Executor>> children_;

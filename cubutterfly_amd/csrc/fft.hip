@@ -42,6 +42,10 @@ struct FftArgs {
     const float2* twa;  // w^(4096 k), k < 4096
     const float2* twb;  // w^k, k < 4096
     std::uint32_t l1, l2;  // high / low index bits (l1 = 0: one pass)
+    // Column passes: the low cbits bits of the column index number
+    // independent transforms (the other axis of a rank-2 block) and stay out
+    // of the level twiddles; 0 for a one-dimensional transform.
+    std::uint32_t cbits;
     std::uint32_t rows, tiles;
     float scale;  // 1/n for the normalised inverse on the final store, else 1
     // Elements between consecutive transforms of the input / output buffer:
@@ -198,7 +202,10 @@ constexpr int digit_bits_for(int lb, bool single) { return single && lb >= 13 ? 
 // order and bit 1 writes the output in bit-reversed order (the DIF result's
 // own order, so the final store skips the reversal); for row passes, bit 2
 // reads the block's rows in natural order (a row-major 2^l1 x 2^l2 block
-// whose row transforms are written transposed: the rank-2 axis step).
+// whose row transforms are written transposed: the rank-2 axis step), and
+// bit 3 writes row k of the block's bit-reversed row order back as row k,
+// transformed, in natural order (the last step of a rank-2 transform whose
+// first axis ran as column passes).
 template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD = 0>
 struct FftPass {
     static constexpr int LB = LT + LI;
@@ -249,14 +256,15 @@ struct FftPass {
         } else {
             constexpr int ws = window<P>(), ds = digit_bits<P>();
             const std::uint32_t lo_rel = std::uint32_t(ws);
-            const std::uint32_t lo = COL ? a.l2 + lo_rel : lo_rel;
+            const std::uint32_t lo = COL ? a.l2 - a.cbits + lo_rel : lo_rel;
             const std::uint32_t h = lo + ds;
             const std::uint32_t i0 = index<tile_window<P>()>(t, 0);
             // Index bits below the digit: for columns, the low transform bits
-            // of the column index and the column; for rows, the low bits.
+            // of the column index and the column's transform bits (the column
+            // without its low cbits); for rows, the low bits.
             const std::uint32_t x0 = COL ? (i0 >> LI) : (i0 & ((1u << LT) - 1u));
             std::uint32_t jl = x0 & ((1u << lo_rel) - 1u);
-            if (COL) jl = (jl << a.l2) | (c0 + (i0 & ((1u << LI) - 1u)));
+            if (COL) jl = (jl << (a.l2 - a.cbits)) | ((c0 + (i0 & ((1u << LI) - 1u))) >> a.cbits);
             const std::uint32_t f = jl << (m - h);
             const __amdgpu_buffer_rsrc_t ta = make_rsrc(a.twa, 4096u * 8u), tb = make_rsrc(a.twb, 4096u * 8u);
             return cmul(buffer_load<float2>(ta, (f >> 12) * 8u), buffer_load<float2>(tb, (f & 4095u) * 8u));
@@ -429,7 +437,7 @@ struct FftPass {
     // 168.7 -> 156.4 us; on the 32-byte segments of 4096-point transposing
     // rows the hint measured 2.6x slower). Column passes write the
     // intermediate the next pass reads (nontemporal there: C3a 183 us).
-    static constexpr int kStoreAux = !COL && (SINGLE || LI >= 6) ? 2 : 0;
+    static constexpr int kStoreAux = !COL && (SINGLE || LI >= 6 || (ORD & 8) != 0) ? 2 : 0;
     static __device__ __forceinline__ void store_at(float2 x, __amdgpu_buffer_rsrc_t dst, std::uint32_t lane_bytes,
                                                     std::uint32_t reg_bytes) {
         if (kLaneOnly || reg_bytes < 4096u) buffer_store<float2, kStoreAux>(x, dst, lane_bytes + reg_bytes);
@@ -659,6 +667,11 @@ struct FftPass {
             // Bit-reversed output order is the DIF result's own order.
             i = ((ORD & 2) != 0 ? xp : brev(xp, LT)) | (rr << LT);
             off = (rr << LT) + xp;
+        } else if constexpr ((ORD & 8) != 0) {  // tile rows bitrev(k0 + rr) land on rows k0 + rr
+            const std::uint32_t xp = g & ((1u << LT) - 1u), rr = g >> LT;
+            const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
+            i = brev(xp, LT) | (rr << LT);
+            off = ((k0 + rr) << LT) + xp;
         } else {  // grid transpose: tile rows are bitrev(k0 + rr) of one transform
             const std::uint32_t rr = g & ((1u << LI) - 1u), cp = g >> LI;
             const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
@@ -912,6 +925,16 @@ void add_rows_natural() {
     registry()[Key{LT, 14 - LT, false, false, true, 4}] = &launch<LT, 14 - LT, false, false, true, 4>;
 }
 
+// Rank-2 blocks: column passes of 2^LT points over whole 2^14-point tiles,
+// and rows written back in natural order in 2^12-point tiles (a quarter of
+// the LDS each, so four workgroups per CU overlap one another's loads and
+// butterflies where the rows of 2^9 points and more have no prefetching walk).
+template <int LT>
+void add_rank2_rows() {
+    registry()[Key{LT, 12 - LT, false, false, false, 8}] = &launch<LT, 12 - LT, false, false, false, 8>;
+    registry()[Key{LT, 12 - LT, false, false, true, 8}] = &launch<LT, 12 - LT, false, false, true, 8>;
+}
+
 void register_all() {
     add<1, single_li(1), false, true>();
     add<2, single_li(2), false, true>();
@@ -946,6 +969,14 @@ void register_all() {
     add_rows_natural<10>();
     add_rows_natural<11>();
     add_rows_natural<12>();
+    add<4, 10, true, false>();
+    add<5, 9, true, false>();
+    add<6, 8, true, false>();
+    add_rank2_rows<8>();
+    add_rank2_rows<9>();
+    add_rank2_rows<10>();
+    add_rank2_rows<11>();
+    add_rank2_rows<12>();
 }
 
 Launch lookup(const Key& k) {
@@ -1275,6 +1306,106 @@ class FftRowsTransposedExecutor final : public Executor {
     DeviceBuffer twa_, twb_;
 };
 
+// Rank-2 FFTs of row-major 2^l0 x 2^l1 blocks (r.n = 2^(l0 + l1) points per
+// block, r.batch blocks): the axis-0 transform as one or two column passes
+// over each block (the low l1 bits of their column index number
+// independent transforms, FftArgs::cbits), then the rows: each row pass tile
+// gathers rows from the column passes' bit-reversed axis-0 order and writes
+// them back transformed, in natural order. Every pass reads and writes whole
+// segments of 2^(14 - t) columns or whole rows, where the transposing row
+// passes of the same blocks move 2^(14 - l1)-element segments.
+class FftRank2ColumnsExecutor final : public Executor {
+  public:
+    FftRank2ColumnsExecutor(const Request& r, std::uint32_t l0, std::uint32_t ta, std::uint32_t tb) {
+        const std::uint32_t l1 = r.log_n - l0;
+        upload_twiddles(twa_, twb_, int(r.log_n), r.inverse);
+        FftArgs base{};
+        base.twa = twa_.as<float2>();
+        base.twb = twb_.as<float2>();
+        base.scale = 1.0f;
+        const std::uint64_t n = r.n;
+        // First column pass: the top ta bits of axis 0, columns = the rest of
+        // the block (tb axis-0 bits, then l1 bits that are not transformed).
+        {
+            const int li = 14 - int(ta);
+            Step s{find(Key{int(ta), li, true, false, r.inverse}), base, false, true};
+            s.args.l1 = ta;
+            s.args.l2 = tb + l1;
+            s.args.cbits = l1;
+            s.args.rows = unsigned(r.batch << ta);
+            s.args.tiles = unsigned(r.batch << (tb + l1 - std::uint32_t(li)));
+            s.args.in_pitch = s.args.out_pitch = n;
+            steps_.push_back(s);
+        }
+        if (tb > 0) {
+            // Second column pass, in place: 2^ta transforms of 2^tb points per
+            // block, each over 2^l1 columns; its own tables (level twiddles
+            // of a 2^(tb + l1)-point span).
+            upload_twiddles(sub_twa_, sub_twb_, int(tb + l1), r.inverse);
+            const int li = 14 - int(tb);
+            Step s{find(Key{int(tb), li, true, false, r.inverse}), base, true, true};
+            s.args.twa = sub_twa_.as<float2>();
+            s.args.twb = sub_twb_.as<float2>();
+            s.args.l1 = tb;
+            s.args.l2 = l1;
+            s.args.cbits = l1;
+            s.args.rows = unsigned((r.batch << ta) << tb);
+            s.args.tiles = unsigned((r.batch << ta) << (l1 - std::uint32_t(li)));
+            s.args.in_pitch = s.args.out_pitch = std::uint64_t{1} << (tb + l1);
+            steps_.push_back(s);
+        }
+        {
+            const int li = 12 - int(l1);
+            Step s{find(Key{int(l1), li, false, false, r.inverse, 8}), base, true, false};
+            s.args.l1 = l0;
+            s.args.l2 = l1;
+            s.args.rows = unsigned(r.batch << l0);
+            s.args.tiles = unsigned(r.batch << (l0 - std::uint32_t(li)));
+            s.args.scale = r.normalize ? 1.0f / float(n) : 1.0f;
+            s.args.in_pitch = s.args.out_pitch = n;
+            steps_.push_back(s);
+        }
+        workspace_ = static_cast<std::size_t>(r.batch * n) * sizeof(float2);
+        algorithm = "fft-c64-rank2-columns-r16";
+        reason = "axis 0 (2^" + std::to_string(l0) + ") as " + (tb > 0 ? "two column passes" : "one column pass") +
+                 " over each block, then the 2^" + std::to_string(l1) + "-point rows, stored in natural order";
+        json::Writer w;
+        w.begin_object()
+            .field("schema_version", 1u)
+            .field("operator", "fft")
+            .field("algorithm", algorithm)
+            .field("log_n", r.log_n)
+            .field("axis0_bits", l0)
+            .field("column_passes", tb > 0 ? 2u : 1u)
+            .field("blocks", r.batch)
+            .field("direction", r.inverse ? "inverse" : "forward")
+            .field("workspace_bytes", std::uint64_t(workspace_))
+            .end_object();
+        mapping_json = w.str();
+    }
+    std::size_t workspace_bytes() const override { return workspace_; }
+    void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
+        require(ws != nullptr, "a rank-2 column plan needs its workspace");
+        for (const auto& s : steps_) {
+            FftArgs a = s.args;
+            a.in = static_cast<const float2*>(s.reads_ws ? ws : in);
+            a.out = static_cast<float2*>(s.writes_ws ? ws : out);
+            s.fn(a, stream);
+            hip_check(hipGetLastError(), "FFT pass launch");
+        }
+    }
+
+  private:
+    struct Step {
+        Launch fn;
+        FftArgs args;
+        bool reads_ws, writes_ws;
+    };
+    DeviceBuffer twa_, twb_, sub_twa_, sub_twb_;
+    std::vector<Step> steps_;
+    std::size_t workspace_ = 0;
+};
+
 }  // namespace
 
 std::unique_ptr<Executor> make_fft_rows_transposed(const Request& r, std::uint32_t l1) {
@@ -1287,6 +1418,26 @@ std::unique_ptr<Executor> make_fft_rows_transposed(const Request& r, std::uint32
     const Launch fn = lookup(Key{l2, 14 - l2, false, false, r.inverse, 4});
     if (fn == nullptr) return nullptr;
     return std::make_unique<FftRowsTransposedExecutor>(r, l1, fn);
+}
+
+std::unique_ptr<Executor> make_fft_rank2_columns(const Request& r, std::uint32_t l0) {
+    const std::uint32_t m = r.log_n;
+    if (l0 < 4 || l0 >= m) return nullptr;
+    const std::uint32_t l1 = m - l0;
+    // Rows of 2^8 .. 2^12 points (whole 2^14-point row tiles within a block),
+    // blocks of at most 2^24 points (the level-twiddle tables' reach), and
+    // axis 0 in one column pass of 4 .. 8 bits or two: the second over tb >= 14 - l1
+    // bits (its 2^(14 - tb) columns within the 2^l1 of a row), the first over
+    // the rest, each within 4 .. 8 bits.
+    if (l1 < 8 || l1 > 12 || m > 24 || l0 < 14 - l1) return nullptr;
+    std::uint32_t ta = l0, tb = 0;
+    if (l0 > 8) {
+        tb = std::max(l0 / 2, 14 - l1);
+        ta = l0 - tb;
+        if (tb > 8 || ta < 4 || ta > 8) return nullptr;
+    }
+    if (r.batch > (0xffffffffull >> l0)) return nullptr;
+    return std::make_unique<FftRank2ColumnsExecutor>(r, l0, ta, tb);
 }
 
 // One-pass lengths have one lowering; two-pass lengths add the neighbouring

@@ -27,6 +27,10 @@ std::unique_ptr<Executor> make_fwht_mfma_executor(const Request& r);
 // (r.batch rows in all), each block's result stored transposed; null where
 // no kernel covers the shape.
 std::unique_ptr<Executor> make_fft_rows_transposed(const Request& r, std::uint32_t l1);
+// Rank-2 FFTs of row-major 2^l0 x 2^(r.log_n - l0) blocks (r.batch blocks of
+// r.n points): axis 0 as column passes, then the rows in natural order; null
+// where no kernel covers the shape.
+std::unique_ptr<Executor> make_fft_rank2_columns(const Request& r, std::uint32_t l0);
 std::vector<std::string> fft_candidates(const Request& r);
 std::vector<std::string> ntt_candidates(const Request& r);
 

@@ -160,7 +160,7 @@ def test_mapping_reports_children(torch_gpu, lib):
         assert plan.workspace_size() == m["workspace_bytes"] >= 2 * 2 * 64 * (1 << 13) * 8
 
 
-@pytest.mark.parametrize("extents", [(256, 256), (1024, 512), (4096, 16), (16, 4096)])
+@pytest.mark.parametrize("extents", [(256, 256), (1024, 512), (4096, 16), (512, 1024)])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_fft_transposing_rows(torch_gpu, lib, stream, extents, inverse):
     # Two row passes with transposing stores, no transpose kernels.
@@ -174,6 +174,47 @@ def test_fft_transposing_rows(torch_gpu, lib, stream, extents, inverse):
         assert plan.workspace_size() == batch * extents[0] * extents[1] * 8  # one intermediate
     got = run_plan(torch_gpu, lib, t, x, stream).astype(np.complex128)
     ref = (np.fft.ifftn if inverse else np.fft.fftn)(x.astype(np.complex128), axes=(1, 2))
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
+
+
+# Axes of 2^11 points or more: axis 0 as one column pass (2^4 .. 2^8 points)
+# or two (the split of 2^9 .. 2^16), then the rows stored in natural order.
+@pytest.mark.parametrize("extents,batch,inverse", [
+    ((4096, 4096), 1, False),
+    ((4096, 4096), 1, True),
+    ((2048, 4096), 1, False),
+    ((4096, 2048), 1, True),
+    ((16, 4096), 3, False),     # one 4-bit column pass
+    ((256, 2048), 2, True),     # one 8-bit column pass
+    ((512, 4096), 2, False),    # 5 + 4 bits
+    ((8192, 1024), 1, True),    # 7 + 6 bits
+    ((65536, 256), 1, False),   # 8 + 8 bits, 256-point rows
+])
+def test_fft_rank2_columns(torch_gpu, lib, stream, extents, batch, inverse):
+    x = data((batch,) + extents, np.complex64, 10)
+    t = fft_t(extents, batch, inverse=inverse)
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name() == "rank2-columns[fft-c64-rank2-columns-r16]+direct-input+direct-output"
+        m = plan.mapping()
+        assert m["lowering"] == "columns-then-rows"
+        assert [s["step"] for s in m["schedule"]] == ["axes"]
+        child = m["schedule"][0]["child"]
+        assert child["axis0_bits"] == int(np.log2(extents[0]))
+        assert child["column_passes"] == (1 if extents[0] <= 256 else 2)
+        assert plan.workspace_size() == batch * extents[0] * extents[1] * 8  # one intermediate
+    got = run_plan(torch_gpu, lib, t, x, stream).astype(np.complex128)
+    ref = (np.fft.ifftn if inverse else np.fft.fftn)(x.astype(np.complex128), axes=(1, 2))
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
+
+
+def test_fft_rank2_columns_in_place_unnormalised(torch_gpu, lib, stream):
+    extents, batch = (2048, 4096), 1
+    x = data((batch,) + extents, np.complex64, 11)
+    t = fft_t(extents, batch, inverse=True, normalize_inverse=False, placement=cb.Placement.IN_PLACE)
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name().startswith("rank2-columns[")
+    got = run_plan(torch_gpu, lib, t, x, stream, in_place=True).astype(np.complex128)
+    ref = np.fft.ifftn(x.astype(np.complex128), axes=(1, 2)) * (extents[0] * extents[1])
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
 
 
