@@ -218,6 +218,37 @@ def test_fft_rank2_columns_in_place_unnormalised(torch_gpu, lib, stream):
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
 
 
+def test_fft_rank2_columns_strided_sides(torch_gpu, lib, stream):
+    # Pitched rows on both sides: gather into packed order, the column plan,
+    # scatter; the gaps between rows stay untouched.
+    n0, n1, batch, pitch = 2048, 2048, 1, 2048 + 16
+    span = (batch * n0 - 1) * pitch + n1
+    rng = np.random.default_rng(12)
+    flat = (rng.standard_normal(span) + 1j * rng.standard_normal(span)).astype(np.complex64)
+    t = fft_t((n0, n1), batch, input_strides=[pitch, 1], input_batch_stride=n0 * pitch,
+              output_strides=[pitch, 1], output_batch_stride=n0 * pitch)
+    with cb.Plan(lib, t) as plan:
+        name = plan.algorithm_name()
+        assert name.startswith("rank2-columns[") and "+direct" not in name
+    x = to_device(torch_gpu, flat)
+    y = to_device(torch_gpu, np.full(span, 7 + 7j, np.complex64))
+    with cb.Plan(lib, t, stream=stream) as plan:
+        ws_bytes = plan.workspace_size()
+        ws = torch_gpu.empty(ws_bytes, dtype=torch_gpu.uint8, device="cuda")
+        plan.set_workspace(ws, ws_bytes)
+        plan.execute(x, y)
+        torch_gpu.cuda.synchronize()
+    got = to_host(torch_gpu, y, np.complex64)
+    rows = np.stack([flat[k * pitch: k * pitch + n1] for k in range(n0)])
+    ref = np.fft.fftn(rows.astype(np.complex128))
+    got_rows = np.stack([got[k * pitch: k * pitch + n1] for k in range(n0)]).astype(np.complex128)
+    assert np.linalg.norm(got_rows - ref) / np.linalg.norm(ref) <= 1e-5
+    gaps = np.ones(span, bool)
+    for k in range(n0):
+        gaps[k * pitch: k * pitch + n1] = False
+    assert np.all(got[gaps] == np.complex64(7 + 7j))
+
+
 def test_fft_transposing_rows_strided_in_place(torch_gpu, lib, stream):
     # In place on pitched rows: gather, the two row passes, scatter.
     n0, n1, batch, pitch = 256, 256, 2, 256 + 8

@@ -2,7 +2,7 @@
 times, with eager work between replays, match their eager results on every
 replay: one-, two- and three-pass FFT, one- and two-pass NTT, FWHT (packed and
 pitched; the lane-swap and MFMA lowerings too), a semantic-boundary plan and
-a rank-2 composition. Execution
+rank-2 compositions (transposing rows, column passes). Execution
 allocates nothing and records no memset, so capture is legal for every plan
 (reference execution semantics, docs/c_api.md:29-33)."""
 import numpy as np
@@ -45,6 +45,7 @@ CASES = {
                           output_batch_stride=1040), np.float32, 7 * 1040 + 1024),
     "boundary": (fft(256, 6, input_strides=[6], input_batch_stride=1), np.complex64, 6 * 256),
     "rank2": (fft([64, 128], 2), np.complex64, 2 * 64 * 128),
+    "rank2-columns": (fft([512, 2048], 2), np.complex64, 2 * 512 * 2048),
     "fwht-fp16-lanes": (fwht16(128, 4096 + 7), np.float16, (4096 + 7) * 128),
     "fwht-fp32-lanes": (fwht(256, 300), np.float32, 300 * 256),
     "fwht-fp16-mfma": (fwht16(4096, 64, arithmetic_policy=cb.ArithmeticPolicy.ALLOW_FP16_MMA), np.float16, 1 << 18),
