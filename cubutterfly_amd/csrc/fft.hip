@@ -154,9 +154,9 @@ constexpr int digit_bits_for(int lb, bool single);
 // FftPass::logical_thread) also rotate the column index (bit 0 to the top),
 // so a 16-lane group's columns 2c + h, c consecutive, land on 16 distinct
 // 8-byte bank pairs again instead of 8 (checked by enumeration).
-template <bool COL, int LT, int LI, bool SINGLE, bool PAIRED = false>
+template <bool COL, int LT, int LI, bool SINGLE, bool PAIRED = false, int DBX = 0>
 struct FftLds {
-    static constexpr int DB = digit_bits_for(LT + LI, SINGLE);
+    static constexpr int DB = DBX ? DBX : digit_bits_for(LT + LI, SINGLE);
     static constexpr bool kXor = SINGLE && LI == 0 && LT >= DB + 8;
     // Row layouts are sums of terms over disjoint index bit fields, so
     // addr(a | b) = addr(a) + addr(b) for disjoint a, b; the XOR layout is
@@ -194,6 +194,9 @@ struct FftLds {
 // slower with 5-bit digits and prefetching (their 32-byte column segments,
 // not the VALU, bound them), so they keep the 4-bit layout.
 constexpr int digit_bits_for(int lb, bool single) { return single && lb >= 13 ? 5 : 4; }
+// A pass's digit width: ORD bit 4 asks one-pass tiles of 2^13 / 2^14 points
+// for 4-bit digits (16 values per thread, twice the threads per tile).
+constexpr int pass_digit_bits(int lb, bool single, int ord) { return (ord & 16) ? 4 : digit_bits_for(lb, single); }
 
 // One FFT pass over LT transform bits. COL: high bits, tile of 2^LI columns;
 // ROW: low bits, tile of 2^LI rows (the final pass, storing in natural order);
@@ -205,19 +208,22 @@ constexpr int digit_bits_for(int lb, bool single) { return single && lb >= 13 ? 
 // whose row transforms are written transposed: the rank-2 axis step), and
 // bit 3 writes row k of the block's bit-reversed row order back as row k,
 // transformed, in natural order (the last step of a rank-2 transform whose
-// first axis ran as column passes).
+// first axis ran as column passes). Bit 4 gives one-pass tiles of 2^13 and
+// 2^14 points 4-bit digits (pass_digit_bits).
 template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD = 0>
 struct FftPass {
     static constexpr int LB = LT + LI;
-    static constexpr int DB = digit_bits_for(LB, SINGLE);
+    static constexpr int DB = pass_digit_bits(LB, SINGLE, ORD);
     static constexpr int kE = 1 << DB;
     static constexpr std::uint32_t T = 1u << (LB - DB);
     static constexpr int kPhases = (LT + DB - 1) / DB;
     // Prefetching needs registers for two tiles: with 16 values per thread
-    // that fits the 128-register budget for passes of at most two digits.
-    static constexpr bool kPrefetch = DB == 5 || kPhases <= 2;
+    // that fits the 128-register budget for passes of at most two digits,
+    // and for the 4-bit one-pass tiles of 2^13 / 2^14 points, whose bases
+    // beyond the third are fetched digit by digit.
+    static constexpr bool kPrefetch = DB == 5 || kPhases <= 2 || (ORD & 16) != 0;
     static constexpr bool kPairedColumns = COL && LI == 6 && kE == 16;
-    using L = FftLds<COL, LT, LI, SINGLE, kPairedColumns>;
+    using L = FftLds<COL, LT, LI, SINGLE, kPairedColumns, DB>;
 
     template <int P>
     static constexpr int window() {  // transform-relative register window start
@@ -841,8 +847,8 @@ struct FftPass {
 };
 
 template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD>
-__global__ __launch_bounds__(1 << (LT + LI - digit_bits_for(LT + LI, SINGLE)))
-__attribute__((amdgpu_waves_per_eu(digit_bits_for(LT + LI, SINGLE) == 5 ? 2 : 4))) void fft_pass_kernel(FftArgs a) {
+__global__ __launch_bounds__(1 << (LT + LI - pass_digit_bits(LT + LI, SINGLE, ORD)))
+__attribute__((amdgpu_waves_per_eu(pass_digit_bits(LT + LI, SINGLE, ORD) == 5 ? 2 : 4))) void fft_pass_kernel(FftArgs a) {
     FftPass<LT, LI, COL, SINGLE, INV, ORD>::run(a);
 }
 
@@ -862,7 +868,8 @@ struct Key {
 // multiple of 8 when larger. Other passes launch one workgroup per tile.
 template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD>
 void launch(const FftArgs& a, hipStream_t stream) {
-    constexpr std::uint32_t bytes = FftLds<COL, LT, LI, SINGLE>::kWords * sizeof(float2);
+    constexpr std::uint32_t bytes =
+        FftLds<COL, LT, LI, SINGLE, false, FftPass<LT, LI, COL, SINGLE, INV, ORD>::DB>::kWords * sizeof(float2);
     constexpr int threads = int(FftPass<LT, LI, COL, SINGLE, INV, ORD>::T);
     static const std::uint64_t resident = [] {
         const void* fn = reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, SINGLE, INV, ORD>);
@@ -950,6 +957,12 @@ void register_all() {
     add<12, single_li(12), false, true>();
     add<13, 0, false, true>();
     add<14, 0, false, true>();
+    for (bool inv : {false, true}) {
+        registry()[Key{13, 0, false, true, inv, 16}] = inv ? &launch<13, 0, false, true, true, 16>
+                                                           : &launch<13, 0, false, true, false, 16>;
+        registry()[Key{14, 0, false, true, inv, 16}] = inv ? &launch<14, 0, false, true, true, 16>
+                                                           : &launch<14, 0, false, true, false, 16>;
+    }
     add_two<15>();
     add_two<16>();
     add_two<17>();
@@ -1083,8 +1096,9 @@ std::string order_suffix(const Request& r) {
 class FftExecutor final : public Executor {
   public:
     // split: column bits of a two-pass lowering (0: one pass); mid > 0: the
-    // middle bits of a three-pass lowering with `split` top bits.
-    FftExecutor(const Request& r, int split, int mid = 0) : r_(r) {
+    // middle bits of a three-pass lowering with `split` top bits; radix16: a
+    // one-pass tile of 2^13 / 2^14 points with 4-bit digits.
+    FftExecutor(const Request& r, int split, int mid = 0, bool radix16 = false) : r_(r) {
         const std::uint32_t m = r.log_n;
         supported(m >= 1 && m <= 24, "complex FFT lengths above 2^24 are not yet lowered for gfx950");
         upload_twiddles(twa_, twb_, int(m), r.inverse);
@@ -1139,7 +1153,7 @@ class FftExecutor final : public Executor {
         } else if (split == 0) {
             const int li = single_li(int(m));
             const std::uint64_t tiles = (r.batch + (1ull << li) - 1) >> li;
-            const int ord = (r.input_bit_reversed ? 1 : 0) | (r.output_bit_reversed ? 2 : 0);
+            const int ord = (r.input_bit_reversed ? 1 : 0) | (r.output_bit_reversed ? 2 : 0) | (radix16 ? 16 : 0);
             Step s{find(Key{int(m), li, false, true, r.inverse, ord}), base, false, false};
             s.args.l1 = 0;
             s.args.l2 = m;
@@ -1148,7 +1162,7 @@ class FftExecutor final : public Executor {
             s.args.in_pitch = in_pitch;
             s.args.out_pitch = out_pitch;
             steps_.push_back(s);
-            algorithm = m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16";
+            algorithm = m >= 13 && !radix16 ? "fft-c64-resident-r32" : "fft-c64-resident-r16";
         } else {
             const std::uint32_t l1 = std::uint32_t(split), l2 = m - l1;
             const int col_li = col_lines(int(l1), int(l2));
@@ -1237,9 +1251,14 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r) {
         variant.resize(variant.size() - suffix.size());
     }
     if (m <= 14) {
-        supported(variant.empty() || variant == (m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16"),
+        // 2^13 / 2^14 points: radix-32 tiles by default, radix-16 by name
+        // (natural orders only).
+        const bool radix16 = m >= 13 && variant == "fft-c64-resident-r16";
+        supported(variant.empty() || radix16 || variant == (m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16"),
                   "'" + r.variant + "' is not a lowering of this FFT");
-        return std::make_unique<FftExecutor>(r, 0);
+        supported(!radix16 || !(r.input_bit_reversed || r.output_bit_reversed),
+                  "radix-16 tiles of 2^13 / 2^14 points take natural orders only");
+        return std::make_unique<FftExecutor>(r, 0, 0, radix16);
     }
     int top = 0, mid = 0;
     if (variant.empty() && default_three_pass(m, r.inverse, top, mid)) return std::make_unique<FftExecutor>(r, top, mid);
@@ -1445,7 +1464,12 @@ std::unique_ptr<Executor> make_fft_rank2_columns(const Request& r, std::uint32_t
 std::vector<std::string> fft_candidates(const Request& r) {
     const int m = int(r.log_n);
     const std::string suffix = order_suffix(r) + (r.pitched ? "-pitched" : "");
-    if (m <= 14) return {std::string(m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16") + suffix};
+    if (m <= 14) {
+        std::vector<std::string> names{std::string(m >= 13 ? "fft-c64-resident-r32" : "fft-c64-resident-r16") + suffix};
+        if (m >= 13 && !(r.input_bit_reversed || r.output_bit_reversed))
+            names.push_back("fft-c64-resident-r16" + suffix);
+        return names;
+    }
     std::vector<std::string> names;
     int top = 0, mid = 0;
     const bool three = default_three_pass(m, r.inverse, top, mid);

@@ -86,7 +86,7 @@ def test_measure_records_and_default_replays(torch_gpu, lib, stream, tmp_path):
         assert plan.selection_source() == cb.SelectionSource.STATIC_MODEL
 
 
-@pytest.mark.parametrize("log_n", [15, 16, 18, 20, 22, 23, 24])
+@pytest.mark.parametrize("log_n", [13, 14, 15, 16, 18, 20, 22, 23, 24])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_every_fft_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path, log_n, inverse):
     batch = 1 << max(0, 18 - log_n)
@@ -94,8 +94,13 @@ def test_every_fft_candidate_matches_the_oracle(torch_gpu, lib, stream, tmp_path
     with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream,
                  cache_path=tmp_path / "c.tsv") as plan:
         names = measured(plan)
-    # The static model's choice comes first: three passes from 2^23.
-    assert names[0].startswith("fft-c64-three-pass-r16" if log_n >= 23 else "fft-c64-two-pass-r16")
+    # The static model's choice comes first: radix-32 one-pass tiles up to
+    # 2^14 (radix-16 tiles are the other candidate), three passes from 2^23.
+    first = ("fft-c64-resident-r32" if log_n <= 14 else
+             "fft-c64-three-pass-r16" if log_n >= 23 else "fft-c64-two-pass-r16")
+    assert names[0].startswith(first)
+    if log_n <= 14:
+        assert names == ["fft-c64-resident-r32", "fft-c64-resident-r16"]
     for name in names:
         opts = {"algorithm": name}
         with cb.Plan(lib, t, **opts) as plan:
