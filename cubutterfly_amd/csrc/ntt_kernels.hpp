@@ -316,13 +316,31 @@ __device__ __forceinline__ std::uint32_t phase_index(std::uint32_t t, std::uint3
 // Padded LDS image of a tile. Column tiles that stage a bit-reversed boundary
 // also swizzle the column by the top transform bits (lanes then walk rows in
 // bit-reversed order, which a plain stride maps onto few banks).
-template <bool COL, bool SWZ, int LT, int LI>
+//
+// Row tiles of 2^8-point rows in 4-byte words (BANKED) give each row bit its
+// own offset instead of one row pitch: 272, 545, 1090, 2180, 4360 words,
+// which are 16, 1, 2, 4, 8 modulo the 32 four-byte banks, at least 272 words
+// apart (a row spans 271). A 32-lane half of every access these tiles make
+// then covers 32 distinct banks: the exchanges' phase layouts (lanes over
+// index bits 4-8, or 0-3 and 8) and the staged boundary permutation (lanes
+// over the row bits and index bit 7), where the single pitch of 273 words
+// (17 modulo 32) put two lanes on each bank (4 conflict cycles per ds_*2_b32
+// instruction, measured, and reproduced by enumerating the accesses).
+template <bool COL, bool SWZ, int LT, int LI, bool BANKED = false>
 struct Lds {
+    static_assert(!BANKED || (!COL && LT == 8 && LI <= 5), "banked row offsets cover 2^8-point rows, up to 32");
+    // Row bit j > 0 contributes 545 * 2^(j - 1): the bits above bit 0 are
+    // one multiple of 545.
+    static __host__ __device__ constexpr std::uint32_t row_offset(std::uint32_t rr) {
+        return 272u * (rr & 1u) + 545u * (rr >> 1);
+    }
     // Without the swizzle, addr() is a sum of terms over disjoint index bit
     // fields, so addr(a | b) = addr(a) + addr(b) for disjoint a, b.
     static constexpr bool kLinear = !(COL && SWZ);
     static constexpr std::uint32_t kWords =
-        COL ? (1u << LT) * ((1u << LI) + 1u) : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
+        COL      ? (1u << LT) * ((1u << LI) + 1u)
+        : BANKED ? row_offset((1u << LI) - 1u) + (1u << LT) + (1u << LT >> 4) - 1u
+                 : (1u << LI) * ((1u << LT) + (1u << LT >> 4) + 1u);
     static __device__ __forceinline__ std::uint32_t addr(std::uint32_t i) {
         if constexpr (COL) {
             const std::uint32_t cc = i & ((1u << LI) - 1u), x = i >> LI;
@@ -332,6 +350,9 @@ struct Lds {
             } else {
                 return x * ((1u << LI) + 1u) + cc;
             }
+        } else if constexpr (BANKED) {
+            const std::uint32_t x = i & ((1u << LT) - 1u), rr = i >> LT;
+            return row_offset(rr) + x + (x >> 4);
         } else {
             const std::uint32_t x = i & ((1u << LT) - 1u), rr = i >> LT;
             return rr * ((1u << LT) + (1u << LT >> 4) + 1u) + x + (x >> 4);
@@ -366,7 +387,7 @@ struct Pass {
     // Rows of a permuted two-pass ROW tile are bitrev(k0 + rr).
     static constexpr bool kPermRows = !COL && !SINGLE && (PIN || POUT);
     static constexpr std::uint32_t kPolyBytes = std::uint32_t(sizeof(W)) << kLogN;
-    using L = Lds<COL, COL && (PIN || POUT), LT, LI>;
+    using L = Lds<COL, COL && (PIN || POUT), LT, LI, !COL && sizeof(W) == 4 && LT == 8 && LI <= 5>;
     // Stores of two-pass inverse (Gentleman-Sande) tiles write through the L2
     // (sc0 sc1), so the end-of-kernel write-back has little left to flush;
     // measured 5-6% faster per C2 / C4 step. Forward passes keep write-back
