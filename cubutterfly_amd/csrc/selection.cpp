@@ -304,14 +304,15 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     const std::size_t out_bytes = r.in_place ? 0 : r.span_bytes(false);
     const std::size_t footprint = in_bytes + out_bytes;
     // Buffer sets: transforms of 16 MiB or more rotate over enough sets that
-    // their footprint exceeds twice the 256 MB Infinity Cache (at most 8
-    // sets, so below 32 MiB part of the data stays cached), so candidates
+    // their inputs alone exceed twice the 256 MB Infinity Cache (nontemporal
+    // output stores do not evict earlier inputs from it; at most 16 sets, so
+    // below 32 MiB of input part of the data stays cached), so candidates
     // are timed at HBM speed as in steady use over large data. The search
     // stays within max(512 MiB, min(2 GiB, free / 4)) of scratch (the
     // reference's tuning budget); beyond it, fewer sets.
     constexpr std::size_t kCacheBytes = std::size_t{256} << 20;
     std::size_t sets = r.data_bytes() >= (std::size_t{16} << 20)
-                           ? std::min<std::size_t>(8, (2 * kCacheBytes) / footprint + 1)
+                           ? std::min<std::size_t>(16, (2 * kCacheBytes) / std::max<std::size_t>(in_bytes, 1) + 1)
                            : 1;
     std::size_t free_bytes = 0, total_bytes = 0;
     if (hipMemGetInfo(&free_bytes, &total_bytes) != hipSuccess) {

@@ -202,10 +202,10 @@ def test_plan_trace(torch_gpu, lib, stream, tmp_path, monkeypatch):
 
 def test_measure_rotates_large_buffers(torch_gpu, lib, stream, tmp_path, monkeypatch):
     # Transforms of 16 MiB or more are timed over rotating buffer sets whose
-    # footprint exceeds twice the 256 MB Infinity Cache (C3b's 128 MiB: 3
-    # sets); small ones on one set.
+    # inputs alone exceed twice the 256 MB Infinity Cache (C3b's 128 MiB
+    # input: 5 sets); small ones on one set.
     import json
-    for log_n, batch, sets in ((16, 2, 1), (14, 1024, 3)):
+    for log_n, batch, sets in ((16, 2, 1), (14, 1024, 5)):
         trace = tmp_path / f"trace{log_n}.jsonl"
         monkeypatch.setenv("CUBUTTERFLY_PLAN_TRACE", str(trace))
         with cb.Plan(lib, fft(log_n, batch), policy=cb.AlgorithmPolicy.MEASURE,
