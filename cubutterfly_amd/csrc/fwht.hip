@@ -566,8 +566,10 @@ __device__ __forceinline__ void wide_store_run(__amdgpu_buffer_rsrc_t r, unsigne
 // WALK: the next tile's loads are issued before the current tile's
 // butterflies (for grids smaller than the row count); without it each tile
 // is loaded when its turn comes, which needs no second register buffer.
-// FP16 storage only: with 32-bit words the two prefetch buffers and the
-// exchange registers exceed 128 VGPRs and spill.
+// WALK for FP16 storage only: with 32-bit words the two prefetch buffers and
+// the exchange registers exceed 128 VGPRs and spill. FP32 rows take the
+// one-tile form (a MEASURE candidate: C1 29.5 against 23.9 us for the
+// 16-register kernel).
 template <int LOG_N, class Io, bool WALK>
 __global__ __launch_bounds__(1 << (LOG_N - kLW), 4) void fwht_wide_kernel(const typename Io::T* __restrict__ input,
                                                                       typename Io::T* output, unsigned rows,
@@ -977,8 +979,15 @@ WideLaunch wide_table_entry(int log_n, std::integer_sequence<int, L...>) {
                                      wide_resident<L + 11, F16Io>}...};
     return table[log_n - 11];
 }
+// FP32 rows: no walking variant (two 32-word prefetch buffers spill).
+template <int... L>
+WideLaunch wide_table_entry_f32(int log_n, std::integer_sequence<int, L...>) {
+    WideLaunch table[] = {WideLaunch{launch_wide<L + 11, F32Io, false>, nullptr, nullptr}...};
+    return table[log_n - 11];
+}
 
-// The 32-register kernel: FP16 rows of 2^11 .. 2^13 points, row count within 32 bits.
+// The 32-register kernel: rows of 2^11 .. 2^13 points (FP16, and FP32 without
+// the walking form), row count within 32 bits.
 // For FP16 rows of 2^7 and 2^8 points, the short-row form of the same
 // lowering (fwht_short_kernel: 4096-element tiles of whole rows, one LDS
 // exchange, a tile's pitched span within 31-bit byte offsets), without a
@@ -986,7 +995,11 @@ WideLaunch wide_table_entry(int log_n, std::integer_sequence<int, L...>) {
 // stores with 16-byte gaps across the lanes, and it measured 64 us against
 // 47 us for C5b's volume; it is not offered there.
 WideLaunch wide_launcher(const Request& r) {
-    if (!r.fp16_final || r.batch > 0xffffffffull) return {};
+    if (r.batch > 0xffffffffull) return {};
+    if (!r.fp16_final) {
+        if (r.log_n < 11 || r.log_n > 13) return {};
+        return wide_table_entry_f32(int(r.log_n), std::make_integer_sequence<int, 3>{});
+    }
     if (r.log_n >= 7 && r.log_n <= 8) {
         const std::uint64_t rows_per_tile = std::uint64_t{1} << (12 - r.log_n);
         const std::uint64_t pitch = r.pitched ? std::max(r.in_batch_stride, r.out_batch_stride) : r.n;
@@ -1138,7 +1151,7 @@ std::vector<FwhtKind> fwht_kinds(const Request& r) {
     if (const WideLaunch wide = wide_launcher(r)) {
         kinds.push_back(FwhtKind::Wide);
         if (wide.walk) kinds.push_back(FwhtKind::WidePersistent);
-        if (r.log_n == 12) std::swap(kinds[0], kinds[1]);
+        if (r.log_n == 12 && r.fp16_final) std::swap(kinds[0], kinds[1]);
     }
     if (lane_launcher(r)) kinds.push_back(FwhtKind::Lanes);
     return kinds;
