@@ -102,7 +102,8 @@ def test_plans_without_workspace_and_oversized_plans(torch_gpu, lib, stream):
 
 
 def test_composite_embedding_and_boundary_plans_after_a_larger_plan(torch_gpu, lib, stream):
-    # Rank-2 FFT (row plan, transposes, workspace ping-pong buffers), the
+    # Rank-2 FFT (row plan, transposes, workspace ping-pong buffers; column
+    # passes and a natural-order row pass), the
     # zero-extended embedding (gather with zero fill, padded transform) and a
     # strided boundary plan, each run right after a larger plan filled the
     # shared array with non-zero data: no plan may read a word it did not
@@ -113,6 +114,12 @@ def test_composite_embedding_and_boundary_plans_after_a_larger_plan(torch_gpu, l
                                             compute=cb.ComputeType.FP32, batch=1), (64 << 13,), np.complex64),
         ("rank-2 fft 64 x 128, batch 2", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64, 128],
                                               compute=cb.ComputeType.FP32, batch=2), (2 * 64 * 128,), np.complex64),
+        ("rank-2 fft 16 x 4096, batch 2 (one column pass)",
+         cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [16, 4096], compute=cb.ComputeType.FP32, batch=2),
+         (2 * 16 * 4096,), np.complex64),
+        ("rank-2 fft 512 x 2048 (two column passes)",
+         cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [512, 2048], compute=cb.ComputeType.FP32, batch=1),
+         (512 * 2048,), np.complex64),
         ("zero-extended fft 3000 x 4", cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [3000],
                                                   compute=cb.ComputeType.FP32, batch=4,
                                                   length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING),
