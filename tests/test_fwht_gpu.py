@@ -60,29 +60,6 @@ def test_fp32_inverse_normalised_in_place(torch_gpu, lib, stream, log_n, batch):
     np.testing.assert_array_equal(raw.view(np.uint32), oracle.fwht_f32(x).view(np.uint32))
 
 
-@pytest.mark.parametrize("log_n,batch", [(11, 37), (12, 64), (12, 5), (13, 9)])
-def test_fp32_32_register_rows_bit_exact(torch_gpu, lib, stream, log_n, batch):
-    # The 32-register lowering over FP32 rows (by name): forward, normalised
-    # inverse in place, and pitched rows.
-    print(f"case fwht fp32 resident-r32 log_n={log_n} batch={batch}", flush=True)
-    n = 1 << log_n
-    x = random_floats(batch, n, seed=log_n * 31 + batch)
-    got = run_plan(torch_gpu, lib, fwht32(n, batch), x, stream, algorithm="fwht-fp32-resident-r32")
-    np.testing.assert_array_equal(got.view(np.uint32), oracle.fwht_f32(x).view(np.uint32))
-    t = fwht32(n, batch, inverse=True, placement=cb.Placement.IN_PLACE)
-    got = run_plan(torch_gpu, lib, t, x, stream, in_place=True, algorithm="fwht-fp32-resident-r32")
-    expected = oracle.fwht_f32(x, inverse=True, normalize=True)
-    np.testing.assert_array_equal(got.view(np.uint32), expected.view(np.uint32))
-    pitch = n + 64
-    flat = np.zeros((batch - 1) * pitch + n, np.float32)
-    for b in range(batch):
-        flat[b * pitch: b * pitch + n] = x[b]
-    t = fwht32(n, batch, input_strides=[1], input_batch_stride=pitch, output_strides=[1], output_batch_stride=pitch)
-    out = run_plan(torch_gpu, lib, t, flat, stream, algorithm="fwht-fp32-resident-r32-pitched")
-    rows = np.stack([out[b * pitch: b * pitch + n] for b in range(batch)])
-    np.testing.assert_array_equal(rows.view(np.uint32), oracle.fwht_f32(x).view(np.uint32))
-
-
 def check_fp16(got, expected):
     err = np.max(np.abs(got.astype(np.float32) - expected.astype(np.float32)))
     assert err <= 2e-3, f"max abs err {err}"

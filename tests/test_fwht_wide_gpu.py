@@ -1,8 +1,10 @@
-"""The 32-register FWHT lowering (`fwht-fp16-fp32-resident-r32`, FP16 rows
-of 2^11..2^13 points): bit-exact against the stage-ordered oracle (src/butterfly_reference.cpp:
-349-369; FP16 final-storage contract tests/test_fwht_final_storage.py:28-40)
-on packed and pitched rows, in and out of place, forward and normalised
-inverse, selected explicitly and by MEASURE."""
+"""The 32-register FWHT lowering (`fwht-fp16-fp32-resident-r32` for FP16
+rows of 2^11..2^13 points, `fwht-fp32-resident-r32` for FP32 rows of the
+same lengths, without the walking form): bit-exact against the stage-ordered
+oracle (src/butterfly_reference.cpp:349-369; FP16 final-storage contract
+tests/test_fwht_final_storage.py:28-40) on packed and pitched rows, in and
+out of place, forward and normalised inverse, selected explicitly and by
+MEASURE."""
 import json
 
 import numpy as np
@@ -48,7 +50,7 @@ def bits(a):
     return a.view(np.uint16 if a.dtype == np.float16 else np.uint32)
 
 
-@pytest.mark.parametrize("fp16", [True])
+@pytest.mark.parametrize("fp16", [True, False])
 @pytest.mark.parametrize("log_n", [11, 12, 13])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_packed(torch_gpu, lib, stream, fp16, log_n, inverse):
@@ -62,7 +64,7 @@ def test_packed(torch_gpu, lib, stream, fp16, log_n, inverse):
     np.testing.assert_array_equal(bits(got), bits(expected(x, log_n, fp16, inverse)))
 
 
-@pytest.mark.parametrize("fp16", [True])
+@pytest.mark.parametrize("fp16", [True, False])
 def test_in_place(torch_gpu, lib, stream, fp16):
     log_n, batch = 12, 97
     x = inputs(log_n, batch, fp16, seed=5)
@@ -71,7 +73,7 @@ def test_in_place(torch_gpu, lib, stream, fp16):
     np.testing.assert_array_equal(bits(got), bits(expected(x, log_n, fp16, False)))
 
 
-@pytest.mark.parametrize("fp16", [True])
+@pytest.mark.parametrize("fp16", [True, False])
 @pytest.mark.parametrize("log_n", [11, 13])
 def test_pitched(torch_gpu, lib, stream, fp16, log_n):
     n, batch = 1 << log_n, 41
@@ -109,12 +111,19 @@ def test_measure_lists_both_lowerings(torch_gpu, lib, stream, tmp_path):
                     "fwht-fp16-fp32-resident-r32-persistent")
 
 
-@pytest.mark.parametrize("log_n,fp16", [(10, True), (14, True), (12, False)])
+@pytest.mark.parametrize("log_n,fp16", [(10, True), (14, True), (10, False), (14, False)])
 def test_other_shapes_refuse_the_wide_lowering(lib, log_n, fp16):
-    # Only FP16 rows of 2^7, 2^8 (the short-row kernel) and 2^11..2^13 points
-    # (FP32 words would spill the registers).
+    # Only rows of 2^11..2^13 points, and FP16 rows of 2^7, 2^8 (the
+    # short-row kernel).
     with pytest.raises(cb.AbiError) as e:
         cb.Plan(lib, transform(log_n, 8, fp16), **explicit(wide_name(fp16)))
+    assert e.value.status == cb.Status.NOT_SUPPORTED
+
+
+def test_fp32_rows_refuse_the_walking_form(lib):
+    # Two 32-word prefetch buffers would spill the registers.
+    with pytest.raises(cb.AbiError) as e:
+        cb.Plan(lib, transform(12, 8, False), **explicit(wide_name(False).replace("-r32", "-r32-persistent")))
     assert e.value.status == cb.Status.NOT_SUPPORTED
 
 
