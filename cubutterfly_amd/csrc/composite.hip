@@ -18,6 +18,7 @@
 // 2^n points; where an axis has 2^11 points or more (segments under 128
 // bytes) the block runs instead as column passes over axis 0 and a row pass
 // over axis 1 that stores whole rows (every segment 512 bytes or longer).
+// Either lowering can be named (EXPLICIT) where its kernels cover the shape.
 //
 // FWHT needs none of this: the Sylvester Hadamard matrix of n0 * n1 points
 // is the Kronecker product H(n0) (x) H(n1), and the innermost-first axis
@@ -175,7 +176,13 @@ class CompositeExecutor final : public Executor {
         in_side_ = side(true, logs);
         out_side_ = side(false, logs);
         std::vector<std::string> names;
-        if (!flatten && r.op == Op::Fft && rank == 2 && std::max(logs[0], logs[1]) >= 11) {
+        // A rank-2 FFT named explicitly as one of its two lowerings takes that
+        // one (EXPLICIT); otherwise column passes from 2^11-point axes.
+        const bool named = r.policy == CUBUTTERFLY_ALGORITHM_EXPLICIT;
+        const bool want_columns = named && r.explicit_algorithm.rfind("rank2-columns[", 0) == 0;
+        const bool want_rows = named && r.explicit_algorithm.rfind("rank2-transposing[", 0) == 0;
+        if (!flatten && r.op == Op::Fft && rank == 2 && !want_rows &&
+            (want_columns || std::max(logs[0], logs[1]) >= 11)) {
             // Axis 0 as column passes over each block, then the rows.
             auto cols = make_fft_rank2_columns(axis_request(r.n, r.batch), logs[0]);
             if (cols) {
@@ -184,7 +191,7 @@ class CompositeExecutor final : public Executor {
                 steps_.push_back(Step{false, 0, 0, 0, 0, 0});
             }
         }
-        if (!columns_ && !flatten && r.op == Op::Fft && rank == 2) {
+        if (!columns_ && !want_columns && !flatten && r.op == Op::Fft && rank == 2) {
             // Each axis as one row pass that stores its blocks transposed:
             // rows of the caller's layout, then rows of the transposed one,
             // which lands back in the original order. No transpose kernels.

@@ -207,6 +207,34 @@ def test_fft_rank2_columns(torch_gpu, lib, stream, extents, batch, inverse):
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
 
 
+ROWS_NAME = "rank2-transposing[fft-c64-rows-transposed-r16,fft-c64-rows-transposed-r16]+direct-input+direct-output"
+COLUMNS_NAME = "rank2-columns[fft-c64-rank2-columns-r16]+direct-input+direct-output"
+
+
+@pytest.mark.parametrize("extents,batch,name", [
+    ((2048, 4096), 1, ROWS_NAME),     # the default there is column passes
+    ((1024, 512), 2, COLUMNS_NAME),   # the default there is transposing rows
+])
+def test_fft_rank2_lowering_by_name(torch_gpu, lib, stream, extents, batch, name):
+    x = data((batch,) + extents, np.complex64, 13)
+    t = fft_t(extents, batch)
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name() != name
+    with cb.Plan(lib, t, algorithm=name) as plan:
+        assert plan.algorithm_name() == name
+        assert plan.selection_source() == cb.SelectionSource.EXPLICIT
+    got = run_plan(torch_gpu, lib, t, x, stream, algorithm=name).astype(np.complex128)
+    ref = np.fft.fftn(x.astype(np.complex128), axes=(1, 2))
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
+
+
+def test_fft_rank2_columns_by_name_where_no_kernel_covers_it(lib):
+    # 16-point rows: no natural-order row tiles of that length.
+    with pytest.raises(cb.AbiError) as e:
+        cb.Plan(lib, fft_t((4096, 16), 1), algorithm=COLUMNS_NAME)
+    assert e.value.status == cb.Status.NOT_SUPPORTED
+
+
 def test_fft_rank2_columns_in_place_unnormalised(torch_gpu, lib, stream):
     extents, batch = (2048, 4096), 1
     x = data((batch,) + extents, np.complex64, 11)
