@@ -167,7 +167,9 @@ struct Step {
 
 class CompositeExecutor final : public Executor {
   public:
-    CompositeExecutor(const Request& r, bool flatten, Selection* sel) : r_(r) {
+    // force: 0 the static rule (or the name an EXPLICIT request gives), 1 a
+    // rank-2 FFT's column passes, 2 its transposing row passes.
+    CompositeExecutor(const Request& r, bool flatten, Selection* sel, int force = 0) : r_(r) {
         const std::uint32_t rank = r.rank;
         std::vector<std::uint32_t> logs(rank);
         for (std::uint32_t a = 0; a < rank; ++a) logs[a] = log2_u64(r.extents[a]);
@@ -179,8 +181,8 @@ class CompositeExecutor final : public Executor {
         // A rank-2 FFT named explicitly as one of its two lowerings takes that
         // one (EXPLICIT); otherwise column passes from 2^11-point axes.
         const bool named = r.policy == CUBUTTERFLY_ALGORITHM_EXPLICIT;
-        const bool want_columns = named && r.explicit_algorithm.rfind("rank2-columns[", 0) == 0;
-        const bool want_rows = named && r.explicit_algorithm.rfind("rank2-transposing[", 0) == 0;
+        const bool want_columns = force == 1 || (named && r.explicit_algorithm.rfind("rank2-columns[", 0) == 0);
+        const bool want_rows = force == 2 || (named && r.explicit_algorithm.rfind("rank2-transposing[", 0) == 0);
         if (!flatten && r.op == Op::Fft && rank == 2 && !want_rows &&
             (want_columns || std::max(logs[0], logs[1]) >= 11)) {
             // Axis 0 as column passes over each block, then the rows.
@@ -312,6 +314,9 @@ class CompositeExecutor final : public Executor {
         return used;
     }
 
+    bool columns() const { return columns_; }
+    bool transposing() const { return transposing_; }
+
     std::size_t workspace_bytes() const override {
         // The ping-pong buffers, then the largest child's workspace.
         return buffers() * align16(r_.data_bytes()) + align16(child_ws_);
@@ -347,9 +352,18 @@ class CompositeExecutor final : public Executor {
         if (!direct_out_) move(false, cur, out, count, out_side_, stream);
     }
 
+    // Whether a rank-2 FFT request has both lowerings (no device work).
+    static bool both_rank2_lowerings(const Request& r) {
+        const std::uint32_t l0 = log2_u64(r.extents[0]), l1 = log2_u64(r.extents[1]);
+        return fft_rank2_columns_available(axis_request_of(r, r.n, r.batch), l0) &&
+               fft_rows_transposed_available(axis_request_of(r, r.extents[1], r.batch * r.extents[0]), l0) &&
+               fft_rows_transposed_available(axis_request_of(r, r.extents[0], r.batch * r.extents[1]), l1);
+    }
+
   private:
-    Request axis_request(std::uint64_t n, std::uint64_t batch) const {
-        Request c = r_;
+    Request axis_request(std::uint64_t n, std::uint64_t batch) const { return axis_request_of(r_, n, batch); }
+    static Request axis_request_of(const Request& r, std::uint64_t n, std::uint64_t batch) {
+        Request c = r;
         c.rank = 1;
         c.extents.clear();
         c.in_strides.clear();
@@ -436,6 +450,42 @@ std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* s
             "composite plans need rank 2 to 8, the zero-extended embedding or a factored FWHT");
     // A flattened FWHT is one rank-1 plan; it exists up to the resident length.
     const bool flatten = r.op == Op::Fwht && !(r.inverse && r.normalize) && r.log_n <= 13;
+    // A rank-2 FFT with both lowerings: MEASURE times the two, DEFAULT
+    // replays a selection-cache record of that choice (keyed by the extents
+    // too), the static rule decides otherwise.
+    if (!flatten && r.op == Op::Fft && r.rank == 2 && !r.embedding && sel != nullptr &&
+        r.policy != CUBUTTERFLY_ALGORITHM_EXPLICIT &&
+        (sel->policy == CUBUTTERFLY_ALGORITHM_MEASURE ||
+         (sel->policy == CUBUTTERFLY_ALGORITHM_DEFAULT && !sel->cache_path.empty()))) {
+        const std::string key = selection_key(r) + "|rank2-fft|" + std::to_string(r.extents[0]) + "x" +
+                                std::to_string(r.extents[1]);
+        if (sel->policy == CUBUTTERFLY_ALGORITHM_DEFAULT) {
+            const std::string cached = lookup_cache(sel->cache_path, key);
+            const int force = cached.rfind("rank2-columns[", 0) == 0       ? 1
+                              : cached.rfind("rank2-transposing[", 0) == 0 ? 2
+                                                                           : 0;
+            if (force) {
+                auto e = std::make_unique<CompositeExecutor>(r, flatten, sel, force);
+                if (e->algorithm == cached) {
+                    combine_source(*sel, CUBUTTERFLY_SELECTION_USER_CACHE);
+                    note_selection(*sel, "replayed '" + cached + "' from the selection cache");
+                    return e;
+                }
+                note_selection(*sel, "ignored cache record '" + cached + "' (not a lowering of this request)");
+            }
+        } else if (CompositeExecutor::both_rank2_lowerings(r)) {
+            require_no_capture(*sel);
+            auto cols = std::make_unique<CompositeExecutor>(r, flatten, sel, 1);
+            auto rows = std::make_unique<CompositeExecutor>(r, flatten, sel, 2);
+            if (cols->columns() && rows->transposing()) {
+                std::vector<std::unique_ptr<Executor>> alternatives;
+                alternatives.push_back(std::move(cols));
+                alternatives.push_back(std::move(rows));
+                const std::size_t best = measure_executors(r, key, alternatives, *sel);
+                if (best < alternatives.size()) return std::move(alternatives[best]);
+            }
+        }
+    }
     return std::make_unique<CompositeExecutor>(r, flatten, sel);
 }
 

@@ -1427,35 +1427,51 @@ class FftRank2ColumnsExecutor final : public Executor {
 
 }  // namespace
 
-std::unique_ptr<Executor> make_fft_rows_transposed(const Request& r, std::uint32_t l1) {
+bool fft_rows_transposed_available(const Request& r, std::uint32_t l1) {
     const int l2 = int(r.log_n);
     // Level-twiddle tables reach 2^24-th roots (so l1 + l2 <= 24, which also
     // keeps a block's byte offsets in 32 bits).
-    if (l2 < 4 || l2 > 12 || int(l1) < 14 - l2 || l1 + std::uint32_t(l2) > 24 ||
-        (r.batch & ((std::uint64_t{1} << l1) - 1)) != 0)
-        return nullptr;
-    const Launch fn = lookup(Key{l2, 14 - l2, false, false, r.inverse, 4});
-    if (fn == nullptr) return nullptr;
-    return std::make_unique<FftRowsTransposedExecutor>(r, l1, fn);
+    return l2 >= 4 && l2 <= 12 && int(l1) >= 14 - l2 && l1 + std::uint32_t(l2) <= 24 &&
+           (r.batch & ((std::uint64_t{1} << l1) - 1)) == 0 &&
+           lookup(Key{l2, 14 - l2, false, false, r.inverse, 4}) != nullptr;
 }
 
-std::unique_ptr<Executor> make_fft_rank2_columns(const Request& r, std::uint32_t l0) {
+std::unique_ptr<Executor> make_fft_rows_transposed(const Request& r, std::uint32_t l1) {
+    if (!fft_rows_transposed_available(r, l1)) return nullptr;
+    const int l2 = int(r.log_n);
+    return std::make_unique<FftRowsTransposedExecutor>(r, l1, lookup(Key{l2, 14 - l2, false, false, r.inverse, 4}));
+}
+
+// The column-pass split of axis 0 (ta top bits, then tb; tb = 0 for one
+// pass), or false where no kernels cover the shape: rows of 2^8 .. 2^12
+// points (whole 2^14-point row tiles within a block), blocks of at most 2^24
+// points (the level-twiddle tables' reach), and axis 0 in one column pass of
+// 4 .. 8 bits or two: the second over tb >= 14 - l1 bits (its 2^(14 - tb)
+// columns within the 2^l1 of a row), the first over the rest, each within
+// 4 .. 8 bits.
+bool rank2_columns_split(const Request& r, std::uint32_t l0, std::uint32_t& ta, std::uint32_t& tb) {
     const std::uint32_t m = r.log_n;
-    if (l0 < 4 || l0 >= m) return nullptr;
+    if (l0 < 4 || l0 >= m) return false;
     const std::uint32_t l1 = m - l0;
-    // Rows of 2^8 .. 2^12 points (whole 2^14-point row tiles within a block),
-    // blocks of at most 2^24 points (the level-twiddle tables' reach), and
-    // axis 0 in one column pass of 4 .. 8 bits or two: the second over tb >= 14 - l1
-    // bits (its 2^(14 - tb) columns within the 2^l1 of a row), the first over
-    // the rest, each within 4 .. 8 bits.
-    if (l1 < 8 || l1 > 12 || m > 24 || l0 < 14 - l1) return nullptr;
-    std::uint32_t ta = l0, tb = 0;
+    if (l1 < 8 || l1 > 12 || m > 24 || l0 < 14 - l1) return false;
+    ta = l0;
+    tb = 0;
     if (l0 > 8) {
         tb = std::max(l0 / 2, 14 - l1);
         ta = l0 - tb;
-        if (tb > 8 || ta < 4 || ta > 8) return nullptr;
+        if (tb > 8 || ta < 4 || ta > 8) return false;
     }
-    if (r.batch > (0xffffffffull >> l0)) return nullptr;
+    return r.batch <= (0xffffffffull >> l0);
+}
+
+bool fft_rank2_columns_available(const Request& r, std::uint32_t l0) {
+    std::uint32_t ta = 0, tb = 0;
+    return rank2_columns_split(r, l0, ta, tb);
+}
+
+std::unique_ptr<Executor> make_fft_rank2_columns(const Request& r, std::uint32_t l0) {
+    std::uint32_t ta = 0, tb = 0;
+    if (!rank2_columns_split(r, l0, ta, tb)) return nullptr;
     return std::make_unique<FftRank2ColumnsExecutor>(r, l0, ta, tb);
 }
 

@@ -31,6 +31,9 @@ std::unique_ptr<Executor> make_fft_rows_transposed(const Request& r, std::uint32
 // r.n points): axis 0 as column passes, then the rows in natural order; null
 // where no kernel covers the shape.
 std::unique_ptr<Executor> make_fft_rank2_columns(const Request& r, std::uint32_t l0);
+// Whether those two factories would build a plan (no device work).
+bool fft_rows_transposed_available(const Request& r, std::uint32_t l1);
+bool fft_rank2_columns_available(const Request& r, std::uint32_t l0);
 std::vector<std::string> fft_candidates(const Request& r);
 std::vector<std::string> ntt_candidates(const Request& r);
 
@@ -45,6 +48,11 @@ struct Selection {
     std::string notes;
 };
 void combine_source(Selection& sel, cubutterflySelectionSource_t next);
+// Appends a note to the plan's selection reason.
+void note_selection(Selection& sel, const std::string& text);
+// MEASURE's refusal on a capturing stream (NOT_SUPPORTED), to be called
+// before any candidate is built: building allocates device tables.
+void require_no_capture(const Selection& sel);
 std::string selection_key(const Request& r);
 std::string lookup_cache(const std::string& path, const std::string& key);
 void store_cache(const std::string& path, const std::string& key, const std::string& algorithm);
@@ -52,6 +60,12 @@ std::unique_ptr<Executor> build_leaf(const Request& r);
 // A packed rank-1 plan: explicit variant, cached record (DEFAULT), measured
 // candidates (MEASURE) or the static model.
 std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel);
+// MEASURE between alternative executors of one request (MEASURE's timing
+// protocol and scratch): records the fastest's name under `key` in the
+// selection cache and returns its index, or built.size() when the scratch
+// could not be allocated.
+std::size_t measure_executors(const Request& r, const std::string& key,
+                              const std::vector<std::unique_ptr<Executor>>& built, Selection& sel);
 
 // Gather / packed child / scatter, for strided sides and FWHT / FFT orders.
 std::unique_ptr<Executor> make_boundary_executor(const Request& r, Selection* sel);

@@ -197,6 +197,14 @@ std::vector<double> time_executors(const std::vector<std::unique_ptr<Executor>>&
 
 }  // namespace
 
+void note_selection(Selection& sel, const std::string& text) { note(sel, text); }
+
+void require_no_capture(const Selection& sel) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    hip_check(hipStreamIsCapturing(sel.stream, &capture), "MEASURE capture query");
+    supported(capture == hipStreamCaptureStatusNone, "MEASURE cannot time candidates during stream capture");
+}
+
 void combine_source(Selection& sel, cubutterflySelectionSource_t next) {
     if (rank_of(next) > rank_of(sel.source)) sel.source = next;
 }
@@ -270,6 +278,14 @@ std::vector<std::string> leaf_candidates(const Request& r) {
     return {};
 }
 
+// MEASURE over built executors of one request, with the search trace of the
+// caller: times them on rotating scratch buffers, records the fastest under
+// `key` and notes the figures. Returns the fastest's index, or built.size()
+// when the scratch could not be allocated (the caller keeps its static choice).
+static std::size_t measure_traced(const Request& r, const std::string& key,
+                                  const std::vector<std::unique_ptr<Executor>>& built, Selection& sel,
+                                  std::size_t candidate_count, SearchTrace& trace);
+
 std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     if (sel == nullptr || sel->policy == CUBUTTERFLY_ALGORITHM_EXPLICIT) {
         if (r.policy != CUBUTTERFLY_ALGORITHM_EXPLICIT) return build_leaf(r);
@@ -294,10 +310,40 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
         }
         return build_leaf(r);
     }
-    // MEASURE: every candidate on the device, on shared scratch buffers.
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    hip_check(hipStreamIsCapturing(sel->stream, &capture), "MEASURE capture query");
-    supported(capture == hipStreamCaptureStatusNone, "MEASURE cannot time candidates during stream capture");
+    // MEASURE: every candidate on the device, on shared scratch buffers
+    // (refused before any candidate allocates its tables on a capturing
+    // stream).
+    require_no_capture(*sel);
+    SearchTrace trace;
+    const auto names = leaf_candidates(r);
+    std::vector<std::unique_ptr<Executor>> built;
+    for (const auto& name : names) {
+        Request v = r;
+        v.variant = name;
+        try {
+            built.push_back(build_leaf(v));
+        } catch (const NotSupported& e) {  // not a lowering here after all: skip it
+            trace.event("result", "\"candidate\":" + json::quote(name) + ",\"status\":\"rejected\",\"reason\":" +
+                                      json::quote(e.what()));
+        }
+    }
+    require(!built.empty(), "no candidate lowering to measure");
+    const std::size_t best = measure_traced(r, key, built, *sel, names.size(), trace);
+    if (best == built.size()) return build_leaf(r);
+    return std::move(built[best]);
+}
+
+std::size_t measure_executors(const Request& r, const std::string& key,
+                              const std::vector<std::unique_ptr<Executor>>& built, Selection& sel) {
+    SearchTrace trace;
+    return measure_traced(r, key, built, sel, built.size(), trace);
+}
+
+static std::size_t measure_traced(const Request& r, const std::string& key,
+                                  const std::vector<std::unique_ptr<Executor>>& built, Selection& sel,
+                                  std::size_t candidate_count, SearchTrace& trace) {
+    require_no_capture(sel);
+    require(!built.empty(), "no candidate lowering to measure");
     // Scratch sides span what the kernels address: a pitched leaf reads and
     // writes row b at b * batch stride, up to (batch - 1) * pitch + n elements.
     const std::size_t in_bytes = r.in_place ? std::max(r.span_bytes(true), r.span_bytes(false)) : r.span_bytes(true);
@@ -320,24 +366,11 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
         free_bytes = 0;
     }
     const std::size_t budget = std::max(std::size_t{512} << 20, std::min(std::size_t{2} << 30, free_bytes / 4));
-    SearchTrace trace;
-    const auto names = leaf_candidates(r);
-    std::vector<std::unique_ptr<Executor>> built;
     std::size_t ws_bytes = 0;
-    for (const auto& name : names) {
-        Request v = r;
-        v.variant = name;
-        try {
-            built.push_back(build_leaf(v));
-            ws_bytes = std::max(ws_bytes, built.back()->workspace_bytes());
-        } catch (const NotSupported& e) {  // not a lowering here after all: skip it
-            trace.event("result", "\"candidate\":" + json::quote(name) + ",\"status\":\"rejected\",\"reason\":" +
-                                      json::quote(e.what()));
-        }
-    }
-    require(!built.empty(), "no candidate lowering to measure");
+    for (const auto& e : built) ws_bytes = std::max(ws_bytes, e->workspace_bytes());
     while (sets > 1 && sets * footprint + ws_bytes > budget) --sets;
-    trace.event("inventory", "\"key\":" + json::quote(key) + ",\"candidate_count\":" + std::to_string(names.size()) +
+    trace.event("inventory", "\"key\":" + json::quote(key) + ",\"candidate_count\":" +
+                                 std::to_string(candidate_count) +
                                  ",\"timing_protocol\":\"interleaved-rounds\",\"warmup\":" +
                                  std::to_string(kWarmup) + ",\"rounds\":" + std::to_string(kRounds) +
                                  ",\"calls_per_round\":" + std::to_string(kCalls) + "," +
@@ -353,21 +386,21 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
         for (std::size_t k = 0; k < sets; ++k) {
             in.emplace_back(in_bytes);
             out.emplace_back(out_bytes);
-            hip_check(hipMemsetAsync(in.back().ptr, 0, in_bytes, sel->stream), "MEASURE input fill");
+            hip_check(hipMemsetAsync(in.back().ptr, 0, in_bytes, sel.stream), "MEASURE input fill");
         }
         ws = std::make_unique<DeviceScratch>(ws_bytes);
     } catch (const std::bad_alloc&) {
         // Not enough device memory to time the candidates: keep the static
         // model's lowering and say so, instead of failing the plan.
         trace.event("selected", "\"algorithm\":null,\"reason\":\"scratch allocation failed\"");
-        note(*sel, "MEASURE skipped: could not allocate " + std::to_string(sets * footprint + ws_bytes) +
-                       " bytes of scratch; static model used");
-        return build_leaf(r);
+        note(sel, "MEASURE skipped: could not allocate " + std::to_string(sets * footprint + ws_bytes) +
+                      " bytes of scratch; static model used");
+        return built.size();
     }
     std::size_t best = 0;
     double best_ms = std::numeric_limits<double>::infinity();
     std::string results;
-    const std::vector<double> times = time_executors(built, in, out, r.in_place, ws->ptr, sel->stream);
+    const std::vector<double> times = time_executors(built, in, out, r.in_place, ws->ptr, sel.stream);
     for (std::size_t i = 0; i < built.size(); ++i) {
         const double ms = times[i];
         char text[64];
@@ -382,10 +415,10 @@ std::unique_ptr<Executor> select_leaf(const Request& r, Selection* sel) {
     }
     trace.event("selected", "\"algorithm\":" + json::quote(built[best]->algorithm) +
                                 ",\"kernel_ms\":" + std::to_string(best_ms));
-    store_cache(sel->cache_path, key, built[best]->algorithm);
-    combine_source(*sel, CUBUTTERFLY_SELECTION_RUNTIME_MEASURED);
-    note(*sel, "measured " + results);
-    return std::move(built[best]);
+    store_cache(sel.cache_path, key, built[best]->algorithm);
+    combine_source(sel, CUBUTTERFLY_SELECTION_RUNTIME_MEASURED);
+    note(sel, "measured " + results);
+    return best;
 }
 
 }  // namespace cbw

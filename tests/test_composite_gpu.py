@@ -228,6 +228,38 @@ def test_fft_rank2_lowering_by_name(torch_gpu, lib, stream, extents, batch, name
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
 
 
+def test_fft_rank2_measure_times_both_lowerings_and_the_cache_replays(torch_gpu, lib, stream, tmp_path):
+    extents, batch = (512, 2048), 2
+    t = fft_t(extents, batch)
+    cache = tmp_path / "sel.tsv"
+    with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream, cache_path=cache) as plan:
+        reason = plan.selection_reason()
+        chosen = plan.algorithm_name()
+        assert plan.selection_source() == cb.SelectionSource.RUNTIME_MEASURED
+    assert "rank2-columns[" in reason and "rank2-transposing[" in reason, reason
+    assert chosen in (ROWS_NAME, COLUMNS_NAME)
+    records = [line.split("\t") for line in cache.read_text().splitlines()]
+    assert records[-1][0].endswith("|rank2-fft|512x2048") and records[-1][1] == chosen
+    with cb.Plan(lib, t, stream=stream, cache_path=cache) as plan:
+        assert plan.algorithm_name() == chosen
+        assert plan.selection_source() == cb.SelectionSource.USER_CACHE
+    x = data((batch,) + extents, np.complex64, 14)
+    got = run_plan(torch_gpu, lib, t, x, stream, cache_path=cache).astype(np.complex128)
+    ref = np.fft.fftn(x.astype(np.complex128), axes=(1, 2))
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
+
+
+def test_fft_rank2_measure_refuses_stream_capture(torch_gpu, lib):
+    # Refused before either lowering allocates its tables: the capture stays
+    # valid.
+    s = torch_gpu.cuda.Stream()
+    graph = torch_gpu.cuda.CUDAGraph()
+    with torch_gpu.cuda.graph(graph, stream=s):
+        with pytest.raises(cb.AbiError) as e:
+            cb.Plan(lib, fft_t((512, 2048), 2), policy=cb.AlgorithmPolicy.MEASURE, stream=s.cuda_stream)
+        assert e.value.status == cb.Status.NOT_SUPPORTED and "capture" in e.value.detail
+
+
 def test_fft_rank2_columns_by_name_where_no_kernel_covers_it(lib):
     # 16-point rows: no natural-order row tiles of that length.
     with pytest.raises(cb.AbiError) as e:
