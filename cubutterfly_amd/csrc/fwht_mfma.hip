@@ -28,11 +28,13 @@
 //      radix-2 transform in registers (VALU, fp32, bits in stage order).
 //
 // The output element (k2, k1, k0) of lane l, register r is k2 * 256 +
-// (l % 16) * 16 + 4 (l / 16) + r: four consecutive halves, one 8-byte store.
-// No LDS is used. Accumulation order differs from the radix-2 stage order of
-// the STRICT kernels, so results can differ from them by one fp16 ulp where a
-// value sits near a rounding boundary; this lowering is taken only when the
-// caller names it (or MEASURE picks it) under the ALLOW_FP16_MMA policy.
+// (l % 16) * 16 + 4 (l / 16) + r: four consecutive halves. Blocks move in
+// pairs, one 16-byte access per lane each way, with one v_permlane16_swap per
+// dword to trade the halves of neighbouring 16-lane groups. No LDS is used.
+// Accumulation order differs from the radix-2 stage order of the STRICT
+// kernels, so results can differ from them by one fp16 ulp where a value sits
+// near a rounding boundary; this lowering is taken only when the caller names
+// it (or MEASURE picks it) under the ALLOW_FP16_MMA policy.
 //
 // Rows stay independent. The block matrices I (x) H(2^t) hold zeros for the
 // element pairs of different rows (rows shorter than 16 points in the first
@@ -81,8 +83,7 @@ __device__ __forceinline__ half4 hadamard_block(unsigned lane, int t) {
 // fp16 narrowing two separate roundings.
 __device__ __forceinline__ void opaque(float& x) { asm volatile("" : "+v"(x)); }
 
-// y = (x * norm) * scale rounded to fp32 twice, then one RNE narrowing, for
-// the four values of one 8-byte store.
+// y = (x * norm) * scale rounded to fp32 twice, then one RNE narrowing.
 __device__ __forceinline__ unsigned short narrow(float x, float norm, float scale) {
     float y = (x * norm) * scale;
     opaque(y);
@@ -98,10 +99,12 @@ __device__ __forceinline__ unsigned short narrow(float x, float norm, float scal
 // leave in the input's own layout. The tile is loaded again here, so that no
 // input register stays live into this path: the common path keeps its own
 // allocation and this one spills what does not fit.
-// This path needs about 200 VGPRs where the MFMA path needs 120, and the
-// kernel's allocation covers both: the kernel therefore asks for four waves
-// per SIMD (at most 128 VGPRs), so what does not fit spills here, in the
-// path that only tiles holding inf or NaN take. Scheduling barriers after
+// This path needs about 200 VGPRs where the MFMA path needs 120 (rows of
+// more than 256 points, which hold all 64 results for the register stages)
+// or 96 (shorter rows), and the kernel's allocation covers both: the kernel
+// therefore asks for four waves per SIMD (at most 128 VGPRs) or five (at most
+// 96; C5b 48.1 -> 47.7 us), so what does not fit spills here, in the path
+// that only tiles holding inf or NaN take. Scheduling barriers after
 // each group of four lane exchanges keep the compiler from hoisting all 64
 // of a stage at once.
 template <int LOG_N>
@@ -154,9 +157,13 @@ __device__ __forceinline__ void stage_ordered_tile(__amdgpu_buffer_rsrc_t src, u
     }
 }
 
+// Waves per SIMD: 4 where the register stages hold all 64 results, 5 for
+// rows of up to 256 points.
+constexpr int mfma_waves_per_simd(int log_n) { return log_n <= 8 ? 5 : 4; }
+
 template <int LOG_N>
-__global__ __launch_bounds__(64 * kWavesPerBlock) __attribute__((amdgpu_waves_per_eu(4))) void fwht_mfma_kernel(
-    const __half* __restrict__ input, __half* output, std::uint64_t total, float norm, float scale) {
+__global__ __launch_bounds__(64 * kWavesPerBlock) __attribute__((amdgpu_waves_per_eu(mfma_waves_per_simd(LOG_N))))
+void fwht_mfma_kernel(const __half* __restrict__ input, __half* output, std::uint64_t total, float norm, float scale) {
     constexpr int t0 = LOG_N < 4 ? LOG_N : 4;                        // transform bits among 0..3
     constexpr int t1 = LOG_N <= 4 ? 0 : (LOG_N < 8 ? LOG_N - 4 : 4);  // among 4..7
     constexpr int t2 = LOG_N <= 8 ? 0 : LOG_N - 8;                    // among 8..11
@@ -182,11 +189,32 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) __attribute__((amdgpu_waves_pe
     const half4 m1 = hadamard_block(lane, t1 > 0 ? t1 : 1);
 
     using U2 = __attribute__((ext_vector_type(2))) unsigned;
+    using U4 = __attribute__((ext_vector_type(4))) unsigned;
+    // Blocks 2p and 2p + 1 move together as one 16-byte access per lane
+    // (1 KiB of consecutive elements per wave instruction): lanes of even
+    // 16-lane groups g take elements 4g .. 4g + 7 of block 2p's 16-element
+    // row l % 16, lanes of odd groups elements 4 (g - 1) .. 4 (g - 1) + 7 of
+    // block 2p + 1's, and v_permlane16_swap (registers indexed by the old
+    // lane bit 4 afterwards) trades the halves that belong to the other
+    // group. Rows of 8 or more points keep every 16-byte access inside or
+    // outside the tile's range; shorter ones load 8 bytes per block.
+    const unsigned pair_bytes = (lane_bytes & ~15u) + 512u * ((lane >> 4) & 1u);
     half4 a[16];
+    if constexpr (LOG_N >= 3) {
 #pragma unroll
-    for (int i2 = 0; i2 < 16; ++i2) {
-        const U2 raw = __builtin_amdgcn_raw_buffer_load_b64(src, int(lane_bytes + 512u * i2), 0, 0);
-        a[i2] = __builtin_bit_cast(half4, raw);
+        for (int p = 0; p < 8; ++p) {
+            const U4 raw = __builtin_amdgcn_raw_buffer_load_b128(src, int(pair_bytes + 1024u * unsigned(p)), 0, 0);
+            const auto s0 = __builtin_amdgcn_permlane16_swap(raw[0], raw[2], false, false);
+            const auto s1 = __builtin_amdgcn_permlane16_swap(raw[1], raw[3], false, false);
+            a[2 * p] = __builtin_bit_cast(half4, U2{s0[0], s1[0]});
+            a[2 * p + 1] = __builtin_bit_cast(half4, U2{s0[1], s1[1]});
+        }
+    } else {
+#pragma unroll
+        for (int i2 = 0; i2 < 16; ++i2) {
+            const U2 raw = __builtin_amdgcn_raw_buffer_load_b64(src, int(lane_bytes + 512u * i2), 0, 0);
+            a[i2] = __builtin_bit_cast(half4, raw);
+        }
     }
     // Any inf or NaN in the wave's tile (exponent field all ones, i.e. a
     // half whose magnitude bits are 0x7c00 or more), from the per-half
@@ -256,21 +284,34 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) __attribute__((amdgpu_waves_pe
             }
         }
     }
+    if constexpr (t1 > 0) {
+        // Blocks 2p and 2p + 1 leave as one 16-byte nontemporal store per
+        // lane, the load's exchange run backwards: each output is written
+        // once, and a wave instruction writes 1 KiB of consecutive output.
 #pragma unroll
-    for (int k2 = 0; k2 < 16; ++k2) {
-        unsigned short h[4];
+        for (int p = 0; p < 8; ++p) {
+            unsigned w[2][2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) h[r] = narrow(v[k2][r], norm, scale);
-        if constexpr (t1 > 0) {
-            const U2 packed = {unsigned(h[0]) | (unsigned(h[1]) << 16), unsigned(h[2]) | (unsigned(h[3]) << 16)};
-            __builtin_amdgcn_raw_buffer_store_b64(packed, dst, int(lane_bytes + 512u * k2), 0, 0);
-        } else {
-            // Rows of <= 16 points: no second contraction, so lane l holds
-            // D0 rows i1 = 4 (l / 16) + r at column k0 = l % 16, 16 elements apart.
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int d = 0; d < 2; ++d)
+                    w[q][d] = unsigned(narrow(v[2 * p + q][2 * d], norm, scale)) |
+                              (unsigned(narrow(v[2 * p + q][2 * d + 1], norm, scale)) << 16);
+            const auto s0 = __builtin_amdgcn_permlane16_swap(w[0][0], w[1][0], false, false);
+            const auto s1 = __builtin_amdgcn_permlane16_swap(w[0][1], w[1][1], false, false);
+            __builtin_amdgcn_raw_buffer_store_b128(U4{s0[0], s1[0], s0[1], s1[1]}, dst,
+                                                   int(pair_bytes + 1024u * unsigned(p)), 0, 2);
+        }
+    } else {
+        // Rows of <= 16 points: no second contraction, so lane l holds D0
+        // rows i1 = 4 (l / 16) + r at column k0 = l % 16, 16 elements apart.
+#pragma unroll
+        for (int k2 = 0; k2 < 16; ++k2) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const unsigned e = 256u * k2 + 16u * (4u * (lane >> 4) + unsigned(r)) + (lane & 15u);
-                __builtin_amdgcn_raw_buffer_store_b16(h[r], dst, int(e * sizeof(__half)), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b16(narrow(v[k2][r], norm, scale), dst, int(e * sizeof(__half)), 0,
+                                                      0);
             }
         }
     }
