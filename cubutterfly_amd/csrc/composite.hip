@@ -38,6 +38,7 @@
 // two: the forward input side (logical extents) is gathered with zeros in
 // the padding, the inverse output side keeps the first logical-extent
 // elements of each axis.
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -442,6 +443,124 @@ class CompositeExecutor final : public Executor {
     std::size_t child_ws_ = 0;
 };
 
+// FP16 final-storage FWHT rows of more than 2^13 points: the reference's
+// FP32 promotion (src/butterfly.cu:1452-1470) -- the input widened into an
+// FP32 buffer, the factored FP32 transform in place on it (with the
+// inverse's 1/n), then y * scale rounded to FP32 and narrowed once to FP16
+// (round to nearest even) -- which is the stage-ordered FP32 transform
+// narrowed once, as the one-tile FP16 kernels compute it.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void widen_f16_kernel(const __half* __restrict__ src, float* __restrict__ dst,
+                                                             std::uint64_t count) {
+    const std::uint64_t step = std::uint64_t(gridDim.x) * kThreads;
+    if constexpr (VEC) {  // 8 halves per 16-byte load, both sides 16-byte aligned
+        for (std::uint64_t c = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; c < count / 8; c += step) {
+            const uint4 raw = reinterpret_cast<const uint4*>(src)[c];
+            const unsigned w[4] = {raw.x, raw.y, raw.z, raw.w};
+            float f[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                f[2 * k] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[k] & 0xffffu)));
+                f[2 * k + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[k] >> 16)));
+            }
+            reinterpret_cast<float4*>(dst)[2 * c] = make_float4(f[0], f[1], f[2], f[3]);
+            reinterpret_cast<float4*>(dst)[2 * c + 1] = make_float4(f[4], f[5], f[6], f[7]);
+        }
+    } else {
+        for (std::uint64_t i = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < count; i += step)
+            dst[i] = __half2float(src[i]);
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void narrow_f16_kernel(const float* __restrict__ src, __half* __restrict__ dst,
+                                                              std::uint64_t count, float scale) {
+    const std::uint64_t step = std::uint64_t(gridDim.x) * kThreads;
+    if constexpr (VEC) {
+        for (std::uint64_t c = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; c < count / 8; c += step) {
+            const float4 a = reinterpret_cast<const float4*>(src)[2 * c];
+            const float4 b = reinterpret_cast<const float4*>(src)[2 * c + 1];
+            const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            unsigned w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                w[k] = unsigned(__half_as_ushort(__float2half_rn(f[2 * k] * scale))) |
+                       (unsigned(__half_as_ushort(__float2half_rn(f[2 * k + 1] * scale))) << 16);
+            reinterpret_cast<uint4*>(dst)[c] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    } else {
+        for (std::uint64_t i = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < count; i += step)
+            dst[i] = __float2half_rn(src[i] * scale);
+    }
+}
+
+class FwhtPromotedExecutor final : public Executor {
+  public:
+    FwhtPromotedExecutor(const Request& r, Selection* sel) : r_(r) {
+        Request c = r;
+        c.storage = CUBUTTERFLY_DATA_FP32;
+        c.element_bytes = sizeof(float);
+        c.fp16_final = false;
+        c.allow_mma = false;
+        c.output_scale = 1.0f;
+        c.in_place = false;
+        c.policy = CUBUTTERFLY_ALGORITHM_DEFAULT;
+        c.explicit_algorithm.clear();
+        c.variant.clear();
+        factor_long_fwht(c);
+        child_ = make_composite_executor(c, sel);
+        f32_bytes_ = align16(c.data_bytes());
+        algorithm = "fwht-fp16-promoted[" + child_->algorithm + "]";
+        reason = "FP16 rows beyond one resident tile: widened to FP32, the factored FP32 transform, one final "
+                 "narrowing of y * scale; child: " + child_->reason;
+        json::Writer w;
+        w.begin_object()
+            .field("schema_version", 1u)
+            .field("kind", "fp32-promotion")
+            .field("operator", "fwht")
+            .field("algorithm", algorithm)
+            .field("log_n", r.log_n)
+            .field("batch", r.batch)
+            .field("fp32_buffer_bytes", std::uint64_t(f32_bytes_))
+            .key("child")
+            .value_raw(child_->mapping_json)
+            .end_object();
+        mapping_json = w.str();
+    }
+
+    std::size_t workspace_bytes() const override { return f32_bytes_ + child_->workspace_bytes(); }
+
+    void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
+        require(ws != nullptr, "the FP32 promotion needs its workspace");
+        auto* buffer = static_cast<float*>(ws);
+        void* child_ws = child_->workspace_bytes() ? static_cast<unsigned char*>(ws) + f32_bytes_ : nullptr;
+        const std::uint64_t count = r_.n * r_.batch;
+        const bool vec = reinterpret_cast<std::uintptr_t>(in) % 16 == 0 && reinterpret_cast<std::uintptr_t>(out) % 16 == 0;
+        const std::uint64_t work = vec ? count / 8 : count;
+        const unsigned blocks = unsigned(std::min<std::uint64_t>((work + kThreads - 1) / kThreads, 65536));
+        const auto* src = static_cast<const __half*>(in);
+        auto* dst = static_cast<__half*>(out);
+        if (vec)
+            hipLaunchKernelGGL((widen_f16_kernel<true>), dim3(blocks), dim3(kThreads), 0, stream, src, buffer, count);
+        else
+            hipLaunchKernelGGL((widen_f16_kernel<false>), dim3(blocks), dim3(kThreads), 0, stream, src, buffer, count);
+        hip_check(hipGetLastError(), "FP16 widening launch");
+        child_->execute(buffer, buffer, child_ws, stream);
+        if (vec)
+            hipLaunchKernelGGL((narrow_f16_kernel<true>), dim3(blocks), dim3(kThreads), 0, stream, buffer, dst, count,
+                               r_.output_scale);
+        else
+            hipLaunchKernelGGL((narrow_f16_kernel<false>), dim3(blocks), dim3(kThreads), 0, stream, buffer, dst, count,
+                               r_.output_scale);
+        hip_check(hipGetLastError(), "FP16 narrowing launch");
+    }
+
+  private:
+    Request r_;
+    std::unique_ptr<Executor> child_;
+    std::size_t f32_bytes_ = 0;
+};
+
 }  // namespace
 
 std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel) {
@@ -487,6 +606,14 @@ std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* s
         }
     }
     return std::make_unique<CompositeExecutor>(r, flatten, sel);
+}
+
+std::unique_ptr<Executor> make_long_fwht_executor(const Request& r, Selection* sel) {
+    require(r.op == Op::Fwht && r.rank == 1 && r.log_n > 13 && !r.boundary, "a packed rank-1 FWHT beyond 2^13 points");
+    if (r.fp16_final) return std::make_unique<FwhtPromotedExecutor>(r, sel);
+    Request f = r;
+    factor_long_fwht(f);
+    return make_composite_executor(f, sel);
 }
 
 }  // namespace cbw

@@ -239,6 +239,38 @@ void validate_descriptor(const cubutterflyDescriptor& d) {
                 "stage matrices require the structured operator within the rank");
 }
 
+// H(2^a) (x) H(2^b) (x) ... factors an FWHT beyond one resident tile into
+// axes of at most 2^12 points, lowest index bits innermost, so the composite
+// plan's innermost-first axis order is the rank-1 stage order (bits 0
+// upward) and the result is bit-identical. The rank-1 element strides carry
+// over to the factors; bit-reversed orders do not factor.
+void factor_long_fwht(Request& r) {
+    require(r.op == Op::Fwht && r.rank == 1 && !r.factored && !r.embedding && !r.fp16_final &&
+                !r.input_bit_reversed && !r.output_bit_reversed,
+            "only natural-order FP32 FWHT rows factor");
+    std::vector<std::uint32_t> bits;  // innermost first
+    for (std::uint32_t left = r.log_n; left > 0; left -= std::min<std::uint32_t>(left, 12))
+        bits.push_back(std::min<std::uint32_t>(left, 12));
+    supported(bits.size() <= kMaxRank, "FWHT length exceeds the factored rank");
+    r.factored = true;
+    r.rank = std::uint32_t(bits.size());
+    r.extents.assign(r.rank, 0);
+    r.in_strides.assign(r.rank, 0);
+    r.out_strides.assign(r.rank, 0);
+    std::uint64_t below = 1;
+    for (std::size_t k = 0; k < bits.size(); ++k) {
+        const std::size_t axis = r.rank - 1 - k;
+        r.extents[axis] = std::uint64_t{1} << bits[k];
+        r.in_strides[axis] = r.in_stride * below;
+        r.out_strides[axis] = r.out_stride * below;
+        below <<= bits[k];
+    }
+    r.in_extents = r.out_extents = r.extents;
+    r.in_reversed.assign(r.rank, 0);
+    r.out_reversed.assign(r.rank, 0);
+    r.boundary = r.pitched = false;
+}
+
 Request lower_request(const cubutterflyDescriptor& d) {
     validate_descriptor(d);
     supported(d.rank <= kMaxRank, "ranks above eight are not executable");
@@ -376,35 +408,16 @@ Request lower_request(const cubutterflyDescriptor& d) {
         default:
             throw NotSupported("operator has no MI355X lowering");
     }
-    // FWHT beyond one resident tile (2^13 points): H(2^a) (x) H(2^b) (x) ...
-    // factors the transform into axes of at most 2^12 points, lowest index
-    // bits innermost, so the composite plan's innermost-first axis order is
-    // the rank-1 stage order (bits 0 upward) and the result is bit-identical.
+    // FWHT beyond one resident tile (2^13 points). FP32 rows in natural order
+    // factor here, their strides carried by the factors; FP16 rows (the FP32
+    // promotion) and bit-reversed orders are planned as rank-1 requests, the
+    // orders and strides through the boundary, and factor when their packed
+    // FP32 transform is planned (factor_long_fwht). No kernel loads long rows
+    // at a pitch.
     if (r.op == Op::Fwht && d.rank == 1 && !embedding && r.log_n > 13) {
-        supported(!r.fp16_final, "FP16 FWHT lengths above 2^13 are not executable (one final narrowing)");
-        supported(!r.input_bit_reversed && !r.output_bit_reversed,
-                  "bit-reversed FWHT orders above 2^13 points are not executable");
-        std::vector<std::uint32_t> bits;  // innermost first
-        for (std::uint32_t left = r.log_n; left > 0; left -= std::min<std::uint32_t>(left, 12))
-            bits.push_back(std::min<std::uint32_t>(left, 12));
-        supported(bits.size() <= kMaxRank, "FWHT length exceeds the factored rank");
-        r.factored = true;
-        r.rank = std::uint32_t(bits.size());
-        r.extents.assign(r.rank, 0);
-        r.in_strides.assign(r.rank, 0);
-        r.out_strides.assign(r.rank, 0);
-        std::uint64_t below = 1;
-        for (std::size_t k = 0; k < bits.size(); ++k) {
-            const std::size_t axis = r.rank - 1 - k;
-            r.extents[axis] = std::uint64_t{1} << bits[k];
-            r.in_strides[axis] = r.in_stride * below;
-            r.out_strides[axis] = r.out_stride * below;
-            below <<= bits[k];
-        }
-        r.in_extents = r.out_extents = r.extents;
-        r.in_reversed.assign(r.rank, 0);
-        r.out_reversed.assign(r.rank, 0);
-        r.boundary = r.pitched = false;
+        r.pitched = false;
+        r.boundary = strided || reversed;
+        if (!r.fp16_final && !reversed) factor_long_fwht(r);
     }
     return r;
 }

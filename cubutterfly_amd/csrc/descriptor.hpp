@@ -120,6 +120,9 @@ struct Request {
 // rules for the fields this library accepts (src/semantic_contract.cpp:189-280).
 void validate_descriptor(const cubutterflyDescriptor& d);
 Request lower_request(const cubutterflyDescriptor& d);
+// A natural-order FP32 FWHT request of more than 2^13 points as its factors
+// (axes of at most 2^12 points, lowest bits innermost).
+void factor_long_fwht(Request& r);
 
 std::string descriptor_json(const cubutterflyDescriptor& d);
 cubutterflyDescriptor descriptor_from_json(const std::string& text);

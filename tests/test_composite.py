@@ -177,7 +177,33 @@ def test_long_fwht_is_factored(lib):
         m = plan.mapping()
         assert m["extents"] == [256, 4096]
         assert [s["axis"] for s in m["schedule"] if s["step"] == "axis"] == [1, 0]
-    fp16 = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [1 << 14], compute=cb.ComputeType.FP32, output_rounding=cb.OutputRounding.FINAL_STORAGE)
-    with pytest.raises(cb.AbiError) as e:
-        cb.Plan(lib, fp16)
-    assert e.value.status == cb.Status.NOT_SUPPORTED
+
+
+def test_long_fp16_fwht_is_promoted(lib):
+    # FP16 final-storage rows beyond 2^13 points: widened into an FP32 buffer
+    # of the workspace, the factored FP32 plan, one narrowing (the reference's
+    # FP32 promotion, src/butterfly.cu:1452-1470).
+    n, batch = 1 << 14, 3
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [n], compute=cb.ComputeType.FP32, batch=batch,
+                    output_scale=n ** -0.5, output_rounding=cb.OutputRounding.FINAL_STORAGE)
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name().startswith("fwht-fp16-promoted[fwht-factored[")
+        assert plan.input_size() == plan.output_size() == batch * n * 2
+        m = plan.mapping()
+        assert m["kind"] == "fp32-promotion" and m["fp32_buffer_bytes"] == batch * n * 4
+        assert m["child"]["extents"] == [4, 4096]
+        assert plan.workspace_size() >= batch * n * 4
+    # Strided or bit-reversed sides gather to packed rows first.
+    strided = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [n], compute=cb.ComputeType.FP32, batch=batch,
+                          input_strides=[2], input_batch_stride=2 * n, output_rounding=cb.OutputRounding.FINAL_STORAGE)
+    with cb.Plan(lib, strided) as plan:
+        assert plan.algorithm_name().startswith("semantic-boundary[fwht-fp16-promoted[")
+
+
+def test_long_fwht_bit_reversed_orders_use_the_boundary(lib):
+    # A whole-length bit reversal does not factor into per-axis reversals:
+    # the boundary gathers to natural order, and the packed child factors.
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << 16], compute=cb.ComputeType.FP32, batch=2,
+                    input_orders=[cb.LogicalOrder.BIT_REVERSED], output_orders=[cb.LogicalOrder.NATURAL])
+    with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name().startswith("semantic-boundary[fwht-factored[")
