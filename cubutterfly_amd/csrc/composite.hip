@@ -472,6 +472,17 @@ __global__ __launch_bounds__(kThreads) void widen_f16_kernel(const __half* __res
     }
 }
 
+// y = x * scale rounded to FP32, then to FP16 (round to nearest even). The
+// empty asm keeps the two roundings apart: without it the compiler fuses the
+// product and the narrowing into one v_fma_mixlo_f16, a single rounding of
+// the exact product, which differs from the contract for scales that are not
+// powers of two.
+__device__ __forceinline__ __half narrow_scaled(float x, float scale) {
+    float y = x * scale;
+    asm volatile("" : "+v"(y));
+    return __float2half_rn(y);
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void narrow_f16_kernel(const float* __restrict__ src, __half* __restrict__ dst,
                                                               std::uint64_t count, float scale) {
@@ -484,13 +495,13 @@ __global__ __launch_bounds__(kThreads) void narrow_f16_kernel(const float* __res
             unsigned w[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                w[k] = unsigned(__half_as_ushort(__float2half_rn(f[2 * k] * scale))) |
-                       (unsigned(__half_as_ushort(__float2half_rn(f[2 * k + 1] * scale))) << 16);
+                w[k] = unsigned(__half_as_ushort(narrow_scaled(f[2 * k], scale))) |
+                       (unsigned(__half_as_ushort(narrow_scaled(f[2 * k + 1], scale))) << 16);
             reinterpret_cast<uint4*>(dst)[c] = make_uint4(w[0], w[1], w[2], w[3]);
         }
     } else {
         for (std::uint64_t i = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < count; i += step)
-            dst[i] = __float2half_rn(src[i] * scale);
+            dst[i] = narrow_scaled(src[i], scale);
     }
 }
 
