@@ -1,8 +1,10 @@
 """Seeded random parity over the whole public surface, on the GPU: every
 operator with random lengths and batches, strided, pitched and bit-reversed
 sides (the semantic boundary, reference src/c_api.cpp:5064-5085), NTT
-layouts and rings, in-place plans, long FWHTs (factored and FP32-promoted)
-and rank-2 / rank-3 composites. Each case is checked against the CPU oracle
+layouts and rings, in-place plans, long FWHTs (factored and FP32-promoted),
+rank-2 / rank-3 composites, and RNS plans through the RNS C ABI (random
+domains, roots, polynomial slots, orders and placements; the layout rules of
+the reference's tests/test_rns_ntt.cu:113-162). Each case is checked against the CPU oracle
 (bit-exact for FWHT and NTT; FFT within rel-L2 1e-5 against numpy in
 complex128), and every output element outside the output layout must keep
 its sentinel. Cases are drawn from fixed seeds, so a failure names a case
@@ -14,6 +16,7 @@ import pytest
 
 import cubutterfly_amd as cb
 import oracle
+from cubutterfly_amd import rns
 from gpu_util import run_plan, to_device, to_host
 
 pytestmark = pytest.mark.gpu
@@ -236,8 +239,62 @@ def composite_case(torch, lib, stream, rng, index):
     return desc, np.array_equal(got, want)
 
 
+RNS_SENTINEL = np.uint64(0xFEDCBA9876543210)
+
+
+def rns_case(torch, lib, stream, rng, index):
+    """An RNS plan: 1-3 domains (primes from 2^59 to above 2^62, roots an odd
+    power of a primitive root), 1-5 polynomials in permuted slots of padded
+    rows, random orders, ring, direction and placement; sentinel words around
+    every slot must survive (out of place) or keep the input (in place)."""
+    log_n = rng.randint(12, 17)
+    n = 1 << log_n
+    negacyclic = rng.random() < 0.6
+    inverse, in_rev, out_rev, in_place = (rng.random() < 0.5 for _ in range(4))
+    root_bits = log_n + int(negacyclic)
+    primes = [q for q in U64 if two_adic(q - 1) >= root_bits]
+    domains = []
+    for _ in range(rng.randint(1, 3)):
+        q = rng.choice(primes)
+        domains.append((q, pow(oracle.find_primitive_root(root_bits, q), rng.choice([1, 3, 5, 7, 9, 11]), q)))
+    count = rng.randint(1, 5)
+    slots = count + rng.randint(0, 2)
+    pad, base = rng.randint(0, 40), rng.randint(0, 20)
+    ins, outs = rng.sample(range(slots), count), rng.sample(range(slots), count)
+    polys = [{"domain": rng.randrange(len(domains)), "input_offset": i * (n + pad) + base,
+              "output_offset": o * (n + pad) + base} for i, o in zip(ins, outs)]
+    cfg = rns.request(log_n, domains, polynomials=polys, inverse=inverse,
+                      ring="negacyclic" if negacyclic else "cyclic",
+                      input_order="bit_reversed" if in_rev else "natural",
+                      output_order="bit_reversed" if out_rev else "natural")
+    words = slots * (n + pad) + base + 7
+    data = np.full(words, RNS_SENTINEL)
+    values = np.random.default_rng(index)
+    for poly in polys:
+        q = domains[poly["domain"]][0]
+        data[poly["input_offset"]:poly["input_offset"] + n] = values.integers(0, q, n, dtype=np.uint64)
+    want = data.copy() if in_place else np.full(words, RNS_SENTINEL)
+    for poly in polys:
+        q, root = domains[poly["domain"]]
+        row = data[poly["input_offset"]:poly["input_offset"] + n]
+        want[poly["output_offset"]:poly["output_offset"] + n] = oracle.rns(
+            row[None], [q], [root], negacyclic=negacyclic, inverse=inverse, input_bit_reversed=in_rev,
+            output_bit_reversed=out_rev)[0]
+    x = to_device(torch, data)
+    y = x if in_place else to_device(torch, np.full(words, RNS_SENTINEL))
+    with rns.RnsPlan(lib, cfg) as plan:
+        plan.prepare(stream, in_place=in_place, repetitions=1)
+        plan.execute(x, y, stream)
+        torch.cuda.synchronize()
+        mapping = plan.info()["mapping"]["algorithm"]
+    got = to_host(torch, y, np.uint64)
+    desc = (f"rns n=2^{log_n} negacyclic={negacyclic} inverse={inverse} orders=({in_rev},{out_rev}) "
+            f"in_place={in_place} domains={domains} polynomials={polys} [{mapping}]")
+    return desc, np.array_equal(got, want)
+
+
 KINDS = {"layouts": (layout_case, 120), "ntt": (ntt_case, 50), "fft": (fft_case, 40),
-         "composites": (composite_case, 30)}
+         "composites": (composite_case, 30), "rns": (rns_case, 25)}
 
 
 @pytest.mark.parametrize("seed", [7, 11])
