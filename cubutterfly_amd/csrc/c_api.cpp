@@ -396,14 +396,26 @@ cubutterflyStatus_t cubutterflyCreatePlan(cubutterflyHandle_t handle, cubutterfl
         }
         if (!selection.notes.empty()) {
             created->executor->reason += "; " + selection.notes;
-            log_event(handle, CUBUTTERFLY_LOG_INFO,
-                      created->request.policy == CUBUTTERFLY_ALGORITHM_MEASURE ? "measure-complete" : "cache-replay",
-                      selection.notes + "; algorithm=" + created->executor->algorithm);
+            if (created->request.policy == CUBUTTERFLY_ALGORITHM_MEASURE)
+                log_event(handle, CUBUTTERFLY_LOG_INFO, "measure-complete",
+                          selection.notes + "; algorithm=" + created->executor->algorithm);
         }
         created->input_bytes = created->request.span_bytes(true);
         created->output_bytes = created->request.span_bytes(false);
         created->workspace_bytes = created->executor->workspace_bytes();
-        log_event(handle, CUBUTTERFLY_LOG_INFO, "plan-created", created->executor->algorithm);
+        // The reference's log events (src/c_api.cpp:4526-4529, 4782;
+        // docs/c_api.md:193-198): every plan reports its selection, and a
+        // DEFAULT plan that took the static model -- no measured or cached
+        // mapping for this exact workload -- warns and recommends MEASURE.
+        log_event(handle, CUBUTTERFLY_LOG_INFO, "algorithm-selection",
+                  created->executor->reason + "; algorithm=" + created->executor->algorithm);
+        if (created->request.policy == CUBUTTERFLY_ALGORITHM_DEFAULT &&
+            (created->source == CUBUTTERFLY_SELECTION_STATIC_MODEL ||
+             created->source == CUBUTTERFLY_SELECTION_UNMEASURED_FALLBACK))
+            log_event(handle, CUBUTTERFLY_LOG_WARNING, "workload-profile-miss",
+                      "no measured or cached mapping for this workload on gfx950; " +
+                          cbw::selection_key(created->request) + "; " + created->executor->reason + "; using " +
+                          created->executor->algorithm + "; set MEASURE with a cache path to calibrate this workload");
         *plan = created.release();
     });
 }

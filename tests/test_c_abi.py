@@ -222,3 +222,48 @@ def test_abi_error_names_the_entry_point(lib):
     e = info.value
     assert e.function == "cubutterflyDescriptorSetJson" and e.status == cb.Status.INVALID_VALUE
     assert str(e).startswith("cubutterflyDescriptorSetJson -> invalid value") and e.detail
+
+
+LOG_CALLBACK = ct.CFUNCTYPE(None, ct.c_int, ct.c_char_p, ct.c_char_p, ct.c_void_p)
+
+
+def plan_events(lib, desc, callback_on=True):
+    """(level, event, message) of every log callback during one CreatePlan."""
+    events = []
+    callback = LOG_CALLBACK(lambda level, event, message, user: events.append(
+        (abi.enums["LogLevel"](level), event.decode(), message.decode())))
+    handle = ct.c_void_p()
+    lib("Create", ct.byref(handle))
+    try:
+        lib("SetLogCallback", handle, ct.cast(callback, ct.c_void_p) if callback_on else None, None)
+        with cb.DescriptorHandle(lib, desc) as d:
+            plan = ct.c_void_p()
+            lib("CreatePlan", handle, d.handle, ct.byref(plan))
+            lib("DestroyPlan", plan)
+    finally:
+        lib("Destroy", handle)
+    return events
+
+
+def test_log_callback_reports_selection_and_profile_miss(lib):
+    # The reference's events (src/c_api.cpp:4526-4529, 4782; docs/c_api.md:
+    # 193-198): every plan reports `algorithm-selection`; a DEFAULT plan on
+    # the static model, with no measured or cached mapping, warns
+    # `workload-profile-miss` with the fallback and the MEASURE advice.
+    LogLevel = abi.enums["LogLevel"]
+    desc = fwht(n=1024, batch=4)
+    events = plan_events(lib, desc)
+    names = [e[1] for e in events]
+    assert "algorithm-selection" in names
+    miss = [e for e in events if e[1] == "workload-profile-miss"]
+    assert len(miss) == 1 and miss[0][0] == LogLevel.WARNING
+    with cb.Plan(lib, desc) as plan:
+        chosen = plan.algorithm_name()
+    assert f"using {chosen};" in miss[0][2] and "MEASURE" in miss[0][2]
+    info = next(e for e in events if e[1] == "algorithm-selection")
+    assert info[0] == LogLevel.INFO and info[2].endswith(f"algorithm={chosen}")
+    # An explicitly named lowering is no profile miss.
+    explicit = dict(desc, algorithm_policy=int(cb.AlgorithmPolicy.EXPLICIT), explicit_algorithm=chosen)
+    assert [e[1] for e in plan_events(lib, explicit)] == ["algorithm-selection"]
+    # A null callback turns the events off.
+    assert plan_events(lib, desc, callback_on=False) == []
