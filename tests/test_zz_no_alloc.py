@@ -104,8 +104,9 @@ def test_plans_without_workspace_and_oversized_plans(torch_gpu, lib, stream):
 def test_composite_embedding_and_boundary_plans_after_a_larger_plan(torch_gpu, lib, stream):
     # Rank-2 FFT (row plan, transposes, workspace ping-pong buffers; column
     # passes and a natural-order row pass), the
-    # zero-extended embedding (gather with zero fill, padded transform) and a
-    # strided boundary plan, each run right after a larger plan filled the
+    # zero-extended embedding (gather with zero fill, padded transform), a
+    # strided boundary plan and long FWHTs (the FP32 promotion's buffer, a
+    # bit-reversed boundary around a factored plan), each run right after a larger plan filled the
     # shared array with non-zero data: no plan may read a word it did not
     # write first, so both entry points agree bit for bit.
     rng = np.random.default_rng(5)
@@ -132,6 +133,14 @@ def test_composite_embedding_and_boundary_plans_after_a_larger_plan(torch_gpu, l
                                                                compute=cb.ComputeType.FP32, batch=8,
                                                                input_strides=[8], input_batch_stride=1),
          (8 * 4096,), np.float32),
+        ("fp16 fwht 2^15 x 3 (FP32 promotion)",
+         cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [1 << 15], compute=cb.ComputeType.FP32, batch=3,
+                     output_scale=float(np.float32((1 << 15) ** -0.5)),
+                     output_rounding=cb.OutputRounding.FINAL_STORAGE), (3 << 15,), np.float16),
+        ("fwht 2^16 x 2, bit-reversed input (boundary, factored)",
+         cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << 16], compute=cb.ComputeType.FP32, batch=2,
+                     input_orders=[cb.LogicalOrder.BIT_REVERSED], output_orders=[cb.LogicalOrder.NATURAL]),
+         (2 << 16,), np.float32),
     ]
     for name, desc, shape, dtype in cases:
         print(f"case no-alloc {name} after C2's forward", flush=True)
@@ -139,7 +148,7 @@ def test_composite_embedding_and_boundary_plans_after_a_larger_plan(torch_gpu, l
         if dtype == np.complex64:
             host = (rng.standard_normal(shape) + 1j * rng.standard_normal(shape)).astype(np.complex64)
         else:
-            host = rng.standard_normal(shape).astype(np.float32)
+            host = rng.standard_normal(shape).astype(dtype)
         bound, static = both(torch_gpu, lib, stream, desc, host, dtype)
-        width = np.uint64 if dtype == np.complex64 else np.uint32
+        width = {np.complex64: np.uint64, np.float32: np.uint32, np.float16: np.uint16}[dtype]
         np.testing.assert_array_equal(static.view(width), bound.view(width), err_msg=name)
