@@ -160,3 +160,29 @@ def test_fp16_strided_sides(torch_gpu, lib, stream):
     for b in range(batch):
         want[b * out_bs: b * out_bs + n] = result[b]
     np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("inverse", [False, True])
+def test_rank2_with_a_long_axis(torch_gpu, lib, stream, inverse):
+    # H(4) (x) H(2^14): the 2^14-point axis is itself factored; innermost
+    # first, the composition is the flat transform's stage order, bit for bit.
+    batch, n0, n1 = 2, 4, 1 << 14
+    x = np.random.default_rng(31).standard_normal((batch, n0 * n1)).astype(np.float32)
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n0, n1], compute=cb.ComputeType.FP32, batch=batch,
+                    inverse=inverse, normalize_inverse=inverse)
+    got = run_plan(torch_gpu, lib, t, x, stream)
+    want = oracle.fwht_f32(x, inverse=inverse, normalize=inverse)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_zero_extended_long_rows(torch_gpu, lib, stream):
+    # 20000 logical points run at 2^15: the forward input is zero-extended,
+    # the output holds all 2^15 points (reference docs/c_api.md:74-79).
+    batch, n, padded = 2, 20000, 1 << 15
+    x = np.random.default_rng(32).standard_normal((batch, n)).astype(np.float32)
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=batch,
+                    length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING)
+    got = run_plan(torch_gpu, lib, t, x, stream).reshape(batch, padded)
+    full = np.zeros((batch, padded), np.float32)
+    full[:, :n] = x
+    np.testing.assert_array_equal(got.view(np.uint32), oracle.fwht_f32(full).view(np.uint32))
