@@ -2,7 +2,7 @@
 operator with random lengths and batches, strided, pitched and bit-reversed
 sides (the semantic boundary, reference src/c_api.cpp:5064-5085), NTT
 layouts and rings, in-place plans, long FWHTs (factored and FP32-promoted),
-rank-2 / rank-3 composites, and RNS plans through the RNS C ABI (random
+rank-2 / rank-3 composites, the zero-extended embedding, and RNS plans through the RNS C ABI (random
 domains, roots, polynomial slots, orders and placements; the layout rules of
 the reference's tests/test_rns_ntt.cu:113-162). Each case is checked against the CPU oracle
 (bit-exact for FWHT and NTT; FFT within rel-L2 1e-5 against numpy in
@@ -239,6 +239,61 @@ def composite_case(torch, lib, stream, rng, index):
     return desc, np.array_equal(got, want)
 
 
+def embedding_case(torch, lib, stream, rng, index):
+    """The zero-extended embedding (reference docs/c_api.md:74-79): each axis
+    runs at its next power of two; the forward takes the logical extents and
+    returns the padded ones, the inverse the reverse. Checked against the
+    transform of the zero-padded input (forward) and the cut transform of the
+    padded input (inverse)."""
+    op = rng.choice(["fft", "fwht", "ntt"])
+    rank = rng.choice([1, 1, 2])
+    logical = [rng.randint(3, 5000 if rank == 1 else 300) for _ in range(rank)]
+    padded = [1 << (e - 1).bit_length() for e in logical]
+    batch = rng.randint(1, 3)
+    inverse = rng.random() < 0.5
+    data = np.random.default_rng(index)
+    in_ext, out_ext = (padded, logical) if inverse else (logical, padded)
+    shape_in = (batch, *in_ext)
+    axes = tuple(range(1, rank + 1))
+    if op == "fft":
+        x = (data.standard_normal(shape_in) + 1j * data.standard_normal(shape_in)).astype(np.complex64)
+        t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, logical, compute=cb.ComputeType.FP32,
+                        batch=batch, inverse=inverse, normalize_inverse=inverse,
+                        length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING)
+    elif op == "fwht":
+        x = data.integers(-4, 5, shape_in).astype(np.float32)
+        t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, logical, compute=cb.ComputeType.FP32, batch=batch,
+                        length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING, inverse=inverse)
+    else:
+        q = 998244353
+        x = data.integers(0, q, shape_in, dtype=np.uint64).astype(np.uint32)
+        t = cb.describe(cb.Operator.NTT, cb.DataType.UINT32, logical, compute=cb.ComputeType.UINT32, batch=batch,
+                        modulus=q, word_bits=32, inverse=inverse, length_mode=cb.LengthMode.ZERO_EXTENDED_EMBEDDING)
+    full = np.zeros((batch, *padded), dtype=x.dtype)
+    full[(slice(None),) + tuple(slice(0, e) for e in in_ext)] = x
+    if op == "fft":
+        want = (np.fft.ifftn if inverse else np.fft.fftn)(full.astype(np.complex128), axes=axes)
+    elif op == "fwht":
+        # normalize_inverse defaults to true; integer data and a power-of-two
+        # 1/n keep every order of the additions exact
+        want = oracle.fwht_f32(full.reshape(batch, -1), inverse=inverse, normalize=inverse).reshape(full.shape)
+    else:
+        want = full.astype(np.uint64)
+        for axis in axes:
+            moved = np.moveaxis(want, axis, -1)
+            flat = np.ascontiguousarray(moved.reshape(-1, moved.shape[-1]))
+            want = np.moveaxis(oracle.ntt_cyclic(flat, q, inverse=inverse).reshape(moved.shape), -1, axis)
+    want = want[(slice(None),) + tuple(slice(0, e) for e in out_ext)]
+    got = run_plan(torch, lib, t, np.ascontiguousarray(x), stream).reshape((batch, *out_ext))
+    desc = f"embedded {op} logical={logical} batch={batch} inverse={inverse}"
+    if op == "fft":
+        err = np.linalg.norm(got.astype(np.complex128) - want) / np.linalg.norm(want)
+        return desc + f" rel-L2 {err:.2e}", err <= 1e-5
+    if op == "fwht":
+        return desc, np.array_equal(got, want)
+    return desc, np.array_equal(got.astype(np.uint64), want)
+
+
 RNS_SENTINEL = np.uint64(0xFEDCBA9876543210)
 
 
@@ -294,7 +349,7 @@ def rns_case(torch, lib, stream, rng, index):
 
 
 KINDS = {"layouts": (layout_case, 120), "ntt": (ntt_case, 50), "fft": (fft_case, 40),
-         "composites": (composite_case, 30), "rns": (rns_case, 25)}
+         "composites": (composite_case, 30), "embedding": (embedding_case, 30), "rns": (rns_case, 25)}
 
 
 @pytest.mark.parametrize("seed", [7, 11])
