@@ -2,7 +2,8 @@
 operator with random lengths and batches, strided, pitched and bit-reversed
 sides (the semantic boundary, reference src/c_api.cpp:5064-5085), NTT
 layouts and rings, in-place plans, long FWHTs (factored and FP32-promoted),
-rank-2 / rank-3 composites, the zero-extended embedding, and RNS plans through the RNS C ABI (random
+rank-2 / rank-3 composites, the zero-extended embedding, MEASURE selection
+with its cache replay, and RNS plans through the RNS C ABI (random
 domains, roots, polynomial slots, orders and placements; the layout rules of
 the reference's tests/test_rns_ntt.cu:113-162). Each case is checked against the CPU oracle
 (bit-exact for FWHT and NTT; FFT within rel-L2 1e-5 against numpy in
@@ -294,6 +295,62 @@ def embedding_case(torch, lib, stream, rng, index):
     return desc, np.array_equal(got.astype(np.uint64), want)
 
 
+def measure_case(torch, lib, stream, rng, index):
+    """MEASURE on a random packed rank-1 request with a fresh selection cache:
+    the measured plan matches the oracle, and a DEFAULT plan on the same
+    cache replays the same lowering from it."""
+    import tempfile
+    op = rng.choice(["fft", "fwht32", "fwht16", "ntt32", "ntt64"])
+    data = np.random.default_rng(index)
+    if op == "fft":
+        log_n = rng.randint(10, 20)
+        batch = max(1, (1 << 18) >> log_n)
+        t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [1 << log_n], compute=cb.ComputeType.FP32,
+                        batch=batch)
+        x = (data.standard_normal((batch, 1 << log_n)) + 1j * data.standard_normal((batch, 1 << log_n))).astype(
+            np.complex64)
+    elif op.startswith("fwht"):
+        log_n = rng.randint(5, 13)
+        batch = max(1, (1 << 18) >> log_n)
+        if op == "fwht32":
+            t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << log_n], compute=cb.ComputeType.FP32, batch=batch)
+            x = data.standard_normal((batch, 1 << log_n)).astype(np.float32)
+        else:
+            scale = float(np.float32((1 << log_n) ** -0.5))
+            t = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [1 << log_n], compute=cb.ComputeType.FP32,
+                            batch=batch, output_scale=scale, output_rounding=cb.OutputRounding.FINAL_STORAGE)
+            x = data.standard_normal((batch, 1 << log_n)).astype(np.float16)
+    else:
+        bits = 32 if op == "ntt32" else 64
+        q = U32[0] if bits == 32 else U64[2]
+        log_n = rng.randint(8, 17)
+        batch = max(1, (1 << 18) >> log_n)
+        t = cb.describe(cb.Operator.NTT, cb.DataType.UINT32 if bits == 32 else cb.DataType.UINT64, [1 << log_n],
+                        compute=cb.ComputeType.UINT32 if bits == 32 else cb.ComputeType.UINT64, batch=batch,
+                        modulus=q, word_bits=bits, ntt_ring=cb.NttRing.NEGACYCLIC)
+        x = data.integers(0, q, (batch, 1 << log_n), dtype=np.uint64).astype(np.uint32 if bits == 32 else np.uint64)
+    with tempfile.TemporaryDirectory() as tmp:
+        cache = f"{tmp}/selection.tsv"
+        with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream, cache_path=cache) as plan:
+            chosen = plan.algorithm_name()
+            measured = plan.selection_source() == cb.SelectionSource.RUNTIME_MEASURED
+        with cb.Plan(lib, t, stream=stream, cache_path=cache) as plan:
+            replayed = plan.algorithm_name() == chosen and plan.selection_source() == cb.SelectionSource.USER_CACHE
+        got = run_plan(torch, lib, t, x, stream, algorithm=chosen)
+    desc = f"measure {op} n=2^{log_n} batch={batch} -> {chosen} (measured {measured}, replayed {replayed})"
+    if op == "fft":
+        want = np.fft.fft(x.astype(np.complex128), axis=1)
+        err = np.linalg.norm(got.astype(np.complex128) - want) / np.linalg.norm(want)
+        ok = err <= 1e-5
+    elif op == "fwht32":
+        ok = np.array_equal(got.view(np.uint32), oracle.fwht_f32(x).view(np.uint32))
+    elif op == "fwht16":
+        ok = np.array_equal(got.view(np.uint16), oracle.fwht_f16_final(x, scale).view(np.uint16))
+    else:
+        ok = np.array_equal(got.astype(np.uint64), oracle.ntt_negacyclic(x.astype(np.uint64), q))
+    return desc, ok and measured and replayed
+
+
 RNS_SENTINEL = np.uint64(0xFEDCBA9876543210)
 
 
@@ -349,7 +406,8 @@ def rns_case(torch, lib, stream, rng, index):
 
 
 KINDS = {"layouts": (layout_case, 120), "ntt": (ntt_case, 50), "fft": (fft_case, 40),
-         "composites": (composite_case, 30), "embedding": (embedding_case, 30), "rns": (rns_case, 25)}
+         "composites": (composite_case, 30), "embedding": (embedding_case, 30), "measure": (measure_case, 12),
+         "rns": (rns_case, 25)}
 
 
 @pytest.mark.parametrize("seed", [7, 11])
