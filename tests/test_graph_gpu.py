@@ -109,3 +109,34 @@ def test_replays_match_eager(torch_gpu, lib, case):
             eager = to_host(torch, y, dtype)
             bits = {2: np.uint16, 4: np.uint32, 8: np.uint64}[np.dtype(dtype).itemsize] if np.dtype(dtype).kind != "c" else np.uint64
             np.testing.assert_array_equal(got.view(bits), eager.view(bits), err_msg=f"{case} replay {replay}")
+
+
+@pytest.mark.parametrize("case", ["fft-two-pass", "rank2-columns", "fwht-fp16-promoted"])
+def test_execute_steady_matches_execute(torch_gpu, lib, case):
+    # cubutterflyExecuteSteady (reference src/c_api.cpp:5390-5411): the same
+    # results as cubutterflyExecute, also after the handle's stream changes
+    # between calls, and the same pointer checks.
+    t, dtype, span = CASES[case]
+    torch = torch_gpu
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    with cb.Plan(lib, t, stream=streams[0].cuda_stream) as plan:
+        ws_bytes = plan.workspace_size()
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+        if ws_bytes:
+            plan.set_workspace(ws, ws_bytes)
+        out_span = plan.output_size() // np.dtype(dtype).itemsize
+        x = to_device(torch, host_data(dtype, span, 4))
+        y_exec = to_device(torch, np.zeros(out_span, dtype))
+        plan.execute(x, y_exec)
+        torch.cuda.synchronize()
+        want = to_host(torch, y_exec, dtype)
+        bits = np.uint64 if np.dtype(dtype).kind == "c" else {2: np.uint16, 4: np.uint32}[np.dtype(dtype).itemsize]
+        for call, s in enumerate([streams[0], streams[0], streams[1], streams[0]]):
+            lib("SetStream", plan.context, s.cuda_stream)
+            y = to_device(torch, np.zeros(out_span, dtype))
+            plan.execute_steady(x, y)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(to_host(torch, y, dtype).view(bits), want.view(bits), err_msg=f"call {call}")
+        with pytest.raises(cb.AbiError) as e:
+            plan.execute_steady(x, x)  # an out-of-place plan refuses aliased pointers
+        assert e.value.status == cb.Status.INVALID_VALUE
