@@ -145,10 +145,10 @@ class OnePlan(Workload):
 
 class FwhtFp32(OnePlan):
     name, dtype = "c1", "f32"
-    description = "C1: FWHT fp32 unnormalized forward, batch 4096 x n=4096, integer inputs in [-8,8]"
 
     def __init__(self, log_n=12, batch=4096):
         self.log_n, self.rows = log_n, batch
+        self.description = f"C1: FWHT fp32 unnormalized forward, batch {batch} x n={1 << log_n}, integer inputs in [-8,8]"
         self.transforms_per_call = batch
         self.bytes_per_call = 2 * batch * (4 << log_n)
 
@@ -175,8 +175,11 @@ class FwhtFp32Pitched(FwhtFp32):
     """C1's transform on rows pitched by n + 64 on both sides (not a BASELINE
     line): the FWHT kernel reads and writes the pitched rows directly."""
     name = "c1p"
-    description = "C1 on rows pitched at n + 64 elements on both sides (pitched-row FWHT kernel)"
     PAD = 64
+
+    def __init__(self, log_n=12, batch=4096):
+        super().__init__(log_n, batch)
+        self.description = "C1 on rows pitched at n + 64 elements on both sides (pitched-row FWHT kernel)"
 
     def descriptor(self, cb):
         n = 1 << self.log_n
@@ -211,13 +214,13 @@ class FwhtFp32Pitched(FwhtFp32):
 class NttNegacyclic(Workload):
     """C2: forward then inverse negacyclic NTT, u32, q = 1073479681, n = 2^16, batch 64."""
     name, dtype = "c2", "u32"
-    description = ("C2: single-prime negacyclic NTT u32, n=2^16, batch 64, q=1073479681 (30-bit, q = 1 mod 2n); "
-                   "one step = forward then inverse of the batch")
     valu_per_butterfly = 8.6
 
     def __init__(self, log_n=16, batch=64):
         from cubutterfly_amd import workloads
         self.log_n, self.rows, self.q = log_n, batch, workloads.C2_MODULUS
+        self.description = (f"C2: single-prime negacyclic NTT u32, n=2^{log_n}, batch {batch}, q=1073479681 (30-bit, "
+                            "q = 1 mod 2n); one step = forward then inverse of the batch")
         self.transforms_per_call = 2 * batch  # forward + inverse transforms
         self.bytes_per_call = 2 * 2 * batch * (4 << log_n)
         self.butterflies_per_call = self.transforms_per_call * (1 << (log_n - 1)) * log_n
@@ -448,6 +451,12 @@ WORKLOADS = {"c1": FwhtFp32, "c1p": FwhtFp32Pitched, "c2": NttNegacyclic, "c3a":
              "c5b_mma": lambda: FwhtFp16(524288, 128, mma=True), "r2": FftC64Rank2, "copy": DeviceCopy}
 
 
+# Configurations whose batch (rows, polynomials) `--batch` can change, for
+# sweeps that separate a kernel's fixed cost from its per-row rate.
+BATCHED = {"c1": lambda b: FwhtFp32(12, b), "c2": lambda b: NttNegacyclic(16, b), "c3b": lambda b: FftC64(14, b),
+           "c5a": lambda b: FwhtFp16(b, 4096), "c5b": lambda b: FwhtFp16(b, 128)}
+
+
 def measured_traffic(name):
     """HBM bytes per call (read, write) for a configuration, from the
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/ (scaled by the copy
@@ -564,7 +573,8 @@ def cpu_rate(workload, threads, target_s=0.25, reps=7):
 
 def measure(torch, lib, name, args, mapping=None):
     """Times one configuration on the GPU; returns its per_config entry."""
-    workload = WORKLOADS[name]()
+    batch = getattr(args, "batch", None)
+    workload = BATCHED[name](batch) if batch else WORKLOADS[name]()
     if mapping:
         if not workload.takes_mapping:
             raise SystemExit(f"--mapping does not apply to {name}")
@@ -576,9 +586,9 @@ def measure(torch, lib, name, args, mapping=None):
     per_call, timed = timer(torch, workload, stream, args.steps, args.warmup)
     ms = statistics.median(per_call)
     achieved = workload.bytes_per_call / (ms * 1e-3) / 1e9
-    traffic = measured_traffic(name)
+    traffic = None if batch else measured_traffic(name)  # the summaries are per BASELINE shape
     entry = {
-        "config": name,
+        "config": name if not batch else f"{name}@batch={batch}",
         "workload": workload.description,
         "dtype": workload.dtype,
         "kernel": workload.kernel_name(),
@@ -629,7 +639,7 @@ def measure(torch, lib, name, args, mapping=None):
             entry["cpu_baseline"].update(value=many, cores=threads, sample=many_sample)
         else:
             entry["cpu_baseline"].update(value=one, cores=1, sample=one_sample + " (one transform: 1 core only)")
-    print(f"# {name}: {ms * 1e3:.2f} us per call, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%}); "
+    print(f"# {entry['config']}: {ms * 1e3:.2f} us per call, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%}); "
           f"median of the first {MIN_REPLAYS} replays {entry['ms_per_call_first7'] * 1e3:.2f} us",
           file=sys.stderr, flush=True)
     return entry
@@ -646,6 +656,8 @@ def main():
     parser.add_argument("--verify", action="store_true", help="check each output against the oracle")
     parser.add_argument("--eager", action="store_true", help="time eager submissions instead of graph replays")
     parser.add_argument("--mapping", default=None, help="plan a single --workload with this lowering (EXPLICIT)")
+    parser.add_argument("--batch", type=int, default=None,
+                        help="rows / polynomials of a single --workload (" + " ".join(sorted(BATCHED)) + ")")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every configuration of the butterfly path runs on one GPU and "
@@ -654,6 +666,10 @@ def main():
         sys.exit(2)
     if args.mapping and args.workload == "all":
         print("--mapping needs a single --workload", file=sys.stderr)
+        sys.exit(2)
+    if args.batch is not None and (args.workload not in BATCHED or args.batch < 1):
+        print("--batch needs a single --workload among " + ", ".join(sorted(BATCHED)) + " and a positive count",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch

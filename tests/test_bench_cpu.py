@@ -51,3 +51,22 @@ def test_baseline_configurations_and_bytes(bench):
                 "c5a": 268435456, "c5b": 268435456}
     for name, nbytes in expected.items():
         assert bench.WORKLOADS[name]().bytes_per_call == nbytes, name
+
+
+def test_batch_override_scales_the_workload(bench):
+    # `--batch` rebuilds one configuration at another batch: the compulsory
+    # bytes scale with it and the transform stays the same.
+    assert sorted(bench.BATCHED) == ["c1", "c2", "c3b", "c5a", "c5b"]
+    for name, standard in [("c1", 4096), ("c2", 64), ("c3b", 1024), ("c5a", 16384), ("c5b", 524288)]:
+        base = bench.WORKLOADS[name]()
+        assert bench.BATCHED[name](standard).bytes_per_call == base.bytes_per_call, name
+        assert bench.BATCHED[name](2 * standard).bytes_per_call == 2 * base.bytes_per_call, name
+
+
+@pytest.mark.parametrize("args", [["--batch", "128"], ["--workload", "c4", "--batch", "64"],
+                                  ["--workload", "c2", "--batch", "0"]])
+def test_batch_override_needs_a_batched_workload(args):
+    done = subprocess.run([sys.executable, str(ROOT / "bench.py")] + args, capture_output=True, text=True,
+                          timeout=120)
+    assert done.returncode == 2
+    assert "--batch needs" in done.stderr
