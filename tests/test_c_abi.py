@@ -267,3 +267,20 @@ def test_log_callback_reports_selection_and_profile_miss(lib):
     assert [e[1] for e in plan_events(lib, explicit)] == ["algorithm-selection"]
     # A null callback turns the events off.
     assert plan_events(lib, desc, callback_on=False) == []
+
+
+def test_capabilities_follow_the_executable_subset(lib):
+    # The capabilities query lowers the descriptor as plan creation does:
+    # long FP16 and bit-reversed FWHTs are eligible, FP16 at rank 2 is not.
+    fp16 = dict(compute=cb.ComputeType.FP32, output_rounding=cb.OutputRounding.FINAL_STORAGE)
+    eligible = [
+        cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [1 << 16], 4, **fp16),
+        cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << 18], 2, compute=cb.ComputeType.FP32,
+                    input_orders=[cb.LogicalOrder.BIT_REVERSED], output_orders=[cb.LogicalOrder.NATURAL]),
+    ]
+    for t in eligible:
+        with cb.DescriptorHandle(lib, t) as d:
+            assert d.capabilities()["eligible"] is True, t
+    with cb.DescriptorHandle(lib, cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [64, 64], 1, **fp16)) as d:
+        caps = d.capabilities()
+    assert caps["eligible"] is False and "rank one" in caps["reason"]
