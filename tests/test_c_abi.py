@@ -284,3 +284,46 @@ def test_capabilities_follow_the_executable_subset(lib):
     with cb.DescriptorHandle(lib, cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [64, 64], 1, **fp16)) as d:
         caps = d.capabilities()
     assert caps["eligible"] is False and "rank one" in caps["reason"]
+
+
+def test_concurrent_plan_creation_matches_serial(lib):
+    # Plans created from several host threads at once (one handle each; ctypes
+    # releases the GIL inside the calls) choose the same lowerings as a serial
+    # run: the kernel registries fill once and are read-only afterwards, and
+    # error strings are per thread.
+    from concurrent.futures import ThreadPoolExecutor
+    # FWHT plans need no device at creation (FFT and NTT plans upload their
+    # twiddle tables; their concurrent creation is a GPU test).
+    descs = [
+        fwht(n=4096, batch=64),
+        fwht(n=1 << 20, batch=2),
+        cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [64, 1 << 14], 2, compute=cb.ComputeType.FP32),
+        cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [4096], 8, compute=cb.ComputeType.FP32, input_strides=[3]),
+        cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [1 << 15], 2, compute=cb.ComputeType.FP32,
+                    output_rounding=cb.OutputRounding.FINAL_STORAGE),
+    ]
+
+    def name_of(desc):
+        with cb.Plan(lib, desc) as plan:
+            return plan.algorithm_name()
+
+    bad = [cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [12], 1, compute=cb.ComputeType.FP32),
+           cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [64, 64], 1, compute=cb.ComputeType.FP32,
+                       output_rounding=cb.OutputRounding.FINAL_STORAGE)]
+
+    def refused(i):
+        try:
+            cb.Plan(lib, bad[i % 2])
+        except cb.AbiError as e:
+            return i % 2, e.status, e.detail
+        return None
+
+    serial = [name_of(d) for d in descs]
+    with ThreadPoolExecutor(max_workers=8) as pool:
+        for _ in range(4):
+            assert list(pool.map(name_of, descs * 4)) == serial * 4
+        errors = list(pool.map(refused, range(64)))
+    # Each thread reads its own error text, whichever refusal ran beside it.
+    expected = {0: (cb.Status.INVALID_VALUE, "power of two"), 1: (cb.Status.NOT_SUPPORTED, "rank one")}
+    for e in errors:
+        assert e is not None and e[1] == expected[e[0]][0] and expected[e[0]][1] in e[2], e
