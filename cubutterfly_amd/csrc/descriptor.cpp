@@ -360,11 +360,14 @@ Request lower_request(const cubutterflyDescriptor& d) {
         r.pitched = rows_pitched && n >= 4096;
     else if (d.op == CUBUTTERFLY_OPERATOR_FFT)  // one transform per tile from 2^12 points
         r.pitched = rows_pitched && !r.input_bit_reversed && !r.output_bit_reversed && n >= 4096;
-    // Logical orders: native to the NTT kernels, and to one-pass FFTs
-    // (n <= 2^14) on packed sides; FWHT orders and longer FFTs use the boundary.
+    // Logical orders: native to the NTT kernels, to one-pass FFTs (n <= 2^14)
+    // on packed sides, and as a bit-reversed output to the final row pass of
+    // longer FFTs; FWHT orders and bit-reversed input of longer FFTs use the
+    // boundary.
     const bool reversed = r.input_bit_reversed || r.output_bit_reversed;
     const bool native_orders =
-        d.op == CUBUTTERFLY_OPERATOR_NTT || (d.op == CUBUTTERFLY_OPERATOR_FFT && n <= (std::size_t{1} << 14));
+        d.op == CUBUTTERFLY_OPERATOR_NTT ||
+        (d.op == CUBUTTERFLY_OPERATOR_FFT && (n <= (std::size_t{1} << 14) || !r.input_bit_reversed));
     r.boundary = d.rank == 1 && !embedding && !r.pitched && (strided || (reversed && !native_orders));
     switch (d.op) {
         case CUBUTTERFLY_OPERATOR_FWHT:

@@ -209,7 +209,12 @@ constexpr int pass_digit_bits(int lb, bool single, int ord) { return (ord & 16) 
 // bit 3 writes row k of the block's bit-reversed row order back as row k,
 // transformed, in natural order (the last step of a rank-2 transform whose
 // first axis ran as column passes). Bit 4 gives one-pass tiles of 2^13 and
-// 2^14 points 4-bit digits (pass_digit_bits).
+// 2^14 points 4-bit digits (pass_digit_bits). Bit 5 makes the final row pass
+// of a two- or three-pass transform write the bit-reversed logical order:
+// output k = k1 + 2^l1 k2 belongs at bitrev(k) = bitrev(k1) 2^l2 +
+// bitrev(k2), and the row pass reads tile row k1 from row bitrev(k1) of the
+// intermediate, so each row goes back to the row it came from, in the DIF
+// result's own order (no reversal, no transpose).
 template <int LT, int LI, bool COL, bool SINGLE, bool INV, int ORD = 0>
 struct FftPass {
     static constexpr int LB = LT + LI;
@@ -443,7 +448,7 @@ struct FftPass {
     // 168.7 -> 156.4 us; on the 32-byte segments of 4096-point transposing
     // rows the hint measured 2.6x slower). Column passes write the
     // intermediate the next pass reads (nontemporal there: C3a 183 us).
-    static constexpr int kStoreAux = !COL && (SINGLE || LI >= 6 || (ORD & 8) != 0) ? 2 : 0;
+    static constexpr int kStoreAux = !COL && (SINGLE || LI >= 6 || (ORD & 40) != 0) ? 2 : 0;
     static __device__ __forceinline__ void store_at(float2 x, __amdgpu_buffer_rsrc_t dst, std::uint32_t lane_bytes,
                                                     std::uint32_t reg_bytes) {
         if (kLaneOnly || reg_bytes < 4096u) buffer_store<float2, kStoreAux>(x, dst, lane_bytes + reg_bytes);
@@ -678,6 +683,11 @@ struct FftPass {
             const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
             i = brev(xp, LT) | (rr << LT);
             off = ((k0 + rr) << LT) + xp;
+        } else if constexpr ((ORD & 32) != 0) {  // bit-reversed output: rows go back where they were read
+            const std::uint32_t xp = g & ((1u << LT) - 1u), rr = g >> LT;
+            const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
+            i = xp | (rr << LT);
+            off = (brev(k0 + rr, a.l1) << LT) + xp;
         } else {  // grid transpose: tile rows are bitrev(k0 + rr) of one transform
             const std::uint32_t rr = g & ((1u << LI) - 1u), cp = g >> LI;
             const std::uint32_t k0 = tl.row0 & ((1u << a.l1) - 1u);
@@ -904,6 +914,10 @@ void add() {
         registry()[Key{LT, LI, COL, SINGLE, false, 3}] = &launch<LT, LI, COL, SINGLE, false, 3>;
         registry()[Key{LT, LI, COL, SINGLE, true, 3}] = &launch<LT, LI, COL, SINGLE, true, 3>;
     }
+    if constexpr (!COL && !SINGLE) {  // final row passes writing the bit-reversed order
+        registry()[Key{LT, LI, COL, SINGLE, false, 32}] = &launch<LT, LI, COL, SINGLE, false, 32>;
+        registry()[Key{LT, LI, COL, SINGLE, true, 32}] = &launch<LT, LI, COL, SINGLE, true, 32>;
+    }
 }
 
 // Shapes: one pass for m <= 14 (2^12-point tiles, 2^13 / 2^14 for m = 13,
@@ -1005,12 +1019,15 @@ Launch find(const Key& k) {
     return fn;
 }
 
+// The final row pass's order flag: 32 for a bit-reversed output order.
+int row_ord(const Request& r) { return r.output_bit_reversed ? 32 : 0; }
+
 // A two-pass split l1 + l2 = m whose column and row kernels both exist.
-bool split_available(int m, int l1, bool inverse) {
+bool split_available(int m, int l1, bool inverse, int ord = 0) {
     const int l2 = m - l1;
     return l1 >= 1 && l2 >= 1 && l1 <= 14 && l2 <= 14 &&
            lookup(Key{l1, col_lines(l1, l2), true, false, inverse}) != nullptr &&
-           lookup(Key{l2, row_lines(l1, l2), false, false, inverse}) != nullptr;
+           lookup(Key{l2, row_lines(l1, l2), false, false, inverse, ord}) != nullptr;
 }
 
 constexpr const char* kTwoPassName = "fft-c64-two-pass-r16";
@@ -1038,12 +1055,12 @@ int parse_split(int m, const std::string& name) {
 // only on the bits below it), and the row pass of a (a + b) x c split. Every
 // pass moves segments of 2^min(14 - bits, ...) elements (512 bytes at
 // 8 + 8 + 8), where the two-pass 12 + 12 split moves 32-byte segments.
-bool split3_available(int m, int a, int b, bool inverse) {
+bool split3_available(int m, int a, int b, bool inverse, int ord = 0) {
     const int c = m - a - b;
     return a >= 1 && b >= 1 && c >= 1 && a <= 14 && b <= 14 && c <= 14 &&
            lookup(Key{a, col_lines(a, b + c), true, false, inverse}) != nullptr &&
            lookup(Key{b, col_lines(b, c), true, false, inverse}) != nullptr &&
-           lookup(Key{c, row_lines(a + b, c), false, false, inverse}) != nullptr;
+           lookup(Key{c, row_lines(a + b, c), false, false, inverse, ord}) != nullptr;
 }
 
 std::string three_pass_name(int m, int a, int b) {
@@ -1066,11 +1083,11 @@ bool parse_split3(int m, const std::string& name, int& a, int& b) {
 // two-pass split's segments drop to 32 or 64 bytes (measured on MI355X:
 // 2^24 x 1 in 171 us against 199 us, 2^23 x 2 in 164 us against 188 us),
 // a = m / 3 top bits and half the rest in the middle.
-bool default_three_pass(int m, bool inverse, int& a, int& b) {
+bool default_three_pass(int m, bool inverse, int& a, int& b, int ord = 0) {
     if (m < 23) return false;
     a = m / 3;
     b = (m - a) / 2;
-    return split3_available(m, a, b, inverse);
+    return split3_available(m, a, b, inverse, ord);
 }
 
 // Level-twiddle tables of a 2^log_len-point transform: A[k] = w^(4096 k),
@@ -1140,7 +1157,7 @@ class FftExecutor final : public Executor {
             sb.args.tiles = unsigned(b_tiles);
             sb.args.scale = 1.0f;
             sb.args.in_pitch = sb.args.out_pitch = std::uint64_t{1} << (tm + tl);
-            Step sc{find(Key{int(tl), c_li, false, false, r.inverse}), base, true, false};
+            Step sc{find(Key{int(tl), c_li, false, false, r.inverse, row_ord(r)}), base, true, false};
             sc.args.l1 = ta + tm;
             sc.args.l2 = tl;
             sc.args.rows = unsigned(r.batch << (ta + tm));
@@ -1178,7 +1195,7 @@ class FftExecutor final : public Executor {
             a.args.scale = 1.0f;
             a.args.in_pitch = in_pitch;
             a.args.out_pitch = r.n;  // the workspace is packed
-            Step b{find(Key{int(l2), row_li, false, false, r.inverse}), base, true, false};
+            Step b{find(Key{int(l2), row_li, false, false, r.inverse, row_ord(r)}), base, true, false};
             b.args.l1 = l1;
             b.args.l2 = l2;
             b.args.rows = unsigned(r.batch << l1);
@@ -1239,8 +1256,7 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r) {
     const int m = int(r.log_n);
     supported(m >= 1 && m <= 24, "complex FFT lengths above 2^24 are not yet lowered for gfx950");
     require(!r.pitched || single_li(m) == 0, "pitched FFT rows need n >= 2^12 (one transform per tile)");
-    require(!(r.input_bit_reversed || r.output_bit_reversed) || m <= 14,
-            "bit-reversed FFT orders are native to one-pass lengths only");
+    require(!r.input_bit_reversed || m <= 14, "bit-reversed FFT input is native to one-pass lengths only");
     // Order and pitch suffixes ride on every candidate name.
     std::string variant = r.variant;
     const std::string suffix = order_suffix(r) + (r.pitched ? "-pitched" : "");
@@ -1261,13 +1277,15 @@ std::unique_ptr<Executor> make_fft_executor(const Request& r) {
         return std::make_unique<FftExecutor>(r, 0, 0, radix16);
     }
     int top = 0, mid = 0;
-    if (variant.empty() && default_three_pass(m, r.inverse, top, mid)) return std::make_unique<FftExecutor>(r, top, mid);
+    if (variant.empty() && default_three_pass(m, r.inverse, top, mid, row_ord(r)))
+        return std::make_unique<FftExecutor>(r, top, mid);
     if (parse_split3(m, variant, top, mid)) {
-        supported(split3_available(m, top, mid, r.inverse), "'" + r.variant + "' is not a lowering of this FFT");
+        supported(split3_available(m, top, mid, r.inverse, row_ord(r)),
+                  "'" + r.variant + "' is not a lowering of this FFT");
         return std::make_unique<FftExecutor>(r, top, mid);
     }
     const int split = variant.empty() ? split_l1(m) : parse_split(m, variant);
-    supported(split > 0 && split_available(m, split, r.inverse),
+    supported(split > 0 && split_available(m, split, r.inverse, row_ord(r)),
               "'" + r.variant + "' is not a lowering of this FFT");
     return std::make_unique<FftExecutor>(r, split);
 }
@@ -1488,16 +1506,17 @@ std::vector<std::string> fft_candidates(const Request& r) {
     }
     std::vector<std::string> names;
     int top = 0, mid = 0;
-    const bool three = default_three_pass(m, r.inverse, top, mid);
+    const int ord = row_ord(r);
+    const bool three = default_three_pass(m, r.inverse, top, mid, ord);
     if (three) names.push_back(three_pass_name(m, top, mid) + suffix);
-    names.push_back(two_pass_name(m, split_l1(m)) + suffix);
+    if (split_available(m, split_l1(m), r.inverse, ord)) names.push_back(two_pass_name(m, split_l1(m)) + suffix);
     for (int l1 : {split_l1(m) - 1, split_l1(m) + 1, split_l1(m) - 2, split_l1(m) + 2})
-        if (split_available(m, l1, r.inverse)) names.push_back(two_pass_name(m, l1) + suffix);
+        if (split_available(m, l1, r.inverse, ord)) names.push_back(two_pass_name(m, l1) + suffix);
     // Three passes from 2^18: splits within one bit of m / 3 per pass.
     if (m >= 18)
         for (int a = m / 3 - 1; a <= m / 3 + 1; ++a)
             for (int b = m / 3 - 1; b <= m / 3 + 1; ++b)
-                if (std::abs(m - a - b - m / 3) <= 1 && split3_available(m, a, b, r.inverse) &&
+                if (std::abs(m - a - b - m / 3) <= 1 && split3_available(m, a, b, r.inverse, ord) &&
                     !(three && a == top && b == mid))
                     names.push_back(three_pass_name(m, a, b) + suffix);
     return names;

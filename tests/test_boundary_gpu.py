@@ -165,15 +165,19 @@ def test_in_place_interleaved(torch_gpu, lib, stream):
 
 
 def test_fft_logical_order_plan(torch_gpu, lib):
-    # One-pass lengths take bit-reversed orders natively; longer ones through
-    # the boundary.
+    # One-pass lengths take bit-reversed orders natively; longer ones write a
+    # bit-reversed output natively (final row pass) and gather a bit-reversed
+    # input through the boundary.
     t = cb.describe(cb.Operator.FFT, cb.DataType.COMPLEX_FP32, [64], compute=cb.ComputeType.FP32, batch=2, output_orders=[cb.LogicalOrder.BIT_REVERSED], input_orders=[cb.LogicalOrder.NATURAL])
     with cb.Plan(lib, t) as plan:
         assert plan.algorithm_name() == "fft-c64-resident-r16-bitrev-out"
     t["shape"] = [1 << 15]
     with cb.Plan(lib, t) as plan:
+        assert plan.algorithm_name() == "fft-c64-two-pass-r16-bitrev-out"
+    t["output_orders"], t["input_orders"] = [int(cb.LogicalOrder.NATURAL)], [int(cb.LogicalOrder.BIT_REVERSED)]
+    with cb.Plan(lib, t) as plan:
         assert plan.algorithm_name().startswith("semantic-boundary[fft-c64")
-        assert plan.mapping()["output_bit_reversed"] is True
+        assert plan.mapping()["input_bit_reversed"] is True
 
 
 def test_packed_ntt_orders_stay_native(torch_gpu, lib):
