@@ -29,9 +29,15 @@ inline void require(bool condition, const std::string& message) {
 inline void supported(bool condition, const std::string& message) {
     if (!condition) throw NotSupported(message);
 }
+// A failed HIP call becomes this library's error status. The runtime's
+// last-error state is cleared first: the library reports the error itself,
+// and a caller's next hipGetLastError (torch checks it after every call)
+// must not see it again.
 inline void hip_check(hipError_t status, const char* what) {
-    if (status != hipSuccess)
+    if (status != hipSuccess) {
+        (void)hipGetLastError();
         throw HipError(std::string(what) + ": " + hipGetErrorString(status));
+    }
 }
 
 inline bool is_pow2(std::uint64_t n) { return n != 0 && (n & (n - 1)) == 0; }
@@ -59,6 +65,7 @@ class DeviceBuffer {
         if (bytes == 0) return;
         if (hipMalloc(&ptr_, bytes) != hipSuccess) {
             ptr_ = nullptr;
+            (void)hipGetLastError();  // reported as ALLOC_FAILED / a runtime status, not left for the caller
             throw std::bad_alloc();
         }
         bytes_ = bytes;

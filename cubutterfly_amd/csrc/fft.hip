@@ -883,10 +883,13 @@ void launch(const FftArgs& a, hipStream_t stream) {
     constexpr int threads = int(FftPass<LT, LI, COL, SINGLE, INV, ORD>::T);
     static const std::uint64_t resident = [] {
         const void* fn = reinterpret_cast<const void*>(&fft_pass_kernel<LT, LI, COL, SINGLE, INV, ORD>);
-        if (bytes > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+        if (bytes > 65536 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) != hipSuccess)
+            (void)hipGetLastError();
         int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, bytes) != hipSuccess || per_cu < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, bytes) != hipSuccess || per_cu < 1) {
+            (void)hipGetLastError();
             per_cu = 1;
+        }
         return std::uint64_t(per_cu) * std::uint64_t(device_cu_count());
     }();
     std::uint64_t grid = a.tiles;

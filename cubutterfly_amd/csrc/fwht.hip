@@ -959,8 +959,10 @@ unsigned wide_resident() {
         int per_cu = 0;
         const void* fn = reinterpret_cast<const void*>(&fwht_wide_kernel<LOG_N, Io, true>);
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 1 << (LOG_N - kLW), 0) != hipSuccess ||
-            per_cu < 1)
+            per_cu < 1) {
+            (void)hipGetLastError();
             per_cu = 1;
+        }
         return unsigned(per_cu) * unsigned(device_cu_count());
     }();
     return resident;

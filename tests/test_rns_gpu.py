@@ -282,3 +282,29 @@ def test_prepare_refuses_stream_capture(torch_gpu, rlib):
         assert not plan.info()["prepared"]
         plan.prepare(s.cuda_stream)  # outside capture it prepares normally
         assert plan.info()["prepared"]
+
+
+def test_prepare_that_cannot_allocate_leaves_the_plan_intact(torch_gpu, rlib):
+    # One polynomial at word offset 2^36 (a 512 GiB input extent): Prepare's
+    # sweep cannot allocate its buffers and fails with a runtime status; the
+    # plan stays unprepared and intact -- Prepare may be called again, and
+    # Execute still refuses it (the reference's allocation-failure contract,
+    # tests/test_rns_mapping_failure.cu, src/rns_ntt.cu:761-785).
+    log_n = 12
+    q = PRIMES[0]
+    root = oracle.find_primitive_root(log_n + 1, q)
+    offset = 1 << 36
+    cfg = rns.request(log_n, [(q, root)], polynomials=[{"domain": 0, "input_offset": offset,
+                                                         "output_offset": 0}])
+    stream = torch_gpu.cuda.Stream().cuda_stream
+    with rns.RnsPlan(rlib, cfg) as plan:
+        for _ in range(2):
+            with pytest.raises(cb.AbiError) as e:
+                plan.prepare(stream)
+            assert e.value.status == 2
+            assert plan.info()["prepared"] is False
+        x = to_device(torch_gpu, np.zeros(1 << log_n, np.uint64))
+        y = to_device(torch_gpu, np.zeros(1 << log_n, np.uint64))
+        with pytest.raises(cb.AbiError) as e:
+            plan.execute(x, y, stream)
+        assert e.value.status == 1

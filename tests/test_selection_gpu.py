@@ -279,3 +279,22 @@ def test_measure_refuses_stream_capture(torch_gpu, lib):
         with pytest.raises(cb.AbiError) as e:
             cb.Plan(lib, fft(16, 1), policy=cb.AlgorithmPolicy.MEASURE, stream=s.cuda_stream)
         assert e.value.status == cb.Status.NOT_SUPPORTED and "capture" in e.value.detail
+
+
+def test_measure_without_room_for_scratch_keeps_the_static_model(torch_gpu, lib, stream, tmp_path):
+    # A request larger than the device (20 Mi rows of 4096 FP32 points, 320 GiB
+    # each way): MEASURE cannot allocate its timing buffers, so the plan keeps
+    # the static model's lowering and says why, instead of failing (the
+    # reference's tuner falls back the same way when a candidate cannot run).
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [4096], 20 << 20, compute=cb.ComputeType.FP32)
+    with cb.Plan(lib, t) as plan:
+        static = plan.algorithm_name()
+    with cb.Plan(lib, t, policy=cb.AlgorithmPolicy.MEASURE, stream=stream, cache_path=tmp_path / "c.tsv") as plan:
+        assert plan.algorithm_name() == static
+        assert plan.selection_source() != cb.SelectionSource.RUNTIME_MEASURED
+        assert "MEASURE skipped: could not allocate" in plan.selection_reason()
+    assert not (tmp_path / "c.tsv").exists() or (tmp_path / "c.tsv").read_text() == ""
+    # The failed allocation is reported by the plan, not left in the HIP
+    # runtime for the caller's next call to find.
+    torch_gpu.zeros(16, device="cuda").add_(1)
+    torch_gpu.cuda.synchronize()
