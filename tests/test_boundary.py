@@ -38,6 +38,18 @@ def test_strided_input_uses_the_boundary(lib):
         m = plan.mapping()
         assert m["kind"] == "semantic-boundary" and m["input_stride"] == 2 and m["input_batch_stride"] == 20
         assert m["child"]["operator"] == "fwht"
+        assert m["direct_input"] is False and m["direct_output"] is True
+
+
+@pytest.mark.parametrize("reversed_input", [True, False])
+def test_packed_natural_side_skips_its_move(lib, reversed_input):
+    # One bit-reversed side: the other, packed in natural order, is read or
+    # written by the packed plan itself.
+    orders = {"input_orders" if reversed_input else "output_orders": [cb.LogicalOrder.BIT_REVERSED]}
+    with cb.Plan(lib, fwht(n=1024, batch=4, **orders)) as plan:
+        m = plan.mapping()
+        assert plan.algorithm_name().startswith("semantic-boundary[")
+        assert m["direct_input"] is (not reversed_input) and m["direct_output"] is reversed_input
 
 
 def test_default_batch_stride_is_the_axis_span(lib):

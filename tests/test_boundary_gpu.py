@@ -93,12 +93,15 @@ LAYOUTS = [
     ((1, 0, False), (1, 0, True)),       # packed, logical order only
     ((1, -8, False), (1, -4, False)),    # pitched rows on both sides
     ((1, -8, False), (1, -3, False)),    # pitched input, odd output pitch
+    ((1, -40, True), (1, -24, True)),    # pitched rows, bit-reversed on both sides
 ]
 
 
+@pytest.mark.parametrize("n", [64, 2048])
 @pytest.mark.parametrize("in_layout,out_layout", LAYOUTS)
-def test_fwht_fp32(torch_gpu, lib, stream, in_layout, out_layout):
-    n, batch = 64, 5
+def test_fwht_fp32(torch_gpu, lib, stream, n, in_layout, out_layout):
+    # 2048: bit-reversed unit-stride rows move through the tiled reversal.
+    batch = 5
     x_flat, rows, out_pos, out_len = case(n, batch, np.float32, 1, in_layout, out_layout, 0)
     t = transform(cb.Operator.FWHT, n, batch, in_layout, out_layout, storage=cb.DataType.FP32,
                   compute=cb.ComputeType.FP32)
@@ -108,9 +111,10 @@ def test_fwht_fp32(torch_gpu, lib, stream, in_layout, out_layout):
     np.testing.assert_array_equal(got, expected)
 
 
+@pytest.mark.parametrize("n", [128, 1024])
 @pytest.mark.parametrize("in_layout,out_layout", LAYOUTS)
-def test_fwht_fp16_final(torch_gpu, lib, stream, in_layout, out_layout):
-    n, batch, scale = 128, 3, 128 ** -0.5
+def test_fwht_fp16_final(torch_gpu, lib, stream, n, in_layout, out_layout):
+    batch, scale = 3, n ** -0.5
     x_flat, rows, out_pos, out_len = case(n, batch, np.float16, 2, in_layout, out_layout, 0)
     t = transform(cb.Operator.FWHT, n, batch, in_layout, out_layout, storage=cb.DataType.FP16,
                   compute=cb.ComputeType.FP32, output_scale=scale, output_rounding=cb.OutputRounding.FINAL_STORAGE)
