@@ -26,7 +26,12 @@
 // the rank-1 stage order. A rank-N FWHT whose point count a single rank-1
 // plan covers therefore runs as that one plan, bit-identically (the inverse
 // with normalisation keeps the per-axis composition, whose per-axis 1/n
-// scaling rounds differently in the subnormal range).
+// scaling rounds differently in the subnormal range). Longer FWHTs, and
+// rank-N ones normalised per axis, run the innermost axis as one packed row
+// plan (at least 64 points) and every other axis, lowest bits first, as
+// in-place column passes of at most 2^7 rows held in registers: the same
+// stages in the same order, with no transposes. A rank-1 FWHT beyond 2^13
+// points is factored into such axes and divides by n once, in its last pass.
 //
 // Strided sides and bit-reversed logical orders are handled as in the
 // rank-1 semantic boundary: an N-dimensional gather into packed natural
@@ -156,14 +161,124 @@ void launch_nd_boundary(bool gather, const void* src, void* dst, std::uint64_t c
     hip_check(hipGetLastError(), "composite gather / scatter launch");
 }
 
-// One step of the schedule: an axis plan, or a batched transpose moving one
-// axis innermost.
+// FWHT stages over the row bits of G blocks of 2^LOG_L rows x 2^log_cols
+// columns (row pitch 2^log_cols elements): for each block and column, the
+// values x[i] of rows i = 0 .. 2^LOG_L - 1 go through the stages of bit 0,
+// 1, ..., LOG_L - 1 of i (pairs i, i + h -> a + b, a - b), then are
+// multiplied by `scale` where `apply_scale` is set. Each lane holds VEC
+// consecutive columns of all the rows in registers, so one load instruction
+// of a wave covers 64 * VEC consecutive elements of a row; no LDS and no
+// barriers. A lane writes exactly the elements it read, so src == dst is
+// allowed (no __restrict__).
+constexpr std::uint32_t kMaxColumnBits = 7;  // rows * VEC <= 128 registers of data
+
+template <int VEC>
+struct ColumnVector;
+template <>
+struct ColumnVector<1> {
+    using type = float;
+};
+template <>
+struct ColumnVector<2> {
+    using type = float __attribute__((ext_vector_type(2)));
+};
+template <>
+struct ColumnVector<4> {
+    using type = float __attribute__((ext_vector_type(4)));
+};
+
+template <int LOG_L, int VEC>
+__global__ __launch_bounds__(kThreads) void fwht_columns_kernel(const float* src, float* dst, std::uint64_t vectors,
+                                                                std::uint32_t log_cols, float scale, int apply_scale) {
+    constexpr int L = 1 << LOG_L;
+    constexpr std::uint32_t kLogVec = VEC == 4 ? 2 : VEC == 2 ? 1 : 0;
+    using V = typename ColumnVector<VEC>::type;
+    const std::uint64_t v = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (v >= vectors) return;
+    const std::uint32_t log_vectors = log_cols - kLogVec;  // column vectors per row
+    const std::uint64_t block = v >> log_vectors;
+    const std::uint64_t base = (block << (LOG_L + log_cols)) + ((v & ((std::uint64_t{1} << log_vectors) - 1)) << kLogVec);
+    V x[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i) x[i] = *reinterpret_cast<const V*>(src + base + (std::uint64_t(i) << log_cols));
+#pragma unroll
+    for (int h = 1; h < L; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+            if ((i & h) == 0) {
+                const V a = x[i], b = x[i + h];
+                x[i] = a + b;
+                x[i + h] = a - b;
+            }
+        }
+    }
+    if (apply_scale) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) x[i] = x[i] * scale;
+    }
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+        __builtin_nontemporal_store(x[i], reinterpret_cast<V*>(dst + base + (std::uint64_t(i) << log_cols)));
+}
+
+template <int LOG_L>
+void launch_fwht_columns_rows(const float* src, float* dst, std::uint64_t count, std::uint32_t log_cols, int vec,
+                              float scale, bool apply_scale, hipStream_t stream) {
+    const std::uint64_t vectors = count >> (LOG_L + (vec == 4 ? 2 : vec == 2 ? 1 : 0));
+    const std::uint64_t blocks = (vectors + kThreads - 1) / kThreads;
+    require(blocks < (std::uint64_t{1} << 31), "FWHT column pass grid too large");
+    const dim3 grid{unsigned(blocks)}, block{kThreads};
+    if constexpr (LOG_L <= 5) {
+        if (vec == 4) {
+            hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 4>), grid, block, 0, stream, src, dst, vectors, log_cols,
+                               scale, int(apply_scale));
+            return;
+        }
+    }
+    if constexpr (LOG_L <= 6) {
+        if (vec == 2) {
+            hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 2>), grid, block, 0, stream, src, dst, vectors, log_cols,
+                               scale, int(apply_scale));
+            return;
+        }
+    }
+    hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 1>), grid, block, 0, stream, src, dst, vectors, log_cols, scale,
+                       int(apply_scale));
+}
+
+// Column pass over `count` FP32 elements (G blocks of 2^log_rows x
+// 2^log_cols), src == dst allowed. The widest vector both pointers' alignment
+// and the register budget allow.
+void launch_fwht_columns(const float* src, float* dst, std::uint64_t count, std::uint32_t log_rows,
+                         std::uint32_t log_cols, float scale, bool apply_scale, hipStream_t stream) {
+    require(log_rows >= 1 && log_rows <= kMaxColumnBits && log_cols >= 6, "FWHT column pass shape");
+    const auto align = reinterpret_cast<std::uintptr_t>(src) | reinterpret_cast<std::uintptr_t>(dst);
+    int vec = align % 16 == 0 ? 4 : align % 8 == 0 ? 2 : 1;
+    if (log_rows == 6) vec = std::min(vec, 2);
+    if (log_rows == 7) vec = 1;
+    switch (log_rows) {
+        case 1: launch_fwht_columns_rows<1>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
+        case 2: launch_fwht_columns_rows<2>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
+        case 3: launch_fwht_columns_rows<3>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
+        case 4: launch_fwht_columns_rows<4>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
+        case 5: launch_fwht_columns_rows<5>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
+        case 6: launch_fwht_columns_rows<6>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
+        default: launch_fwht_columns_rows<7>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
+    }
+    hip_check(hipGetLastError(), "FWHT column pass launch");
+}
+
+// One step of the schedule: an axis plan, a batched transpose moving one
+// axis innermost, or an in-place FWHT column pass over some bits of an axis.
 struct Step {
     bool transpose = false;
     std::size_t child = 0;                // axis plan index (transpose == false)
     std::uint32_t axis = 0;               // logical axis it transforms
-    std::uint64_t groups = 0;             // transpose: blocks, log2 rows / cols
+    std::uint64_t groups = 0;             // transpose / columns: blocks, log2 rows / cols
     std::uint32_t log_rows = 0, log_cols = 0;
+    bool columns = false;                 // FWHT column pass (in place)
+    bool apply_scale = false;             // columns: times `scale` after the stages
+    float scale = 1.0f;
 };
 
 class CompositeExecutor final : public Executor {
@@ -213,6 +328,43 @@ class CompositeExecutor final : public Executor {
         } else if (flatten) {
             children_.push_back(plan_executor(axis_request(r.n, r.batch), sel));
             steps_.push_back(Step{false, 0, 0, 0, 0, 0});
+        } else if (r.op == Op::Fwht && rank >= 2 && r.element_bytes == 4 && logs[rank - 1] >= 6) {
+            // FWHT: the innermost axis as one packed row plan, then every
+            // other axis, lowest bits first, as in-place column passes of at
+            // most 2^7 rows over rows at least 64 elements long -- the
+            // stages in index-bit order, no transposes. A factored rank-1
+            // FWHT divides by n once, after its last stage (the reference's
+            // rank-1 normalisation); a rank-N FWHT by each axis's extent
+            // after that axis.
+            fwht_columns_ = true;
+            const bool normalise = r.inverse && r.normalize;
+            Request rows = axis_request(r.extents[rank - 1], r.batch * (r.n / r.extents[rank - 1]));
+            if (r.factored) rows.normalize = false;
+            children_.push_back(plan_executor(rows, sel));
+            Step first;
+            first.axis = rank - 1;
+            steps_.push_back(first);
+            std::uint32_t log_cols = logs[rank - 1];
+            for (std::uint32_t a = rank - 1; a-- > 0;) {
+                const std::uint32_t bits = logs[a];
+                const std::uint32_t chunks = (bits + kMaxColumnBits - 1) / kMaxColumnBits;
+                std::uint32_t done = 0;
+                for (std::uint32_t k = 0; k < chunks; ++k) {
+                    Step s;
+                    s.columns = true;
+                    s.axis = a;
+                    s.log_rows = (bits - done) / (chunks - k);  // balanced chunks
+                    s.log_cols = log_cols + done;
+                    s.groups = r.batch * (r.n >> (s.log_rows + s.log_cols));
+                    done += s.log_rows;
+                    if (normalise && done == bits && (!r.factored || a == 0)) {
+                        s.apply_scale = true;
+                        s.scale = static_cast<float>(1.0 / double(r.factored ? r.n : r.extents[a]));
+                    }
+                    steps_.push_back(s);
+                }
+                log_cols += bits;
+            }
         } else {
             // Innermost axis first; each axis is first moved innermost.
             std::vector<std::uint32_t> order(rank);
@@ -243,20 +395,28 @@ class CompositeExecutor final : public Executor {
             for (std::uint32_t axis = 0; axis < rank; ++axis) move_innermost(axis);
         }
         for (const auto& c : children_) {
-            names.push_back(c->algorithm);
+            if (!fwht_columns_) names.push_back(c->algorithm);
             child_ws_ = std::max(child_ws_, c->workspace_bytes());
         }
+        if (fwht_columns_)
+            for (const auto& s : steps_)
+                names.push_back(s.columns ? "fwht-fp32-columns-l" + std::to_string(s.log_rows)
+                                          : children_[s.child]->algorithm);
         std::string joined;
         for (std::size_t i = 0; i < names.size(); ++i) joined += (i ? "," : "") + names[i];
         algorithm = std::string(r.factored     ? "fwht-factored"
                                 : rank == 1    ? "zero-extended"
                                 : transposing_ ? "rank2-transposing"
                                 : columns_     ? "rank2-columns"
+                                : fwht_columns_ ? (rank == 2 ? "rank2-fwht-columns" : "rankN-fwht-columns")
                                 : flatten      ? (rank == 2 ? "rank2-kronecker" : "rankN-kronecker")
                                                : (rank == 2 ? "rank2-transpose" : "rankN-composite")) +
                     "[" + joined + "]" + (direct_in_ ? "+direct-input" : "") + (direct_out_ ? "+direct-output" : "");
         reason = transposing_ ? "each axis one row pass with a transposing store (innermost axis first)"
                  : columns_   ? "axis 0 as column passes over each block, then the rows stored in natural order"
+                 : fwht_columns_
+                     ? "innermost axis one row plan, the other axes in-place column passes of at most 2^7 rows "
+                       "(FWHT stages in index-bit order, no transposes)"
                  : flatten    ? "FWHT of the flattened point count: H(n0 n1) = H(n0) (x) H(n1), same stage order"
                               : "one batched rank-1 plan per axis, innermost first, tiled transposes between";
         if (r.embedding) reason += "; sides zero-extended to / cut from the power-of-two extents";
@@ -267,6 +427,7 @@ class CompositeExecutor final : public Executor {
             .field("rank", rank)
             .field("lowering", transposing_ ? "transposing-rows"
                                : columns_   ? "columns-then-rows"
+                               : fwht_columns_ ? "rows-then-columns"
                                : flatten    ? "kronecker"
                                             : "transpose")
             .field("zero_extended", r.embedding);
@@ -282,7 +443,11 @@ class CompositeExecutor final : public Executor {
         w.begin_array("schedule");
         for (const auto& s : steps_) {
             w.begin_object();
-            if (s.transpose) {
+            if (s.columns) {
+                w.field("step", "columns").field("axis", s.axis).field("blocks", s.groups)
+                    .field("rows", std::uint64_t{1} << s.log_rows).field("cols", std::uint64_t{1} << s.log_cols)
+                    .field("scale", s.apply_scale ? double(s.scale) : 1.0);
+            } else if (s.transpose) {
                 w.field("step", "transpose").field("blocks", s.groups).field("rows", std::uint64_t{1} << s.log_rows)
                     .field("cols", std::uint64_t{1} << s.log_cols);
             } else if (columns_) {
@@ -308,11 +473,21 @@ class CompositeExecutor final : public Executor {
         std::size_t used = direct_in_ ? 0 : 1;
         int next = direct_in_ ? 0 : 1;
         for (std::size_t i = 0; i < steps_.size(); ++i) {
-            if (i + 1 == steps_.size() && direct_out_) break;
+            if (steps_[i].columns) continue;  // in place
+            if (i == last_moving() && direct_out_) break;
             used = std::max<std::size_t>(used, std::size_t(next) + 1);
             next ^= 1;
         }
         return used;
+    }
+
+    // The last step that writes a new buffer (the in-place column passes
+    // after it run on its destination).
+    std::size_t last_moving() const {
+        std::size_t last = 0;
+        for (std::size_t i = 0; i < steps_.size(); ++i)
+            if (!steps_[i].columns) last = i;
+        return last;
     }
 
     bool columns() const { return columns_; }
@@ -336,18 +511,25 @@ class CompositeExecutor final : public Executor {
         // not in (the caller's input counts as neither).
         int next = 0;
         const void* cur = in;
+        void* cur_writable = nullptr;  // cur, once it is no longer the caller's input
         if (!direct_in_) {
             move(true, in, buffer[0], count, in_side_, stream);
-            cur = buffer[0];
+            cur = cur_writable = buffer[0];
             next = 1;
         }
+        const std::size_t last = last_moving();
         for (std::size_t i = 0; i < steps_.size(); ++i) {
-            const bool last = i + 1 == steps_.size();
-            void* dst = last && direct_out_ ? out : buffer[next];
             const auto& s = steps_[i];
+            if (s.columns) {
+                require(cur_writable != nullptr, "an FWHT column pass runs on a step's destination");
+                launch_fwht_columns(static_cast<const float*>(cur_writable), static_cast<float*>(cur_writable),
+                                    count, s.log_rows, s.log_cols, s.scale, s.apply_scale, stream);
+                continue;
+            }
+            void* dst = i == last && direct_out_ ? out : buffer[next];
             if (s.transpose) transpose(cur, dst, s, stream);
             else children_[s.child]->execute(cur, dst, child_ws, stream);
-            cur = dst;
+            cur = cur_writable = dst;
             next = dst == buffer[0] ? 1 : 0;
         }
         if (!direct_out_) move(false, cur, out, count, out_side_, stream);
@@ -435,7 +617,7 @@ class CompositeExecutor final : public Executor {
     }
 
     Request r_;
-    bool transposing_ = false, columns_ = false;
+    bool transposing_ = false, columns_ = false, fwht_columns_ = false;
     bool direct_in_ = false, direct_out_ = false;
     NdSide in_side_, out_side_;
     std::vector<std::unique_ptr<Executor>> children_;

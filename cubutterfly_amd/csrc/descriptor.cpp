@@ -248,9 +248,19 @@ void factor_long_fwht(Request& r) {
     require(r.op == Op::Fwht && r.rank == 1 && !r.factored && !r.embedding && !r.fp16_final &&
                 !r.input_bit_reversed && !r.output_bit_reversed,
             "only natural-order FP32 FWHT rows factor");
-    std::vector<std::uint32_t> bits;  // innermost first
-    for (std::uint32_t left = r.log_n; left > 0; left -= std::min<std::uint32_t>(left, 12))
-        bits.push_back(std::min<std::uint32_t>(left, 12));
+    // Innermost: one resident row of 2^12 points, or 2^13 where that saves a
+    // pass; then axes of at most 2^7 points (one in-place column pass each),
+    // as even as their count allows. 2^14 .. 2^20 points take two passes,
+    // 2^21 .. 2^27 three.
+    constexpr std::uint32_t kColumnBits = 7;
+    const std::uint32_t outer = r.log_n - 13;
+    const std::uint32_t passes = (outer + kColumnBits - 1) / kColumnBits;
+    const std::uint32_t inner = r.log_n - 12 <= passes * kColumnBits ? 12u : 13u;
+    std::vector<std::uint32_t> bits{inner};  // innermost first
+    for (std::uint32_t k = 0, done = 0; k < passes; ++k) {
+        bits.push_back((r.log_n - inner - done) / (passes - k));
+        done += bits.back();
+    }
     supported(bits.size() <= kMaxRank, "FWHT length exceeds the factored rank");
     r.factored = true;
     r.rank = std::uint32_t(bits.size());

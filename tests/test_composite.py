@@ -69,9 +69,32 @@ def test_rank3_schedule_restores_axis_order(lib):
         assert order == [0, 1, 2]
 
 
-def test_large_rank2_fwht_uses_transposes(lib):
-    # 2^14 points exceed one resident FWHT plan: per-axis composition.
+def test_large_rank2_fwht_uses_column_passes(lib):
+    # 2^14 points exceed one resident FWHT plan: the rows of axis 1, then axis
+    # 0 as one in-place column pass (no transposes, no workspace).
     with cb.Plan(lib, fwht([128, 128])) as plan:
+        assert plan.algorithm_name() == (
+            "rank2-fwht-columns[fwht-fp32-resident-r16,fwht-fp32-columns-l7]+direct-input+direct-output")
+        assert plan.workspace_size() == 0
+        steps = schedule(plan)
+        assert [s["step"] for s in steps] == ["axis", "columns"]
+        assert (steps[1]["axis"], steps[1]["rows"], steps[1]["cols"], steps[1]["blocks"]) == (0, 128, 128, 1)
+        assert steps[1]["scale"] == 1.0
+
+
+def test_normalised_rank2_fwht_scales_each_axis(lib):
+    # Axis 0 of 2^12 points splits into two column passes of 2^6 rows, lowest
+    # bits first; per-axis normalisation divides by 2^12 after the second.
+    with cb.Plan(lib, fwht([4096, 64], batch=2, inverse=True)) as plan:
+        steps = schedule(plan)
+        assert [s["step"] for s in steps] == ["axis", "columns", "columns"]
+        assert [(s["rows"], s["cols"], s["blocks"]) for s in steps[1:]] == [(64, 64, 2 * 64), (64, 64 * 64, 2)]
+        assert [s["scale"] for s in steps[1:]] == [1.0, 2.0 ** -12]
+
+
+def test_short_inner_axis_keeps_transposes(lib):
+    # Rows under 64 elements would make column passes read short segments.
+    with cb.Plan(lib, fwht([1024, 32], inverse=True)) as plan:
         assert plan.algorithm_name().startswith("rank2-transpose[")
 
 
@@ -167,16 +190,39 @@ def test_fwht_composition_is_the_flat_transform():
     assert not np.array_equal(other.view(np.uint32), flat.view(np.uint32))
 
 
-def test_long_fwht_is_factored(lib):
-    # FWHT beyond 2^13 points: axes of at most 2^12, lowest bits innermost.
-    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << 20], compute=cb.ComputeType.FP32, batch=2)
+@pytest.mark.parametrize("log_n,extents", [
+    (14, [4, 4096]), (19, [128, 4096]), (20, [128, 8192]), (21, [32, 16, 4096]), (26, [128, 128, 4096]),
+    (27, [128, 128, 8192]), (28, [64, 32, 32, 4096]),
+])
+def test_long_fwht_is_factored(lib, log_n, extents):
+    # FWHT beyond 2^13 points: a resident row of 2^12 points (2^13 where that
+    # saves a pass), then axes of at most 2^7 points, lowest bits innermost,
+    # each one in-place column pass.
+    n = 1 << log_n
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=2)
     with cb.Plan(lib, t) as plan:
-        assert plan.algorithm_name().startswith("fwht-factored[fwht-fp32-resident-r16,")
-        assert plan.physical_extents() == [1 << 20]
-        assert plan.input_size() == plan.output_size() == 2 * (1 << 20) * 4
+        assert plan.algorithm_name().startswith("fwht-factored[fwht-fp32-resident-r16,fwht-fp32-columns-l")
+        assert plan.physical_extents() == [n]
+        assert plan.input_size() == plan.output_size() == 2 * n * 4
+        assert plan.workspace_size() == 0
         m = plan.mapping()
-        assert m["extents"] == [256, 4096]
-        assert [s["axis"] for s in m["schedule"] if s["step"] == "axis"] == [1, 0]
+        assert m["extents"] == extents
+        steps = m["schedule"]
+        assert [s["step"] for s in steps] == ["axis"] + ["columns"] * (len(extents) - 1)
+        assert steps[0]["axis"] == len(extents) - 1
+        cols = extents[-1]
+        for s, e in zip(steps[1:], reversed(extents[:-1])):
+            assert (s["rows"], s["cols"], s["blocks"]) == (e, cols, 2 * n // (e * cols))
+            cols *= e
+
+
+def test_long_fwht_inverse_divides_once(lib):
+    # A rank-1 FWHT divides by n after its last stage: the last column pass
+    # multiplies by 2^-16 (the GPU tests pin the values, subnormal ones too).
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << 16], compute=cb.ComputeType.FP32, inverse=True)
+    with cb.Plan(lib, t) as plan:
+        steps = plan.mapping()["schedule"]
+        assert [s["scale"] for s in steps[1:]] == [2.0 ** -16]
 
 
 def test_long_fp16_fwht_is_promoted(lib):

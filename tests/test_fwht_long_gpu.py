@@ -1,7 +1,8 @@
-"""FWHT beyond one resident tile (n > 2^13): factored into axes of at most
-2^12 points, lowest index bits first, which is the reference's stage order
+"""FWHT beyond one resident tile (n > 2^13): factored into a resident row of
+2^12 or 2^13 points and axes of at most 2^7 points (in-place column passes),
+lowest index bits first, which is the reference's stage order
 (src/butterfly_reference.cpp:349-369), so results are bit-identical to the
-oracle. FP16 final-storage rows run as the reference's FP32 promotion
+oracle; the inverse divides by n once, after the last stage. FP16 final-storage rows run as the reference's FP32 promotion
 (src/butterfly.cu:1452-1470: widen, the FP32 transform, one narrowing of
 y * scale), bit-identical to the oracle's FP16 contract
 (tests/test_fwht_final_storage.py:28-40); bit-reversed orders gather through
@@ -170,6 +171,34 @@ def test_rank2_with_a_long_axis(torch_gpu, lib, stream, inverse):
     x = np.random.default_rng(31).standard_normal((batch, n0 * n1)).astype(np.float32)
     t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n0, n1], compute=cb.ComputeType.FP32, batch=batch,
                     inverse=inverse, normalize_inverse=inverse)
+    got = run_plan(torch_gpu, lib, t, x, stream)
+    want = oracle.fwht_f32(x, inverse=inverse, normalize=inverse)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("log_n,batch", [(16, 2), (20, 2), (21, 1)])
+def test_inverse_divides_once_subnormal(torch_gpu, lib, stream, log_n, batch):
+    # The reference divides by n once, after the last stage
+    # (src/operator_traits.cuh:110): with outputs in the subnormal range a
+    # per-pass 1/n_axis would round twice and differ from it.
+    x = (np.random.default_rng(40 + log_n).standard_normal((batch, 1 << log_n)) * 2.0 ** -120).astype(np.float32)
+    got = run_plan(torch_gpu, lib, fwht(1 << log_n, batch, inverse=True), x, stream)
+    want = oracle.fwht_f32(x, inverse=True, normalize=True, threads=oracle.default_threads())
+    assert np.count_nonzero((want != 0) & (np.abs(want) < np.finfo(np.float32).tiny)) > 1000
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("extents,inverse", [([4096, 64], True), ([64, 64, 64], False), ([64, 64, 64], True),
+                                             ([128, 2, 256], True)])
+def test_rank_n_column_passes(torch_gpu, lib, stream, extents, inverse):
+    # The innermost axis as rows, every other axis as in-place column passes
+    # of at most 2^7 rows (a 2^12 axis as two); per-axis normalisation.
+    batch, n = 2, int(np.prod(extents))
+    x = np.random.default_rng(33).standard_normal((batch, n)).astype(np.float32)
+    t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, extents, compute=cb.ComputeType.FP32, batch=batch,
+                    inverse=inverse, normalize_inverse=inverse)
+    with cb.Plan(lib, t) as plan:
+        assert "fwht-columns[" in plan.algorithm_name()
     got = run_plan(torch_gpu, lib, t, x, stream)
     want = oracle.fwht_f32(x, inverse=inverse, normalize=inverse)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
