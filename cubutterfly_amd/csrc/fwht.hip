@@ -1145,15 +1145,18 @@ class FwhtExecutor final : public Executor {
 };
 
 // The lowerings of a request, default first. Default: the 32-register kernel
-// for FP16 rows of 2^12 points (55.7-56.6 us against 56.4-58.5 us for 16384
-// rows); the 16-register kernel elsewhere. The others are MEASURE candidates
-// and explicit choices.
+// for FP16 rows of 2^11 to 2^13 points and FP32 rows of 2^13 points (three
+// LDS phases where the 16-register kernel takes four at 2^13), the
+// 16-register kernel elsewhere. Measured, 2^24 elements per call, HIP events:
+// FP16 2^11 15.3 against 17.6 us, 2^12 14.0 / 17.4, 2^13 15.0 / 22.3; FP32
+// 2^13 24.2 / 34.1, but FP32 2^12 28.5 / 22.9 and 2^11 54.4 / 22.8. The
+// others are MEASURE candidates and explicit choices.
 std::vector<FwhtKind> fwht_kinds(const Request& r) {
     std::vector<FwhtKind> kinds = {FwhtKind::Resident};
     if (const WideLaunch wide = wide_launcher(r)) {
         kinds.push_back(FwhtKind::Wide);
         if (wide.walk) kinds.push_back(FwhtKind::WidePersistent);
-        if (r.log_n == 12 && r.fp16_final) std::swap(kinds[0], kinds[1]);
+        if (r.log_n >= 11 && r.log_n <= 13 && (r.fp16_final || r.log_n == 13)) std::swap(kinds[0], kinds[1]);
     }
     if (lane_launcher(r)) kinds.push_back(FwhtKind::Lanes);
     return kinds;

@@ -201,7 +201,9 @@ def test_long_fwht_is_factored(lib, log_n, extents):
     n = 1 << log_n
     t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=2)
     with cb.Plan(lib, t) as plan:
-        assert plan.algorithm_name().startswith("fwht-factored[fwht-fp32-resident-r16,fwht-fp32-columns-l")
+        # 2^13-point rows: the 32-register kernel.
+        row = "resident-r32" if extents[-1] == 8192 else "resident-r16"
+        assert plan.algorithm_name().startswith(f"fwht-factored[fwht-fp32-{row},fwht-fp32-columns-l")
         assert plan.physical_extents() == [n]
         assert plan.input_size() == plan.output_size() == 2 * n * 4
         assert plan.workspace_size() == 0

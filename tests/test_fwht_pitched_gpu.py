@@ -52,15 +52,17 @@ def run(torch, lib, stream, n, batch, in_pitch, out_pitch, fp16=False, inverse=F
 def test_fp32(torch_gpu, lib, stream, log_n, batch):
     n = 1 << log_n
     name = run(torch_gpu, lib, stream, n, batch, n + 12, n + 4, seed=log_n)
-    assert name == "fwht-fp32-resident-r16-pitched"
+    # 2^13-point FP32 rows default to the 32-register kernel.
+    assert name == ("fwht-fp32-resident-r32-pitched" if log_n == 13 else "fwht-fp32-resident-r16-pitched")
 
 
-@pytest.mark.parametrize("log_n", [4, 7, 12])
+@pytest.mark.parametrize("log_n", [4, 7, 11, 12, 13])
 def test_fp16_final(torch_gpu, lib, stream, log_n):
     n = 1 << log_n
     name = run(torch_gpu, lib, stream, n, 45, n + 24, n + 8, fp16=True, seed=log_n)
-    # 2^12-point FP16 rows default to the 32-register kernel.
-    assert name == ("fwht-fp16-fp32-resident-r32-pitched" if log_n == 12 else "fwht-fp16-fp32-resident-r16-pitched")
+    # FP16 rows of 2^11 to 2^13 points default to the 32-register kernel.
+    wide = 11 <= log_n <= 13
+    assert name == ("fwht-fp16-fp32-resident-r32-pitched" if wide else "fwht-fp16-fp32-resident-r16-pitched")
 
 
 def test_inverse_normalised(torch_gpu, lib, stream):
