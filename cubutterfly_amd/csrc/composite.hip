@@ -161,6 +161,17 @@ void launch_nd_boundary(bool gather, const void* src, void* dst, std::uint64_t c
     hip_check(hipGetLastError(), "composite gather / scatter launch");
 }
 
+// y = x * scale rounded to FP32, then to FP16 (round to nearest even). The
+// empty asm keeps the two roundings apart: without it the compiler fuses the
+// product and the narrowing into one v_fma_mixlo_f16, a single rounding of
+// the exact product, which differs from the contract for scales that are not
+// powers of two.
+__device__ __forceinline__ __half narrow_scaled(float x, float scale) {
+    float y = x * scale;
+    asm volatile("" : "+v"(y));
+    return __float2half_rn(y);
+}
+
 // FWHT stages over the row bits of G blocks of 2^LOG_L rows x 2^log_cols
 // columns (row pitch 2^log_cols elements): for each block and column, the
 // values x[i] of rows i = 0 .. 2^LOG_L - 1 go through the stages of bit 0,
@@ -169,7 +180,9 @@ void launch_nd_boundary(bool gather, const void* src, void* dst, std::uint64_t c
 // consecutive columns of all the rows in registers, so one load instruction
 // of a wave covers 64 * VEC consecutive elements of a row; no LDS and no
 // barriers. A lane writes exactly the elements it read, so src == dst is
-// allowed (no __restrict__).
+// allowed (no __restrict__). NARROW: the results leave as FP16,
+// narrow_scaled(x, out_scale), at the same element offsets of `dst` (the
+// FP32 promotion's final narrowing, fused into its last pass).
 constexpr std::uint32_t kMaxColumnBits = 7;  // rows * VEC <= 128 registers of data
 
 template <int VEC>
@@ -187,9 +200,25 @@ struct ColumnVector<4> {
     using type = float __attribute__((ext_vector_type(4)));
 };
 
-template <int LOG_L, int VEC>
-__global__ __launch_bounds__(kThreads) void fwht_columns_kernel(const float* src, float* dst, std::uint64_t vectors,
-                                                                std::uint32_t log_cols, float scale, int apply_scale) {
+template <int VEC>
+struct HalfVector;
+template <>
+struct HalfVector<1> {
+    using type = unsigned short;
+};
+template <>
+struct HalfVector<2> {
+    using type = unsigned short __attribute__((ext_vector_type(2)));
+};
+template <>
+struct HalfVector<4> {
+    using type = unsigned short __attribute__((ext_vector_type(4)));
+};
+
+template <int LOG_L, int VEC, bool NARROW>
+__global__ __launch_bounds__(kThreads) void fwht_columns_kernel(const float* src, void* dst, std::uint64_t vectors,
+                                                                std::uint32_t log_cols, float scale, int apply_scale,
+                                                                float out_scale) {
     constexpr int L = 1 << LOG_L;
     constexpr std::uint32_t kLogVec = VEC == 4 ? 2 : VEC == 2 ? 1 : 0;
     using V = typename ColumnVector<VEC>::type;
@@ -216,55 +245,92 @@ __global__ __launch_bounds__(kThreads) void fwht_columns_kernel(const float* src
 #pragma unroll
         for (int i = 0; i < L; ++i) x[i] = x[i] * scale;
     }
+    if constexpr (NARROW) {
+        using H = typename HalfVector<VEC>::type;
 #pragma unroll
-    for (int i = 0; i < L; ++i)
-        __builtin_nontemporal_store(x[i], reinterpret_cast<V*>(dst + base + (std::uint64_t(i) << log_cols)));
+        for (int i = 0; i < L; ++i) {
+            H h;
+            if constexpr (VEC == 1) {
+                h = __half_as_ushort(narrow_scaled(x[i], out_scale));
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) h[k] = __half_as_ushort(narrow_scaled(x[i][k], out_scale));
+            }
+            __builtin_nontemporal_store(
+                h, reinterpret_cast<H*>(static_cast<unsigned short*>(dst) + base + (std::uint64_t(i) << log_cols)));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < L; ++i)
+            __builtin_nontemporal_store(
+                x[i], reinterpret_cast<V*>(static_cast<float*>(dst) + base + (std::uint64_t(i) << log_cols)));
+    }
 }
 
-template <int LOG_L>
-void launch_fwht_columns_rows(const float* src, float* dst, std::uint64_t count, std::uint32_t log_cols, int vec,
-                              float scale, bool apply_scale, hipStream_t stream) {
+template <int LOG_L, bool NARROW>
+void launch_fwht_columns_rows(const float* src, void* dst, std::uint64_t count, std::uint32_t log_cols, int vec,
+                              float scale, bool apply_scale, float out_scale, hipStream_t stream) {
     const std::uint64_t vectors = count >> (LOG_L + (vec == 4 ? 2 : vec == 2 ? 1 : 0));
     const std::uint64_t blocks = (vectors + kThreads - 1) / kThreads;
     require(blocks < (std::uint64_t{1} << 31), "FWHT column pass grid too large");
     const dim3 grid{unsigned(blocks)}, block{kThreads};
     if constexpr (LOG_L <= 5) {
         if (vec == 4) {
-            hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 4>), grid, block, 0, stream, src, dst, vectors, log_cols,
-                               scale, int(apply_scale));
+            hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 4, NARROW>), grid, block, 0, stream, src, dst, vectors,
+                               log_cols, scale, int(apply_scale), out_scale);
             return;
         }
     }
     if constexpr (LOG_L <= 6) {
         if (vec == 2) {
-            hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 2>), grid, block, 0, stream, src, dst, vectors, log_cols,
-                               scale, int(apply_scale));
+            hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 2, NARROW>), grid, block, 0, stream, src, dst, vectors,
+                               log_cols, scale, int(apply_scale), out_scale);
             return;
         }
     }
-    hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 1>), grid, block, 0, stream, src, dst, vectors, log_cols, scale,
-                       int(apply_scale));
+    hipLaunchKernelGGL((fwht_columns_kernel<LOG_L, 1, NARROW>), grid, block, 0, stream, src, dst, vectors, log_cols,
+                       scale, int(apply_scale), out_scale);
+}
+
+template <bool NARROW>
+void launch_fwht_columns_of(const float* src, void* dst, std::uint64_t count, std::uint32_t log_rows,
+                            std::uint32_t log_cols, int vec, float scale, bool apply_scale, float out_scale,
+                            hipStream_t stream) {
+    switch (log_rows) {
+        case 1: launch_fwht_columns_rows<1, NARROW>(src, dst, count, log_cols, vec, scale, apply_scale, out_scale, stream); break;
+        case 2: launch_fwht_columns_rows<2, NARROW>(src, dst, count, log_cols, vec, scale, apply_scale, out_scale, stream); break;
+        case 3: launch_fwht_columns_rows<3, NARROW>(src, dst, count, log_cols, vec, scale, apply_scale, out_scale, stream); break;
+        case 4: launch_fwht_columns_rows<4, NARROW>(src, dst, count, log_cols, vec, scale, apply_scale, out_scale, stream); break;
+        case 5: launch_fwht_columns_rows<5, NARROW>(src, dst, count, log_cols, vec, scale, apply_scale, out_scale, stream); break;
+        case 6: launch_fwht_columns_rows<6, NARROW>(src, dst, count, log_cols, vec, scale, apply_scale, out_scale, stream); break;
+        default: launch_fwht_columns_rows<7, NARROW>(src, dst, count, log_cols, vec, scale, apply_scale, out_scale, stream); break;
+    }
 }
 
 // Column pass over `count` FP32 elements (G blocks of 2^log_rows x
-// 2^log_cols), src == dst allowed. The widest vector both pointers' alignment
-// and the register budget allow.
+// 2^log_cols), src == dst allowed; with `narrow_out`, the results go there as
+// FP16 (narrow_scaled(x, out_scale)) instead. The widest vector both
+// pointers' alignment and the register budget allow.
 void launch_fwht_columns(const float* src, float* dst, std::uint64_t count, std::uint32_t log_rows,
-                         std::uint32_t log_cols, float scale, bool apply_scale, hipStream_t stream) {
+                         std::uint32_t log_cols, float scale, bool apply_scale, hipStream_t stream,
+                         __half* narrow_out = nullptr, float out_scale = 1.0f) {
     require(log_rows >= 1 && log_rows <= kMaxColumnBits && log_cols >= 6, "FWHT column pass shape");
-    const auto align = reinterpret_cast<std::uintptr_t>(src) | reinterpret_cast<std::uintptr_t>(dst);
-    int vec = align % 16 == 0 ? 4 : align % 8 == 0 ? 2 : 1;
+    const auto s = reinterpret_cast<std::uintptr_t>(src);
+    int vec = s % 16 == 0 ? 4 : s % 8 == 0 ? 2 : 1;
+    if (narrow_out) {  // VEC halves per store
+        const auto d = reinterpret_cast<std::uintptr_t>(narrow_out);
+        vec = std::min(vec, d % 8 == 0 ? 4 : d % 4 == 0 ? 2 : 1);
+    } else {
+        const auto d = reinterpret_cast<std::uintptr_t>(dst);
+        vec = std::min(vec, d % 16 == 0 ? 4 : d % 8 == 0 ? 2 : 1);
+    }
     if (log_rows == 6) vec = std::min(vec, 2);
     if (log_rows == 7) vec = 1;
-    switch (log_rows) {
-        case 1: launch_fwht_columns_rows<1>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
-        case 2: launch_fwht_columns_rows<2>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
-        case 3: launch_fwht_columns_rows<3>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
-        case 4: launch_fwht_columns_rows<4>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
-        case 5: launch_fwht_columns_rows<5>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
-        case 6: launch_fwht_columns_rows<6>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
-        default: launch_fwht_columns_rows<7>(src, dst, count, log_cols, vec, scale, apply_scale, stream); break;
-    }
+    if (narrow_out)
+        launch_fwht_columns_of<true>(src, narrow_out, count, log_rows, log_cols, vec, scale, apply_scale, out_scale,
+                                     stream);
+    else
+        launch_fwht_columns_of<false>(src, dst, count, log_rows, log_cols, vec, scale, apply_scale, 1.0f, stream);
     hip_check(hipGetLastError(), "FWHT column pass launch");
 }
 
@@ -499,6 +565,18 @@ class CompositeExecutor final : public Executor {
     }
 
     void execute(const void* in, void* out, void* ws, hipStream_t stream) override {
+        run(in, out, ws, stream, nullptr, 1.0f);
+    }
+
+    // Whether run() can narrow to FP16 in the last step: an FWHT whose
+    // schedule ends with a column pass, on packed natural sides.
+    bool narrows() const { return fwht_columns_ && direct_in_ && direct_out_ && steps_.back().columns; }
+
+    // execute(); with `narrow`, the last column pass writes its results there
+    // as FP16, narrow_scaled(x, out_scale), instead of to `out` (which the
+    // earlier steps still use). Needs narrows().
+    void run(const void* in, void* out, void* ws, hipStream_t stream, __half* narrow, float out_scale) {
+        require(narrow == nullptr || narrows(), "FP16 narrowing needs a final FWHT column pass");
         const std::size_t bytes = align16(r_.data_bytes());
         const std::size_t ws_bytes = workspace_bytes();
         require(ws_bytes == 0 || ws != nullptr, "a composite plan needs its workspace");
@@ -522,8 +600,10 @@ class CompositeExecutor final : public Executor {
             const auto& s = steps_[i];
             if (s.columns) {
                 require(cur_writable != nullptr, "an FWHT column pass runs on a step's destination");
+                const bool narrow_here = narrow != nullptr && i + 1 == steps_.size();
                 launch_fwht_columns(static_cast<const float*>(cur_writable), static_cast<float*>(cur_writable),
-                                    count, s.log_rows, s.log_cols, s.scale, s.apply_scale, stream);
+                                    count, s.log_rows, s.log_cols, s.scale, s.apply_scale, stream,
+                                    narrow_here ? narrow : nullptr, out_scale);
                 continue;
             }
             void* dst = i == last && direct_out_ ? out : buffer[next];
@@ -630,7 +710,9 @@ class CompositeExecutor final : public Executor {
 // FP32 buffer, the factored FP32 transform in place on it (with the
 // inverse's 1/n), then y * scale rounded to FP32 and narrowed once to FP16
 // (round to nearest even) -- which is the stage-ordered FP32 transform
-// narrowed once, as the one-tile FP16 kernels compute it.
+// narrowed once, as the one-tile FP16 kernels compute it. The narrowing runs
+// in the factored plan's last column pass, which stores FP16 straight to the
+// output.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void widen_f16_kernel(const __half* __restrict__ src, float* __restrict__ dst,
                                                              std::uint64_t count) {
@@ -652,17 +734,6 @@ __global__ __launch_bounds__(kThreads) void widen_f16_kernel(const __half* __res
         for (std::uint64_t i = std::uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < count; i += step)
             dst[i] = __half2float(src[i]);
     }
-}
-
-// y = x * scale rounded to FP32, then to FP16 (round to nearest even). The
-// empty asm keeps the two roundings apart: without it the compiler fuses the
-// product and the narrowing into one v_fma_mixlo_f16, a single rounding of
-// the exact product, which differs from the contract for scales that are not
-// powers of two.
-__device__ __forceinline__ __half narrow_scaled(float x, float scale) {
-    float y = x * scale;
-    asm volatile("" : "+v"(y));
-    return __float2half_rn(y);
 }
 
 template <bool VEC>
@@ -702,10 +773,13 @@ class FwhtPromotedExecutor final : public Executor {
         c.variant.clear();
         factor_long_fwht(c);
         child_ = make_composite_executor(c, sel);
+        auto* composite = dynamic_cast<CompositeExecutor*>(child_.get());
+        fused_ = composite != nullptr && composite->narrows() ? composite : nullptr;
         f32_bytes_ = align16(c.data_bytes());
         algorithm = "fwht-fp16-promoted[" + child_->algorithm + "]";
         reason = "FP16 rows beyond one resident tile: widened to FP32, the factored FP32 transform, one final "
-                 "narrowing of y * scale; child: " + child_->reason;
+                 "narrowing of y * scale" + std::string(fused_ ? " (in the last column pass)" : "") +
+                 "; child: " + child_->reason;
         json::Writer w;
         w.begin_object()
             .field("schema_version", 1u)
@@ -715,6 +789,7 @@ class FwhtPromotedExecutor final : public Executor {
             .field("log_n", r.log_n)
             .field("batch", r.batch)
             .field("fp32_buffer_bytes", std::uint64_t(f32_bytes_))
+            .field("narrowing", fused_ ? "last-column-pass" : "separate-pass")
             .key("child")
             .value_raw(child_->mapping_json)
             .end_object();
@@ -738,6 +813,10 @@ class FwhtPromotedExecutor final : public Executor {
         else
             hipLaunchKernelGGL((widen_f16_kernel<false>), dim3(blocks), dim3(kThreads), 0, stream, src, buffer, count);
         hip_check(hipGetLastError(), "FP16 widening launch");
+        if (fused_) {
+            fused_->run(buffer, buffer, child_ws, stream, dst, r_.output_scale);
+            return;
+        }
         child_->execute(buffer, buffer, child_ws, stream);
         if (vec)
             hipLaunchKernelGGL((narrow_f16_kernel<true>), dim3(blocks), dim3(kThreads), 0, stream, buffer, dst, count,
@@ -751,6 +830,7 @@ class FwhtPromotedExecutor final : public Executor {
   private:
     Request r_;
     std::unique_ptr<Executor> child_;
+    CompositeExecutor* fused_ = nullptr;  // child_, when it narrows in its last pass
     std::size_t f32_bytes_ = 0;
 };
 

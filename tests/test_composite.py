@@ -239,6 +239,7 @@ def test_long_fp16_fwht_is_promoted(lib):
         assert plan.input_size() == plan.output_size() == batch * n * 2
         m = plan.mapping()
         assert m["kind"] == "fp32-promotion" and m["fp32_buffer_bytes"] == batch * n * 4
+        assert m["narrowing"] == "last-column-pass"
         assert m["child"]["extents"] == [4, 4096]
         assert plan.workspace_size() >= batch * n * 4
     # Strided or bit-reversed sides gather to packed rows first.
