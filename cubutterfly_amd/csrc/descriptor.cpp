@@ -421,16 +421,17 @@ Request lower_request(const cubutterflyDescriptor& d) {
         default:
             throw NotSupported("operator has no MI355X lowering");
     }
-    // FWHT beyond one resident tile (2^13 points). FP32 rows in natural order
-    // factor here, their strides carried by the factors; FP16 rows (the FP32
-    // promotion) and bit-reversed orders are planned as rank-1 requests, the
-    // orders and strides through the boundary, and factor when their packed
-    // FP32 transform is planned (factor_long_fwht). No kernel loads long rows
-    // at a pitch.
+    // FWHT beyond one resident tile (2^13 points). Packed FP32 rows in
+    // natural order factor here; FP16 rows (the FP32 promotion), strided
+    // sides and bit-reversed orders are planned as rank-1 requests, the
+    // orders and strides through the boundary (16-byte chunks for pitched
+    // rows, LDS tiles for bit reversals), and factor when their packed FP32
+    // transform is planned (factor_long_fwht). No kernel loads long rows at a
+    // pitch.
     if (r.op == Op::Fwht && d.rank == 1 && !embedding && r.log_n > 13) {
         r.pitched = false;
         r.boundary = strided || reversed;
-        if (!r.fp16_final && !reversed) factor_long_fwht(r);
+        if (!r.boundary && !r.fp16_final) factor_long_fwht(r);
     }
     return r;
 }

@@ -249,6 +249,16 @@ def test_long_fp16_fwht_is_promoted(lib):
         assert plan.algorithm_name().startswith("semantic-boundary[fwht-fp16-promoted[")
 
 
+def test_long_fwht_strided_sides_use_the_boundary(lib):
+    # Pitched or element-strided FP32 rows: the rank-1 boundary (16-byte
+    # chunks for pitched rows) around the packed factored plan.
+    n = 1 << 16
+    for kw in (dict(input_strides=[1], input_batch_stride=n + 64), dict(output_strides=[2], output_batch_stride=2 * n)):
+        t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=3, **kw)
+        with cb.Plan(lib, t) as plan:
+            assert plan.algorithm_name().startswith("semantic-boundary[fwht-factored[")
+
+
 def test_long_fwht_bit_reversed_orders_use_the_boundary(lib):
     # A whole-length bit reversal does not factor into per-axis reversals:
     # the boundary gathers to natural order, and the packed child factors.
