@@ -30,7 +30,7 @@
 // rank-N ones normalised per axis, run the innermost axis as one packed row
 // plan (at least 64 points) and every other axis, lowest bits first, as
 // in-place column passes of at most 2^7 rows held in registers: the same
-// stages in the same order, with no transposes. A rank-1 FWHT beyond 2^13
+// stages in the same order, with no transposes. A rank-1 FWHT beyond 2^14
 // points is factored into such axes and divides by n once, in its last pass.
 //
 // Strided sides and bit-reversed logical orders are handled as in the
@@ -705,7 +705,7 @@ class CompositeExecutor final : public Executor {
     std::size_t child_ws_ = 0;
 };
 
-// FP16 final-storage FWHT rows of more than 2^13 points: the reference's
+// FP16 final-storage FWHT rows of more than 2^14 points: the reference's
 // FP32 promotion (src/butterfly.cu:1452-1470) -- the input widened into an
 // FP32 buffer, the factored FP32 transform in place on it (with the
 // inverse's 1/n), then y * scale rounded to FP32 and narrowed once to FP16
@@ -841,7 +841,7 @@ std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* s
                 (r.rank >= 2 || r.embedding || r.factored),
             "composite plans need rank 2 to 8, the zero-extended embedding or a factored FWHT");
     // A flattened FWHT is one rank-1 plan; it exists up to the resident length.
-    const bool flatten = r.op == Op::Fwht && !(r.inverse && r.normalize) && r.log_n <= 13;
+    const bool flatten = r.op == Op::Fwht && !(r.inverse && r.normalize) && r.log_n <= kMaxFwhtRowLog;
     // A rank-2 FFT with both lowerings: MEASURE times the two, DEFAULT
     // replays a selection-cache record of that choice (keyed by the extents
     // too), the static rule decides otherwise.
@@ -882,7 +882,8 @@ std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* s
 }
 
 std::unique_ptr<Executor> make_long_fwht_executor(const Request& r, Selection* sel) {
-    require(r.op == Op::Fwht && r.rank == 1 && r.log_n > 13 && !r.boundary, "a packed rank-1 FWHT beyond 2^13 points");
+    require(r.op == Op::Fwht && r.rank == 1 && r.log_n > kMaxFwhtRowLog && !r.boundary,
+            "a packed rank-1 FWHT beyond one resident row");
     if (r.fp16_final) return std::make_unique<FwhtPromotedExecutor>(r, sel);
     Request f = r;
     factor_long_fwht(f);

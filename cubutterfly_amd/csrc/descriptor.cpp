@@ -248,14 +248,15 @@ void factor_long_fwht(Request& r) {
     require(r.op == Op::Fwht && r.rank == 1 && !r.factored && !r.embedding && !r.fp16_final &&
                 !r.input_bit_reversed && !r.output_bit_reversed,
             "only natural-order FP32 FWHT rows factor");
-    // Innermost: one resident row of 2^12 points, or 2^13 where that saves a
-    // pass; then axes of at most 2^7 points (one in-place column pass each),
-    // as even as their count allows. 2^14 .. 2^20 points take two passes,
-    // 2^21 .. 2^27 three.
+    // Innermost: one resident row of 2^12 points, or 2^13 / 2^14 where that
+    // saves a pass; then axes of at most 2^7 points (one in-place column pass
+    // each), as even as their count allows. 2^15 .. 2^21 points take two
+    // passes, 2^22 .. 2^28 three.
     constexpr std::uint32_t kColumnBits = 7;
-    const std::uint32_t outer = r.log_n - 13;
+    const std::uint32_t outer = r.log_n - kMaxFwhtRowLog;
     const std::uint32_t passes = (outer + kColumnBits - 1) / kColumnBits;
-    const std::uint32_t inner = r.log_n - 12 <= passes * kColumnBits ? 12u : 13u;
+    std::uint32_t inner = 12;
+    while (r.log_n - inner > passes * kColumnBits) ++inner;
     std::vector<std::uint32_t> bits{inner};  // innermost first
     for (std::uint32_t k = 0, done = 0; k < passes; ++k) {
         bits.push_back((r.log_n - inner - done) / (passes - k));
@@ -421,14 +422,14 @@ Request lower_request(const cubutterflyDescriptor& d) {
         default:
             throw NotSupported("operator has no MI355X lowering");
     }
-    // FWHT beyond one resident tile (2^13 points). Packed FP32 rows in
+    // FWHT beyond one resident row (2^14 points). Packed FP32 rows in
     // natural order factor here; FP16 rows (the FP32 promotion), strided
     // sides and bit-reversed orders are planned as rank-1 requests, the
     // orders and strides through the boundary (16-byte chunks for pitched
     // rows, LDS tiles for bit reversals), and factor when their packed FP32
     // transform is planned (factor_long_fwht). No kernel loads long rows at a
     // pitch.
-    if (r.op == Op::Fwht && d.rank == 1 && !embedding && r.log_n > 13) {
+    if (r.op == Op::Fwht && d.rank == 1 && !embedding && r.log_n > kMaxFwhtRowLog) {
         r.pitched = false;
         r.boundary = strided || reversed;
         if (!r.boundary && !r.fp16_final) factor_long_fwht(r);

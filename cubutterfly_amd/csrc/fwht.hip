@@ -444,18 +444,20 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_pitched_kernel(const typ
     }
 }
 
-// ---- 32 registers per thread, one row per tile (2^11 .. 2^13 points) -------
+// ---- 32 registers per thread, one row per tile (2^11 .. 2^14 points) -------
 //
 // Thread t holds 32 elements. Phase 0 butterflies element bits 0-4 (t's 32
 // consecutive elements), phase 1 bits 5-9, phase 2 bits 10 .. log n - 1. The
 // registers of phase 2 also carry element bits 0 .. P-1 (P = 15 - log n)
 // without butterflying them, so each thread ends with 2^(5-P) runs of 2^P
-// consecutive results and stores each run as one 8- to 64-byte vector: no
-// 2-byte scatter at the end, and still two LDS exchanges. Same stages in the
+// consecutive results and stores each run as one 4- to 64-byte vector: no
+// 2-byte scatter at the end, and still two LDS exchanges. A row of 2^14
+// points takes 512 threads and a 67.6 KB LDS image (gfx950 gives a
+// workgroup up to 160 KB). Same stages in the
 // same order as the 16-register kernel, so results are bit-identical.
 // LDS image: one pad word per 32 (addr = i + i/32), which leaves every
 // 32-lane group of all four exchange accesses on 32 distinct banks (checked
-// by enumeration for log n = 11, 12, 13), with per-thread bases and
+// by enumeration for log n = 11 .. 14), with per-thread bases and
 // compile-time register offsets.
 constexpr int kLW = 5;
 constexpr int kW = 1 << kLW;
@@ -533,7 +535,7 @@ __device__ __forceinline__ void wide_unpack_first_stage(const unsigned (&w)[wide
     }
 }
 
-// Stores `run` consecutive results (run * sizeof(T) bytes: 8, 16, 32 or 64)
+// Stores `run` consecutive results (run * sizeof(T) bytes: 4, 8, 16, 32 or 64)
 // at byte offset `off` of the tile's output buffer, nontemporal: a wave's
 // store instruction covers 512 bytes or more of consecutive output, written
 // once (C5a 49.1-49.7 -> 47.2-47.6 us).
@@ -551,7 +553,9 @@ __device__ __forceinline__ void wide_store_run(__amdgpu_buffer_rsrc_t r, unsigne
     }
     using V4 = __attribute__((ext_vector_type(4))) unsigned;
     using V2 = __attribute__((ext_vector_type(2))) unsigned;
-    if constexpr (kWords == 2) {
+    if constexpr (kWords == 1) {  // FP16 runs of 2 (2^14-point rows)
+        __builtin_amdgcn_raw_buffer_store_b32(w[0], r, static_cast<int>(off), 0, 2);
+    } else if constexpr (kWords == 2) {
         __builtin_amdgcn_raw_buffer_store_b64(V2{w[0], w[1]}, r, static_cast<int>(off), 0, 2);
     } else {
 #pragma unroll
@@ -576,7 +580,7 @@ __global__ __launch_bounds__(1 << (LOG_N - kLW), 4) void fwht_wide_kernel(const 
                                                                       std::uint64_t in_pitch,
                                                                       std::uint64_t out_pitch, float norm,
                                                                       float scale) {
-    static_assert(LOG_N >= 11 && LOG_N <= 13, "phase 2 covers 1 to 3 bits");
+    static_assert(LOG_N >= 11 && LOG_N <= 14, "phase 2 covers 1 to 4 bits");
     using T = typename Io::T;
     using M = WideMap<LOG_N>;
     constexpr unsigned kN = 1u << LOG_N;
@@ -988,7 +992,7 @@ WideLaunch wide_table_entry_f32(int log_n, std::integer_sequence<int, L...>) {
     return table[log_n - 11];
 }
 
-// The 32-register kernel: rows of 2^11 .. 2^13 points (FP16, and FP32 without
+// The 32-register kernel: rows of 2^11 .. 2^14 points (FP16, and FP32 without
 // the walking form), row count within 32 bits.
 // For FP16 rows of 2^7 and 2^8 points, the short-row form of the same
 // lowering (fwht_short_kernel: 4096-element tiles of whole rows, one LDS
@@ -999,8 +1003,8 @@ WideLaunch wide_table_entry_f32(int log_n, std::integer_sequence<int, L...>) {
 WideLaunch wide_launcher(const Request& r) {
     if (r.batch > 0xffffffffull) return {};
     if (!r.fp16_final) {
-        if (r.log_n < 11 || r.log_n > 13) return {};
-        return wide_table_entry_f32(int(r.log_n), std::make_integer_sequence<int, 3>{});
+        if (r.log_n < 11 || r.log_n > kMaxFwhtRowLog) return {};
+        return wide_table_entry_f32(int(r.log_n), std::make_integer_sequence<int, kMaxFwhtRowLog - 10>{});
     }
     if (r.log_n >= 7 && r.log_n <= 8) {
         const std::uint64_t rows_per_tile = std::uint64_t{1} << (12 - r.log_n);
@@ -1008,8 +1012,8 @@ WideLaunch wide_launcher(const Request& r) {
         if (rows_per_tile * pitch * 2 >= (std::uint64_t{1} << 31)) return {};
         return WideLaunch{r.log_n == 7 ? launch_short<7, F16Io> : launch_short<8, F16Io>, nullptr, nullptr};
     }
-    if (r.log_n < 11 || r.log_n > 13) return {};
-    return wide_table_entry(int(r.log_n), std::make_integer_sequence<int, 3>{});
+    if (r.log_n < 11 || r.log_n > kMaxFwhtRowLog) return {};
+    return wide_table_entry(int(r.log_n), std::make_integer_sequence<int, kMaxFwhtRowLog - 10>{});
 }
 
 template <class Io, int... L>
@@ -1152,11 +1156,13 @@ class FwhtExecutor final : public Executor {
 // 2^13 24.2 / 34.1, but FP32 2^12 28.5 / 22.9 and 2^11 54.4 / 22.8. The
 // others are MEASURE candidates and explicit choices.
 std::vector<FwhtKind> fwht_kinds(const Request& r) {
-    std::vector<FwhtKind> kinds = {FwhtKind::Resident};
+    std::vector<FwhtKind> kinds;
+    if (r.log_n <= kMaxResidentLog) kinds.push_back(FwhtKind::Resident);
     if (const WideLaunch wide = wide_launcher(r)) {
-        kinds.push_back(FwhtKind::Wide);
+        // Rows of 2^14 points have only the 32-register kernels.
+        const bool first = r.log_n > kMaxResidentLog || (r.log_n >= 11 && (r.fp16_final || r.log_n == 13));
+        kinds.insert(first ? kinds.begin() : kinds.end(), FwhtKind::Wide);
         if (wide.walk) kinds.push_back(FwhtKind::WidePersistent);
-        if (r.log_n >= 11 && r.log_n <= 13 && (r.fp16_final || r.log_n == 13)) std::swap(kinds[0], kinds[1]);
     }
     if (lane_launcher(r)) kinds.push_back(FwhtKind::Lanes);
     return kinds;
@@ -1165,8 +1171,8 @@ std::vector<FwhtKind> fwht_kinds(const Request& r) {
 }  // namespace
 
 std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
-    supported(r.log_n <= kMaxResidentLog,
-              "FWHT lengths above 2^" + std::to_string(kMaxResidentLog) + " are not yet lowered for gfx950");
+    supported(r.log_n <= kMaxResidentLog || wide_launcher(r),
+              "FWHT lengths above 2^" + std::to_string(kMaxFwhtRowLog) + " run as factored plans");
     supported(!r.allow_mma || r.fp16_final, "MFMA Hadamard blocks require FP16 storage");
     // ALLOW_FP16_MMA permits the MFMA Hadamard-block kernel but does not make
     // it the default: the stage-ordered VALU kernels are bit-exact and, on
@@ -1182,9 +1188,9 @@ std::unique_ptr<Executor> make_fwht_executor(const Request& r) {
         return make_fwht_mfma_executor(r);
     }
     const Launch launch = r.fp16_final ? resident_launcher<F16Io>(r.log_n) : resident_launcher<F32Io>(r.log_n);
-    require(launch != nullptr, "FWHT length has no launcher");
+    require(launch != nullptr || r.log_n > kMaxResidentLog, "FWHT length has no launcher");
     PitchedLaunch pitched = nullptr;
-    if (r.pitched) {
+    if (r.pitched && r.log_n <= kMaxResidentLog) {
         pitched = r.fp16_final ? pitched_launcher<F16Io>(r.log_n) : pitched_launcher<F32Io>(r.log_n);
         require(pitched != nullptr, "pitched FWHT rows need n >= 16");
     }

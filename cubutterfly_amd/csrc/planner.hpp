@@ -74,15 +74,15 @@ std::unique_ptr<Executor> make_boundary_executor(const Request& r, Selection* se
 // and the original order back; sides padded or cut to their own extents.
 std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel);
 
-// A packed rank-1 FWHT of more than 2^13 points: FP32 rows as the factored
+// A packed rank-1 FWHT of more than 2^14 points: FP32 rows as the factored
 // composite; FP16 final-storage rows through the FP32 promotion (widen, the
-// factored FP32 plan, one narrowing).
+// factored FP32 plan narrowing in its last pass).
 std::unique_ptr<Executor> make_long_fwht_executor(const Request& r, Selection* sel);
 
 inline std::unique_ptr<Executor> plan_executor(const Request& r, Selection* sel = nullptr) {
     if (r.rank > 1 || r.embedding || r.factored) return make_composite_executor(r, sel);
     if (r.boundary) return make_boundary_executor(r, sel);
-    if (r.op == Op::Fwht && r.log_n > 13) return make_long_fwht_executor(r, sel);
+    if (r.op == Op::Fwht && r.log_n > kMaxFwhtRowLog) return make_long_fwht_executor(r, sel);
     return select_leaf(r, sel);
 }
 

@@ -1,6 +1,7 @@
 """The 32-register FWHT lowering (`fwht-fp16-fp32-resident-r32` for FP16
-rows of 2^11..2^13 points, `fwht-fp32-resident-r32` for FP32 rows of the
-same lengths, without the walking form): bit-exact against the stage-ordered
+rows of 2^11..2^14 points, `fwht-fp32-resident-r32` for FP32 rows of the
+same lengths, without the walking form; the only lowering of 2^14-point
+rows, one row per 512-thread workgroup with a 67.6 KB LDS image): bit-exact against the stage-ordered
 oracle (src/butterfly_reference.cpp:349-369; FP16 final-storage contract
 tests/test_fwht_final_storage.py:28-40) on packed and pitched rows, in and
 out of place, forward and normalised inverse, selected explicitly and by
@@ -51,7 +52,7 @@ def bits(a):
 
 
 @pytest.mark.parametrize("fp16", [True, False])
-@pytest.mark.parametrize("log_n", [11, 12, 13])
+@pytest.mark.parametrize("log_n", [11, 12, 13, 14])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_packed(torch_gpu, lib, stream, fp16, log_n, inverse):
     batch = 300 + log_n
@@ -74,7 +75,7 @@ def test_in_place(torch_gpu, lib, stream, fp16):
 
 
 @pytest.mark.parametrize("fp16", [True, False])
-@pytest.mark.parametrize("log_n", [11, 13])
+@pytest.mark.parametrize("log_n", [11, 13, 14])
 def test_pitched(torch_gpu, lib, stream, fp16, log_n):
     n, batch = 1 << log_n, 41
     in_pitch, out_pitch = n + 64, n + 8
@@ -111,9 +112,9 @@ def test_measure_lists_both_lowerings(torch_gpu, lib, stream, tmp_path):
                     "fwht-fp16-fp32-resident-r32-persistent")
 
 
-@pytest.mark.parametrize("log_n,fp16", [(10, True), (14, True), (10, False), (14, False)])
+@pytest.mark.parametrize("log_n,fp16", [(10, True), (15, True), (10, False), (15, False)])
 def test_other_shapes_refuse_the_wide_lowering(lib, log_n, fp16):
-    # Only rows of 2^11..2^13 points, and FP16 rows of 2^7, 2^8 (the
+    # Only rows of 2^11..2^14 points, and FP16 rows of 2^7, 2^8 (the
     # short-row kernel).
     with pytest.raises(cb.AbiError) as e:
         cb.Plan(lib, transform(log_n, 8, fp16), **explicit(wide_name(fp16)))
