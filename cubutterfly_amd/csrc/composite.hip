@@ -30,7 +30,7 @@
 // rank-N ones normalised per axis, run the innermost axis as one packed row
 // plan (at least 64 points) and every other axis, lowest bits first, as
 // in-place column passes of at most 2^7 rows held in registers: the same
-// stages in the same order, with no transposes. A rank-1 FWHT beyond 2^14
+// stages in the same order, with no transposes. A rank-1 FWHT beyond 2^15
 // points is factored into such axes and divides by n once, in its last pass.
 //
 // Strided sides and bit-reversed logical orders are handled as in the
@@ -705,7 +705,7 @@ class CompositeExecutor final : public Executor {
     std::size_t child_ws_ = 0;
 };
 
-// FP16 final-storage FWHT rows of more than 2^14 points: the reference's
+// FP16 final-storage FWHT rows of more than 2^15 points: the reference's
 // FP32 promotion (src/butterfly.cu:1452-1470) -- the input widened into an
 // FP32 buffer, the factored FP32 transform in place on it (with the
 // inverse's 1/n), then y * scale rounded to FP32 and narrowed once to FP16

@@ -248,10 +248,10 @@ void factor_long_fwht(Request& r) {
     require(r.op == Op::Fwht && r.rank == 1 && !r.factored && !r.embedding && !r.fp16_final &&
                 !r.input_bit_reversed && !r.output_bit_reversed,
             "only natural-order FP32 FWHT rows factor");
-    // Innermost: one resident row of 2^12 points, or 2^13 / 2^14 where that
+    // Innermost: one resident row of 2^12 points, or up to 2^15 where that
     // saves a pass; then axes of at most 2^7 points (one in-place column pass
-    // each), as even as their count allows. 2^15 .. 2^21 points take two
-    // passes, 2^22 .. 2^28 three.
+    // each), as even as their count allows. 2^16 .. 2^22 points take two
+    // passes, 2^23 .. 2^29 three.
     constexpr std::uint32_t kColumnBits = 7;
     const std::uint32_t outer = r.log_n - kMaxFwhtRowLog;
     const std::uint32_t passes = (outer + kColumnBits - 1) / kColumnBits;
@@ -422,7 +422,7 @@ Request lower_request(const cubutterflyDescriptor& d) {
         default:
             throw NotSupported("operator has no MI355X lowering");
     }
-    // FWHT beyond one resident row (2^14 points). Packed FP32 rows in
+    // FWHT beyond one resident row (2^15 points). Packed FP32 rows in
     // natural order factor here; FP16 rows (the FP32 promotion), strided
     // sides and bit-reversed orders are planned as rank-1 requests, the
     // orders and strides through the boundary (16-byte chunks for pitched

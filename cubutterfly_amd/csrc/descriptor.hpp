@@ -52,7 +52,7 @@ enum class Op { Fwht, Fft, Ntt };
 constexpr std::uint32_t kMaxRank = 8;
 // Longest FWHT row one workgroup transforms in one pass (the 32-register
 // kernel); longer rows factor into a row pass and column passes.
-constexpr std::uint32_t kMaxFwhtRowLog = 14;
+constexpr std::uint32_t kMaxFwhtRowLog = 15;
 
 // A validated power-of-two request. Rank 1 is described by n, the strides
 // and the orders below; rank 2 and above additionally by the per-axis
@@ -123,8 +123,8 @@ struct Request {
 // rules for the fields this library accepts (src/semantic_contract.cpp:189-280).
 void validate_descriptor(const cubutterflyDescriptor& d);
 Request lower_request(const cubutterflyDescriptor& d);
-// A natural-order FP32 FWHT request of more than 2^14 points as its factors
-// (a resident row of 2^12 to 2^14 points, then axes of at most 2^7 points,
+// A natural-order FP32 FWHT request of more than 2^15 points as its factors
+// (a resident row of 2^12 to 2^15 points, then axes of at most 2^7 points,
 // lowest bits innermost).
 void factor_long_fwht(Request& r);
 

@@ -444,7 +444,7 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_pitched_kernel(const typ
     }
 }
 
-// ---- 32 registers per thread, one row per tile (2^11 .. 2^14 points) -------
+// ---- 32 registers per thread, one row per tile (2^11 .. 2^15 points) -------
 //
 // Thread t holds 32 elements. Phase 0 butterflies element bits 0-4 (t's 32
 // consecutive elements), phase 1 bits 5-9, phase 2 bits 10 .. log n - 1. The
@@ -452,12 +452,14 @@ __global__ __launch_bounds__(1 << (LB - kLE)) void fwht_pitched_kernel(const typ
 // without butterflying them, so each thread ends with 2^(5-P) runs of 2^P
 // consecutive results and stores each run as one 4- to 64-byte vector: no
 // 2-byte scatter at the end, and still two LDS exchanges. A row of 2^14
-// points takes 512 threads and a 67.6 KB LDS image (gfx950 gives a
-// workgroup up to 160 KB). Same stages in the
+// points takes 512 threads and a 67.6 KB LDS image, 2^15 points 1024
+// threads and 132 KB (gfx950 gives a workgroup up to 160 KB); at 2^15 the
+// phase-2 registers carry no low bits and each result leaves on its own
+// (consecutive across the lanes). Same stages in the
 // same order as the 16-register kernel, so results are bit-identical.
 // LDS image: one pad word per 32 (addr = i + i/32), which leaves every
 // 32-lane group of all four exchange accesses on 32 distinct banks (checked
-// by enumeration for log n = 11 .. 14), with per-thread bases and
+// by enumeration for log n = 11 .. 15), with per-thread bases and
 // compile-time register offsets.
 constexpr int kLW = 5;
 constexpr int kW = 1 << kLW;
@@ -535,33 +537,38 @@ __device__ __forceinline__ void wide_unpack_first_stage(const unsigned (&w)[wide
     }
 }
 
-// Stores `run` consecutive results (run * sizeof(T) bytes: 4, 8, 16, 32 or 64)
+// Stores `run` consecutive results (run * sizeof(T) bytes: 2, 4, 8, 16, 32 or 64)
 // at byte offset `off` of the tile's output buffer, nontemporal: a wave's
 // store instruction covers 512 bytes or more of consecutive output, written
 // once (C5a 49.1-49.7 -> 47.2-47.6 us).
 template <class Io, int RUN>
 __device__ __forceinline__ void wide_store_run(__amdgpu_buffer_rsrc_t r, unsigned off, const float* x) {
-    constexpr int kWords = RUN * int(sizeof(typename Io::T)) / 4;
-    unsigned w[kWords];
-#pragma unroll
-    for (int k = 0; k < kWords; ++k) {
-        if constexpr (sizeof(typename Io::T) == 4) {
-            w[k] = __float_as_uint(x[k]);
-        } else {
-            w[k] = pack_f16x2(x[2 * k], x[2 * k + 1]);
-        }
-    }
-    using V4 = __attribute__((ext_vector_type(4))) unsigned;
-    using V2 = __attribute__((ext_vector_type(2))) unsigned;
-    if constexpr (kWords == 1) {  // FP16 runs of 2 (2^14-point rows)
-        __builtin_amdgcn_raw_buffer_store_b32(w[0], r, static_cast<int>(off), 0, 2);
-    } else if constexpr (kWords == 2) {
-        __builtin_amdgcn_raw_buffer_store_b64(V2{w[0], w[1]}, r, static_cast<int>(off), 0, 2);
+    if constexpr (RUN * sizeof(typename Io::T) == 2) {  // one FP16 result (2^15-point rows)
+        __builtin_amdgcn_raw_buffer_store_b16(__half_as_ushort(__float2half_rn(x[0])), r, static_cast<int>(off), 0,
+                                              2);
     } else {
+        constexpr int kWords = RUN * int(sizeof(typename Io::T)) / 4;
+        unsigned w[kWords];
 #pragma unroll
-        for (int k = 0; k < kWords / 4; ++k)
-            __builtin_amdgcn_raw_buffer_store_b128(V4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]}, r,
-                                                   static_cast<int>(off + 16u * k), 0, 2);
+        for (int k = 0; k < kWords; ++k) {
+            if constexpr (sizeof(typename Io::T) == 4) {
+                w[k] = __float_as_uint(x[k]);
+            } else {
+                w[k] = pack_f16x2(x[2 * k], x[2 * k + 1]);
+            }
+        }
+        using V4 = __attribute__((ext_vector_type(4))) unsigned;
+        using V2 = __attribute__((ext_vector_type(2))) unsigned;
+        if constexpr (kWords == 1) {  // one FP32 result, or FP16 runs of 2 (2^14-point rows)
+            __builtin_amdgcn_raw_buffer_store_b32(w[0], r, static_cast<int>(off), 0, 2);
+        } else if constexpr (kWords == 2) {
+            __builtin_amdgcn_raw_buffer_store_b64(V2{w[0], w[1]}, r, static_cast<int>(off), 0, 2);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kWords / 4; ++k)
+                __builtin_amdgcn_raw_buffer_store_b128(V4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]}, r,
+                                                       static_cast<int>(off + 16u * k), 0, 2);
+        }
     }
 }
 
@@ -580,7 +587,7 @@ __global__ __launch_bounds__(1 << (LOG_N - kLW), 4) void fwht_wide_kernel(const 
                                                                       std::uint64_t in_pitch,
                                                                       std::uint64_t out_pitch, float norm,
                                                                       float scale) {
-    static_assert(LOG_N >= 11 && LOG_N <= 14, "phase 2 covers 1 to 4 bits");
+    static_assert(LOG_N >= 11 && LOG_N <= 15, "phase 2 covers 1 to 5 bits");
     using T = typename Io::T;
     using M = WideMap<LOG_N>;
     constexpr unsigned kN = 1u << LOG_N;
@@ -992,7 +999,7 @@ WideLaunch wide_table_entry_f32(int log_n, std::integer_sequence<int, L...>) {
     return table[log_n - 11];
 }
 
-// The 32-register kernel: rows of 2^11 .. 2^14 points (FP16, and FP32 without
+// The 32-register kernel: rows of 2^11 .. 2^15 points (FP16, and FP32 without
 // the walking form), row count within 32 bits.
 // For FP16 rows of 2^7 and 2^8 points, the short-row form of the same
 // lowering (fwht_short_kernel: 4096-element tiles of whole rows, one LDS
@@ -1159,7 +1166,7 @@ std::vector<FwhtKind> fwht_kinds(const Request& r) {
     std::vector<FwhtKind> kinds;
     if (r.log_n <= kMaxResidentLog) kinds.push_back(FwhtKind::Resident);
     if (const WideLaunch wide = wide_launcher(r)) {
-        // Rows of 2^14 points have only the 32-register kernels.
+        // Rows of 2^14 and 2^15 points have only the 32-register kernels.
         const bool first = r.log_n > kMaxResidentLog || (r.log_n >= 11 && (r.fp16_final || r.log_n == 13));
         kinds.insert(first ? kinds.begin() : kinds.end(), FwhtKind::Wide);
         if (wide.walk) kinds.push_back(FwhtKind::WidePersistent);

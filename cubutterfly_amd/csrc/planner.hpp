@@ -74,7 +74,7 @@ std::unique_ptr<Executor> make_boundary_executor(const Request& r, Selection* se
 // and the original order back; sides padded or cut to their own extents.
 std::unique_ptr<Executor> make_composite_executor(const Request& r, Selection* sel);
 
-// A packed rank-1 FWHT of more than 2^14 points: FP32 rows as the factored
+// A packed rank-1 FWHT of more than 2^15 points: FP32 rows as the factored
 // composite; FP16 final-storage rows through the FP32 promotion (widen, the
 // factored FP32 plan narrowing in its last pass).
 std::unique_ptr<Executor> make_long_fwht_executor(const Request& r, Selection* sel);

@@ -70,21 +70,21 @@ def test_rank3_schedule_restores_axis_order(lib):
 
 
 def test_large_rank2_fwht_uses_column_passes(lib):
-    # 2^15 points exceed one resident FWHT plan: the rows of axis 1, then axis
+    # 2^16 points exceed one resident FWHT plan: the rows of axis 1, then axis
     # 0 as one in-place column pass (no transposes, no workspace).
-    with cb.Plan(lib, fwht([128, 256])) as plan:
+    with cb.Plan(lib, fwht([128, 512])) as plan:
         assert plan.algorithm_name() == (
             "rank2-fwht-columns[fwht-fp32-resident-r16,fwht-fp32-columns-l7]+direct-input+direct-output")
         assert plan.workspace_size() == 0
         steps = schedule(plan)
         assert [s["step"] for s in steps] == ["axis", "columns"]
-        assert (steps[1]["axis"], steps[1]["rows"], steps[1]["cols"], steps[1]["blocks"]) == (0, 128, 256, 1)
+        assert (steps[1]["axis"], steps[1]["rows"], steps[1]["cols"], steps[1]["blocks"]) == (0, 128, 512, 1)
         assert steps[1]["scale"] == 1.0
 
 
-def test_rank2_fwht_of_2_14_points_flattens(lib):
-    # One 2^14-point row plan (the 32-register kernel) covers H(128) (x) H(128).
-    with cb.Plan(lib, fwht([128, 128])) as plan:
+def test_rank2_fwht_of_2_15_points_flattens(lib):
+    # One 2^15-point row plan (the 32-register kernel) covers H(128) (x) H(256).
+    with cb.Plan(lib, fwht([128, 256])) as plan:
         assert plan.algorithm_name() == "rank2-kronecker[fwht-fp32-resident-r32]+direct-input+direct-output"
 
 
@@ -197,17 +197,18 @@ def test_fwht_composition_is_the_flat_transform():
 
 
 @pytest.mark.parametrize("log_n,extents", [
-    (15, [8, 4096]), (19, [128, 4096]), (20, [128, 8192]), (21, [128, 16384]), (22, [32, 32, 4096]),
-    (26, [128, 128, 4096]), (27, [128, 128, 8192]), (28, [128, 128, 16384]), (29, [64, 64, 32, 4096]),
+    (16, [16, 4096]), (19, [128, 4096]), (20, [128, 8192]), (21, [128, 16384]), (22, [128, 32768]),
+    (23, [64, 32, 4096]), (26, [128, 128, 4096]), (27, [128, 128, 8192]), (28, [128, 128, 16384]),
+    (29, [128, 128, 32768]), (30, [64, 64, 64, 4096]),
 ])
 def test_long_fwht_is_factored(lib, log_n, extents):
-    # FWHT beyond 2^14 points: a resident row of 2^12 points (2^13 or 2^14
+    # FWHT beyond 2^15 points: a resident row of 2^12 points (up to 2^15
     # where that saves a pass), then axes of at most 2^7 points, lowest bits
     # innermost, each one in-place column pass.
     n = 1 << log_n
     t = cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [n], compute=cb.ComputeType.FP32, batch=2)
     with cb.Plan(lib, t) as plan:
-        # 2^13- and 2^14-point rows: the 32-register kernel.
+        # Rows of 2^13 points and more: the 32-register kernel.
         row = "resident-r32" if extents[-1] >= 8192 else "resident-r16"
         assert plan.algorithm_name().startswith(f"fwht-factored[fwht-fp32-{row},fwht-fp32-columns-l")
         assert plan.physical_extents() == [n]
@@ -234,10 +235,10 @@ def test_long_fwht_inverse_divides_once(lib):
 
 
 def test_long_fp16_fwht_is_promoted(lib):
-    # FP16 final-storage rows beyond 2^14 points: widened into an FP32 buffer
+    # FP16 final-storage rows beyond 2^15 points: widened into an FP32 buffer
     # of the workspace, the factored FP32 plan, one narrowing (the reference's
     # FP32 promotion, src/butterfly.cu:1452-1470).
-    n, batch = 1 << 15, 3
+    n, batch = 1 << 16, 3
     t = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [n], compute=cb.ComputeType.FP32, batch=batch,
                     output_scale=n ** -0.5, output_rounding=cb.OutputRounding.FINAL_STORAGE)
     with cb.Plan(lib, t) as plan:
@@ -246,7 +247,7 @@ def test_long_fp16_fwht_is_promoted(lib):
         m = plan.mapping()
         assert m["kind"] == "fp32-promotion" and m["fp32_buffer_bytes"] == batch * n * 4
         assert m["narrowing"] == "last-column-pass"
-        assert m["child"]["extents"] == [8, 4096]
+        assert m["child"]["extents"] == [16, 4096]
         assert plan.workspace_size() >= batch * n * 4
     # Strided or bit-reversed sides gather to packed rows first.
     strided = cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [n], compute=cb.ComputeType.FP32, batch=batch,

@@ -46,7 +46,8 @@ def ntt_t(extents, batch, word_bits, q, **kw):
     ((16, 64), False, "rank2-kronecker"),
     ((32, 64), True, "rank2-fwht-columns"),    # normalised inverse composes per axis
     ((64, 32), True, "rank2-transpose"),       # rows under 64 points: transposes
-    ((128, 256), False, "rank2-fwht-columns"), # 2^15 points: above one resident plan
+    ((128, 512), False, "rank2-fwht-columns"), # 2^16 points: above one resident plan
+    ((128, 256), False, "rank2-kronecker"),    # 2^15 points: one 2^15-point row plan
     ((4096, 64), True, "rank2-fwht-columns"),  # axis 0 as two column passes
     ((4, 8, 16), True, "rankN-composite"),
     ((8, 4, 64), True, "rankN-fwht-columns"),

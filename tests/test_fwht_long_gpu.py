@@ -1,5 +1,5 @@
-"""FWHT beyond one resident row (n > 2^14): factored into a resident row of
-2^12 or 2^13 points and axes of at most 2^7 points (in-place column passes),
+"""FWHT beyond one resident row (n > 2^15): factored into a resident row of
+2^12 to 2^15 points and axes of at most 2^7 points (in-place column passes),
 lowest index bits first, which is the reference's stage order
 (src/butterfly_reference.cpp:349-369), so results are bit-identical to the
 oracle; the inverse divides by n once, after the last stage. FP16 final-storage rows run as the reference's FP32 promotion
@@ -60,7 +60,7 @@ def f16_rows(batch, n, seed):
 
 # Scales that are not powers of two make the two roundings of y * scale (to
 # FP32, then to FP16) observable: a fused single rounding fails these.
-@pytest.mark.parametrize("log_n,batch,scale", [(15, 3, None), (16, 3, 0.37), (18, 2, 2.0 ** -7.5), (20, 2, None),
+@pytest.mark.parametrize("log_n,batch,scale", [(16, 2, None), (16, 3, 0.37), (18, 2, 2.0 ** -7.5), (20, 2, None),
                                                (17, 2, -0.75)])
 def test_fp16_promoted_bit_exact(torch_gpu, lib, stream, log_n, batch, scale):
     n = 1 << log_n
@@ -75,7 +75,7 @@ def test_fp16_promoted_bit_exact(torch_gpu, lib, stream, log_n, batch, scale):
 
 
 def test_fp16_promoted_inverse_normalised_in_place(torch_gpu, lib, stream):
-    n, batch = 1 << 15, 3
+    n, batch = 1 << 16, 3
     x = f16_rows(batch, n, 9)
     t = fwht16(n, batch, 1.0, inverse=True, normalize_inverse=True, placement=cb.Placement.IN_PLACE)
     got = run_plan(torch_gpu, lib, t, x, stream, in_place=True)
@@ -85,7 +85,7 @@ def test_fp16_promoted_inverse_normalised_in_place(torch_gpu, lib, stream):
 
 def test_fp16_promoted_unaligned_buffers(torch_gpu, lib, stream):
     # Buffers off a 16-byte boundary take the element-wise widening and narrowing.
-    n, batch, scale = 1 << 15, 2, float(np.float32(0.3))
+    n, batch, scale = 1 << 16, 2, float(np.float32(0.3))
     x = f16_rows(batch, n, 11)
     xd = to_device(torch_gpu, np.concatenate([np.zeros(1, np.float16), x.ravel()]))
     yd = to_device(torch_gpu, np.zeros(batch * n + 1, np.float16))
@@ -137,7 +137,7 @@ def test_bit_reversed_orders(torch_gpu, lib, stream, fp16, log_n, rev_in, rev_ou
 def test_fp16_strided_sides(torch_gpu, lib, stream):
     # Element stride 2 on the input, pitched output rows: gathered, promoted,
     # scattered; the output's padding keeps its sentinel.
-    n, batch, scale = 1 << 15, 3, float(np.float32((1 << 15) ** -0.5))
+    n, batch, scale = 1 << 16, 3, float(np.float32((1 << 16) ** -0.5))
     rows = f16_rows(batch, n, 21)
     in_bs, out_bs = 2 * n + 6, n + 24
     flat = np.zeros((batch - 1) * in_bs + 2 * (n - 1) + 1, np.float16)

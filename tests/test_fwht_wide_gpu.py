@@ -52,7 +52,7 @@ def bits(a):
 
 
 @pytest.mark.parametrize("fp16", [True, False])
-@pytest.mark.parametrize("log_n", [11, 12, 13, 14])
+@pytest.mark.parametrize("log_n", [11, 12, 13, 14, 15])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_packed(torch_gpu, lib, stream, fp16, log_n, inverse):
     batch = 300 + log_n
@@ -75,7 +75,7 @@ def test_in_place(torch_gpu, lib, stream, fp16):
 
 
 @pytest.mark.parametrize("fp16", [True, False])
-@pytest.mark.parametrize("log_n", [11, 13, 14])
+@pytest.mark.parametrize("log_n", [11, 13, 14, 15])
 def test_pitched(torch_gpu, lib, stream, fp16, log_n):
     n, batch = 1 << log_n, 41
     in_pitch, out_pitch = n + 64, n + 8
@@ -112,9 +112,9 @@ def test_measure_lists_both_lowerings(torch_gpu, lib, stream, tmp_path):
                     "fwht-fp16-fp32-resident-r32-persistent")
 
 
-@pytest.mark.parametrize("log_n,fp16", [(10, True), (15, True), (10, False), (15, False)])
+@pytest.mark.parametrize("log_n,fp16", [(10, True), (16, True), (10, False), (16, False)])
 def test_other_shapes_refuse_the_wide_lowering(lib, log_n, fp16):
-    # Only rows of 2^11..2^14 points, and FP16 rows of 2^7, 2^8 (the
+    # Only rows of 2^11..2^15 points, and FP16 rows of 2^7, 2^8 (the
     # short-row kernel).
     with pytest.raises(cb.AbiError) as e:
         cb.Plan(lib, transform(log_n, 8, fp16), **explicit(wide_name(fp16)))

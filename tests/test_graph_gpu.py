@@ -51,9 +51,9 @@ CASES = {
     "fwht-fp16-mfma": (fwht16(4096, 64, arithmetic_policy=cb.ArithmeticPolicy.ALLOW_FP16_MMA), np.float16, 1 << 18),
     "fwht-fp16-short": (fwht16(256, 16 * 40 + 3), np.float16, (16 * 40 + 3) * 256),
     "fwht-factored": (fwht(1 << 16, 3), np.float32, 3 << 16),
-    "fwht-fp16-promoted": (fwht16(1 << 15, 3), np.float16, 3 << 15),
-    "fwht-long-bit-reversed": (fwht(1 << 15, 2, input_orders=[cb.LogicalOrder.BIT_REVERSED],
-                                    output_orders=[cb.LogicalOrder.NATURAL]), np.float32, 2 << 15),
+    "fwht-fp16-promoted": (fwht16(1 << 16, 3), np.float16, 3 << 16),
+    "fwht-long-bit-reversed": (fwht(1 << 16, 2, input_orders=[cb.LogicalOrder.BIT_REVERSED],
+                                    output_orders=[cb.LogicalOrder.NATURAL]), np.float32, 2 << 16),
 }
 
 # Explicit lowerings of some cases (the others use the default).

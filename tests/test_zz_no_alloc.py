@@ -133,10 +133,10 @@ def test_composite_embedding_and_boundary_plans_after_a_larger_plan(torch_gpu, l
                                                                compute=cb.ComputeType.FP32, batch=8,
                                                                input_strides=[8], input_batch_stride=1),
          (8 * 4096,), np.float32),
-        ("fp16 fwht 2^15 x 3 (FP32 promotion)",
-         cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [1 << 15], compute=cb.ComputeType.FP32, batch=3,
-                     output_scale=float(np.float32((1 << 15) ** -0.5)),
-                     output_rounding=cb.OutputRounding.FINAL_STORAGE), (3 << 15,), np.float16),
+        ("fp16 fwht 2^16 x 3 (FP32 promotion)",
+         cb.describe(cb.Operator.FWHT, cb.DataType.FP16, [1 << 16], compute=cb.ComputeType.FP32, batch=3,
+                     output_scale=float(np.float32((1 << 16) ** -0.5)),
+                     output_rounding=cb.OutputRounding.FINAL_STORAGE), (3 << 16,), np.float16),
         ("fwht 2^16 x 2, bit-reversed input (boundary, factored)",
          cb.describe(cb.Operator.FWHT, cb.DataType.FP32, [1 << 16], compute=cb.ComputeType.FP32, batch=2,
                      input_orders=[cb.LogicalOrder.BIT_REVERSED], output_orders=[cb.LogicalOrder.NATURAL]),
