@@ -445,7 +445,18 @@ class DeviceCopy(Workload):
         return "torch copy_"
 
 
-WORKLOADS = {"c1": FwhtFp32, "c1p": FwhtFp32Pitched, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1),
+class FwhtFp32Long(FwhtFp32):
+    """C1's 64 MiB as rows of 2^16 points (not a BASELINE line): the factored
+    plan, a resident row pass and one in-place column pass."""
+    name = "c1l"
+
+    def __init__(self, log_n=16, batch=256):
+        super().__init__(log_n, batch)
+        self.description = (f"FWHT fp32 unnormalized forward, batch {batch} x n={1 << log_n} (factored: a resident "
+                            "row pass and an in-place column pass), integer inputs in [-8,8]")
+
+
+WORKLOADS = {"c1": FwhtFp32, "c1p": FwhtFp32Pitched, "c1l": FwhtFp32Long, "c2": NttNegacyclic, "c3a": lambda: FftC64(24, 1),
              "c3b": lambda: FftC64(14, 1024), "c4": RnsNegacyclic, "c5a": lambda: FwhtFp16(16384, 4096),
              "c5b": lambda: FwhtFp16(524288, 128), "c5a_mma": lambda: FwhtFp16(16384, 4096, mma=True),
              "c5b_mma": lambda: FwhtFp16(524288, 128, mma=True), "r2": FftC64Rank2, "copy": DeviceCopy}
